@@ -1,0 +1,61 @@
+"""Input generators and dense references shared by the tests.
+
+The generators restate the reference tests' fixtures: the LCG ``fill`` (tests/attention.rs:3-11),
+the closed-form ``document`` (tests/prefix.rs:7-18) and ``slice_tokens`` (tests/cache.rs:17-34).
+Dense references follow tests/attention.rs:13-38 and tests/prefix.rs:20-68 (f32, as the Rust
+tests compute them) and add an f64 brute force for stricter checks.
+"""
+
+import numpy as np
+
+import kivi
+
+fill = kivi.lcg_fill
+
+
+def document(batch, heads, seq, dim):
+    """tests/prefix.rs:7-18."""
+    n = batch * heads * seq * dim
+    i = np.arange(n, dtype=np.int64)
+    keys = (((i * 17) % 23).astype(np.float32) / np.float32(11.0)) - np.float32(0.4)
+    values = (((i * 13) % 19).astype(np.float32) / np.float32(9.0)) - np.float32(0.2)
+    return keys.astype(np.float32), values.astype(np.float32)
+
+
+def slice_tokens(full, batch, heads, total, dim, offset, count):
+    """tests/cache.rs:17-34: tokens [offset, offset+count) of a [B,H,total,D] tensor."""
+    a = np.asarray(full, dtype=np.float32).reshape(batch, heads, total, dim)
+    return np.ascontiguousarray(a[:, :, offset:offset + count, :]).reshape(-1)
+
+
+def concat_head_major(prefix, extra, batch, heads, prefix_len, extra_len, dim):
+    """tests/prefix.rs:70-95."""
+    a = np.asarray(prefix, np.float32).reshape(batch, heads, prefix_len, dim)
+    b = np.asarray(extra, np.float32).reshape(batch, heads, extra_len, dim)
+    return np.concatenate([a, b], axis=2).reshape(-1)
+
+
+def dense_attend(keys, values, query, batch, kv_heads, q_heads, seq, dim, scale,
+                 dtype=np.float64):
+    """Dense softmax attention over [B,KV,seq,D] K/V for [B,QH,D] queries (GQA qh/(QH/KV)),
+    computed in ``dtype`` (tests/prefix.rs:20-68 computes the same in f32)."""
+    k = np.asarray(keys, dtype).reshape(batch, kv_heads, seq, dim)
+    v = np.asarray(values, dtype).reshape(batch, kv_heads, seq, dim)
+    q = np.asarray(query, dtype).reshape(batch, q_heads, dim)
+    group = q_heads // kv_heads
+    out = np.zeros((batch, q_heads, dim), dtype)
+    for b in range(batch):
+        for qh in range(q_heads):
+            kvh = qh // group
+            logits = (k[b, kvh] @ q[b, qh]) * dtype(scale)
+            logits = logits - logits.max()
+            w = np.exp(logits)
+            w = w / w.sum()
+            out[b, qh] = w @ v[b, kvh]
+    return out.reshape(-1)
+
+
+def max_abs(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.max(np.abs(a - b))) if a.size else 0.0
