@@ -1,0 +1,220 @@
+#!/usr/bin/env python3
+"""Decode-attention benchmark of the MI355X KIVI path (one JSON line on stdout).
+
+Workload (the north-star target): batch 16, 32 query / 8 KV heads,
+head_dim 128, 32768 cached tokens per sequence, 2-bit G=32 R=128, K ~ N(0,1) with 1% of key
+channels (2 per KV head) scaled x10, V ~ N(0,1), fp32 inputs. A step is one decode attention
+over all 16 sequences (the cache and the queries already resident in HBM); value = decode
+tokens/s = 16 * steps / time. The cache build (prefill quantization) is timed once and
+reported as quantize GB/s. The CPU baseline is the oracle (C++ restatement of the
+reference CPU path, 1 core) on one of the 16 sequences.
+
+Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--config c2] [--no-cpu]
+"""
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+PKG = ROOT / "kivi-cache-rs_amd"
+sys.path.insert(0, str(PKG))
+
+METRIC = "decode-attn tokens/s + effective HBM GB/s (% of 8 TB/s); quantize GB/s"
+HBM_PEAK_GBPS = 8000.0
+
+CONFIGS = {
+    # name: (batch, kv_heads, q_heads, head_dim, seq, bits, G, R, description)
+    "c0": (1, 8, 8, 128, 4097, 2, 32, 128, "config 0: batch 1, 8q/8kv heads, seq 4097 (4096 prefill + 1), 2-bit"),
+    "c2": (16, 8, 32, 128, 32768, 2, 32, 128,
+           "config 2: batch 16, 32q/8kv heads, head_dim 128, 32768 cached tokens, 2-bit G=32 R=128"),
+    "c3_4": (1, 8, 64, 128, 131072, 4, 32, 128, "config 3: batch 1, 64q/8kv heads, 131072 tokens, 4-bit"),
+    "c3_8": (1, 8, 64, 128, 131072, 8, 32, 128, "config 3: batch 1, 64q/8kv heads, 131072 tokens, 8-bit"),
+}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def outlier_channels(heads, dim, seed):
+    """1% of channels per KV head (ceil(0.01*D)), fixed by the seed."""
+    rng = np.random.default_rng(seed)
+    k = max(1, math.ceil(0.01 * dim))
+    return [sorted(rng.choice(dim, size=k, replace=False).tolist()) for _ in range(heads)]
+
+
+def gpu_inputs(torch, batch, heads, qh, dim, seq, seed):
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    k = torch.randn((batch, heads, seq, dim), generator=g, device="cuda", dtype=torch.float32)
+    for h, chans in enumerate(outlier_channels(heads, dim, seed)):
+        k[:, h, :, chans] *= 10.0
+    v = torch.randn((batch, heads, seq, dim), generator=g, device="cuda", dtype=torch.float32)
+    q = torch.randn((batch, qh, dim), generator=g, device="cuda", dtype=torch.float32)
+    return k, v, q
+
+
+def cpu_baseline(kivi, cfg_tuple, target_s=12.0):
+    """Oracle (CPU restatement of the reference, one thread) on one sequence of the workload."""
+    _, heads, qh, dim, seq, bits, G, R, _ = cfg_tuple
+    oracle = kivi.Backend.load(ROOT / "oracle" / "libkivi_oracle.so", "kivi_oracle_", device=False)
+    rng = np.random.default_rng(7)
+    k = rng.standard_normal((1, heads, seq, dim), dtype=np.float32)
+    for h, chans in enumerate(outlier_channels(heads, dim, 7)):
+        k[:, h, :, chans] *= 10.0
+    v = rng.standard_normal((1, heads, seq, dim), dtype=np.float32)
+    q = rng.standard_normal((1, qh, dim), dtype=np.float32)
+    cache = kivi.KiviCache(oracle, kivi.KiviConfig(bits, G, R), 1, heads, dim)
+    t0 = time.perf_counter()
+    cache.append(k, v, seq)
+    t_quant = time.perf_counter() - t0
+    quant_bytes = 2 * k.nbytes + cache.memory().compressed_bytes()
+    del k, v
+    scale = 1.0 / math.sqrt(dim)
+    reps, spent = 0, 0.0
+    while spent < target_s and reps < 5:
+        t0 = time.perf_counter()
+        cache.attention(q, qh, scale)
+        spent += time.perf_counter() - t0
+        reps += 1
+    per_step = spent / reps
+    return {
+        "value": 1.0 / per_step,
+        "unit": "tokens/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"1 of the workload's sequences ({heads} KV / {qh} q heads, {seq} tokens): "
+                  f"{reps} decode attention step(s) of the C++ restatement of the reference "
+                  f"CPU path, single thread; prefill quantize {quant_bytes / t_quant / 1e9:.3f} GB/s",
+        "quantize_gbps": quant_bytes / t_quant / 1e9,
+        "ms_per_step": per_step * 1e3,
+        "cpu": _cpu_model(),
+    }
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus "
+              f"{args.gpus}); the (batch, kv_head) units shard with no communication, see DESIGN.md",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import kivi
+
+    amd = kivi.Backend.amd()
+    assert amd["device_count"]() >= 1, "no HIP device"
+    batch, heads, qh, dim, seq, bits, G, R, desc = CONFIGS[args.config]
+    torch.cuda.set_device(0)
+    stream = torch.cuda.Stream()
+    sp = stream.cuda_stream
+
+    log(f"[bench] building inputs {desc}")
+    k, v, q = gpu_inputs(torch, batch, heads, qh, dim, seq, 2001)
+    out = torch.empty((batch, qh, dim), device="cuda", dtype=torch.float32)
+    cache = kivi.KiviCache(amd, kivi.KiviConfig(bits, G, R), batch, heads, dim)
+    cache.reserve(seq)
+    torch.cuda.synchronize()
+    # Prefill quantization, timed once on the library's stream.
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        e0.record(stream)
+        cache.append_device(k.data_ptr(), k.numel(), v.data_ptr(), v.numel(), seq, sp)
+        e1.record(stream)
+    stream.synchronize()
+    t_quant = e0.elapsed_time(e1) / 1e3
+    mem = cache.memory()
+    quant_bytes = 2 * k.numel() * 4 + mem.compressed_bytes()
+    log(f"[bench] prefill quantize {quant_bytes / t_quant / 1e9:.1f} GB/s ({t_quant * 1e3:.2f} ms)")
+    del k, v
+    torch.cuda.empty_cache()
+
+    scale = 1.0 / math.sqrt(dim)
+    qp, op, n_q = q.data_ptr(), out.data_ptr(), q.numel()
+
+    def step():
+        cache.attention_device(qp, n_q, qh, scale, op, n_q, sp)
+
+    with torch.cuda.stream(stream):
+        for _ in range(args.warmup):
+            step()
+    stream.synchronize()
+    torch.cuda.synchronize()
+    t_start = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        t_start.record(stream)
+        for _ in range(args.steps):
+            step()
+        t_end.record(stream)
+    stream.synchronize()
+    torch.cuda.synchronize()
+    per_step = t_start.elapsed_time(t_end) / 1e3 / args.steps
+    algo_bytes = mem.compressed_bytes() + 2 * out.numel() * 4  # KV bytes + query + output
+    eff_gbps = algo_bytes / per_step / 1e9
+    tokens_per_s = batch / per_step
+    log(f"[bench] attention {per_step * 1e6:.1f} us/step, {eff_gbps:.0f} GB/s effective")
+
+    result = {
+        "metric": METRIC,
+        "value": tokens_per_s,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": per_step * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": desc, "batch": batch, "kv_heads": heads, "q_heads": qh,
+                   "head_dim": dim, "cached_tokens": seq, "bits": bits, "group_size": G,
+                   "residual_length": R},
+        "effective_hbm_gbps": eff_gbps,
+        "hbm_fraction": eff_gbps / HBM_PEAK_GBPS,
+        "quantize_gbps": quant_bytes / t_quant / 1e9,
+        "roofline": {
+            "bound": "hbm",
+            "achieved": eff_gbps,
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": eff_gbps / HBM_PEAK_GBPS,
+            "traffic": None,
+            "algorithmic_bytes": algo_bytes,
+            "kernel": "attention step (split kernel + merge), HIP events on the launch stream",
+        },
+    }
+    if not args.no_cpu:
+        log("[bench] CPU baseline (oracle, 1 thread) ...")
+        result["cpu_baseline"] = cpu_baseline(kivi, CONFIGS[args.config])
+        log(f"[bench] CPU {result['cpu_baseline']['value']:.3f} tokens/s")
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

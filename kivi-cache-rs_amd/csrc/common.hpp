@@ -1,0 +1,178 @@
+// common.hpp — device layout of the KIVI cache in HBM and the launch interface shared by
+// the HIP kernels (kernels_*.hip) and the host state machine (cache.cpp).
+//
+// Per (batch, kv_head) "unit" the cache holds four packed arrays, each with a fixed
+// per-unit capacity of `cap` tokens (cap is a multiple of lcm(64, G)):
+//
+//   key codes    u32 [cap][D/ppw]           token-major: word (t, j) holds channels
+//                                           j*ppw .. j*ppw+ppw-1 of token t, channel
+//                                           j*ppw+i at bits [b*i, b*i+b)
+//   key params   f32 [cap/G][D][2]          (scale, zero) per (group, channel) — the
+//                                           reference PackedStream order (src/quant.rs:307-311)
+//   value codes  u32 [cap/64][D][64/ppw]    channel-major in 64-token blocks: word (blk, d, w)
+//                                           holds tokens blk*64 + w*ppw + i of channel d
+//   value params f32 [cap/64][D/G][64][2]   (scale, zero) per (token, channel group)
+//
+// with ppw = 32/bits codes per word. Keys are packed along channels and values along
+// tokens — the axis each is reduced over in attention — so a lane that owns a token
+// (keys) or a channel (values) unpacks whole words of its own codes. The reference packs
+// the other way (keys along tokens, values along channels, src/quant.rs:312-323, 362-372);
+// the quantized codes and (scale, zero) values are identical, and
+// kivi_cache_export_streams re-packs into the reference order bit for bit.
+//
+// fp32 state per unit: key residual [R][D] (linear, token kq+i in slot i) and the value
+// window [R][D] as a ring (token vq+i in slot (vhead+i) % R), so a decode step evicts one
+// token without the reference's O(R*D) memmove (src/cache.rs:559-578).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace kivi {
+
+constexpr uint32_t kValueBlock = 64;  // tokens per value code block
+
+struct Geometry {
+  uint32_t bits;  // 2, 4, 8
+  uint32_t G;     // group size
+  uint32_t R;     // residual length
+  uint32_t D;     // head dim
+  uint32_t units; // batch * kv_heads
+  uint64_t cap;   // token capacity per unit
+
+  __host__ __device__ uint32_t ppw() const { return 32u / bits; }
+  __host__ __device__ uint32_t kwords_per_token() const { return D / ppw(); }
+  __host__ __device__ uint32_t vwords_per_channel() const { return kValueBlock / ppw(); }
+  __host__ __device__ uint32_t ncg() const { return D / G; }
+  __host__ __device__ uint32_t levels() const { return (1u << bits) - 1u; }
+  // per-unit element counts
+  __host__ __device__ uint64_t kcodes_unit() const { return cap * kwords_per_token(); }
+  __host__ __device__ uint64_t kparams_unit() const { return (cap / G) * D * 2; }
+  __host__ __device__ uint64_t vcodes_unit() const { return (cap / kValueBlock) * D * vwords_per_channel(); }
+  __host__ __device__ uint64_t vparams_unit() const { return cap * ncg() * 2; }
+  __host__ __device__ uint64_t residual_unit() const { return (uint64_t)R * D; }
+};
+
+// Device pointers of one cache (or a frozen prefix copy).
+struct CacheView {
+  Geometry geo;
+  uint32_t* kcodes;
+  float* kparams;
+  uint32_t* vcodes;
+  float* vparams;
+  float* kres;   // [units][R][D]
+  float* vring;  // [units][R][D]
+};
+
+// Sequence state of a cache at one instant.
+struct SeqState {
+  uint64_t kq;       // packed key tokens
+  uint64_t vq;       // packed value tokens
+  uint32_t kres;     // key residual length
+  uint32_t vres;     // value window length
+  uint32_t vhead;    // ring slot of token vq
+};
+
+// Where the fp32 rows of a token range come from: [units][seq][D] starting at `offset`
+// (stride_unit = seq*D), or the value ring when ring != 0.
+struct RowSource {
+  const float* base;
+  uint64_t stride_unit;  // floats between units
+  uint64_t offset;       // first token
+  uint32_t ring;         // 1: slot = (offset + i) % R
+};
+
+// ---------------------------------------------------------------- launches (kernels_quant.hip)
+// All return hipSuccess or the launch error; all enqueue on `stream`.
+
+// Copy `count` rows of each unit from src into dst[unit][R][D] slots (dst_slot + i) % R.
+hipError_t launch_copy_rows(const Geometry& g, RowSource src, float* dst, uint32_t dst_slot,
+                            uint32_t count, hipStream_t stream);
+
+// Quantize `ngroups` key groups per unit from src rows into the native key arrays,
+// writing groups g0 .. g0+ngroups-1 (src/quant.rs:275-328 per group).
+hipError_t launch_quant_keys(const CacheView& c, RowSource src, uint64_t g0, uint32_t ngroups,
+                             hipStream_t stream);
+
+// Quantize `n_ring` ring tokens then `n_in` input tokens per unit as stream tokens
+// vq0 .. vq0+n-1 (src/quant.rs:330-377 per token).
+hipError_t launch_quant_values(const CacheView& c, RowSource ring, uint32_t n_ring, RowSource in,
+                               uint64_t n_in, uint64_t vq0, hipStream_t stream);
+
+// Re-pack native streams into the reference PackedStream order, [units][...] concatenated.
+hipError_t launch_export_keys(const CacheView& c, uint64_t kq, uint32_t* codes, float* params,
+                              hipStream_t stream);
+hipError_t launch_export_values(const CacheView& c, uint64_t vq, uint32_t* codes, float* params,
+                                hipStream_t stream);
+
+// Dense [units][seq][D] reconstruction (src/cache.rs:282-325).
+hipError_t launch_dequant_cache(const CacheView& c, const SeqState& s, float* keys, float* values,
+                                hipStream_t stream);
+
+// Copy `units` blocks of `bytes` from src (pitch src_pitch) to dst (pitch dst_pitch).
+hipError_t copy_units(void* dst, size_t dst_pitch, const void* src, size_t src_pitch, size_t bytes,
+                      uint32_t units, hipStream_t stream);
+
+// ---------------------------------------------------------------- standalone codec
+// Reference-order streams for quantize_per_channel / quantize_per_token
+// (src/quant.rs:153-233): codes/params concatenated over units.
+hipError_t launch_quant_ref_keys(const float* data, uint32_t units, uint64_t tokens, uint32_t D,
+                                 uint32_t bits, uint32_t G, uint32_t* codes, float* params,
+                                 hipStream_t stream);
+hipError_t launch_quant_ref_values(const float* data, uint32_t units, uint64_t tokens, uint32_t D,
+                                   uint32_t bits, uint32_t G, uint32_t* codes, float* params,
+                                   hipStream_t stream);
+// QuantizedTensor::dequantize and ::pytorch_codes (src/quant.rs:77-150).
+hipError_t launch_dequant_ref(const uint32_t* codes, const float* params, uint32_t units,
+                              uint64_t tokens, uint32_t D, uint32_t bits, uint32_t G,
+                              int per_channel, float* out, hipStream_t stream);
+hipError_t launch_pytorch_order(const uint32_t* codes, uint32_t units, uint64_t tokens, uint32_t D,
+                                uint32_t bits, uint32_t G, int per_channel, uint32_t* out,
+                                hipStream_t stream);
+
+// ---------------------------------------------------------------- attention (kernels_attn.hip)
+
+// One decode-attention problem over a cache view plus an optional fp32 suffix per unit.
+struct AttnProblem {
+  CacheView cache;
+  SeqState st;
+  uint64_t seq;              // kq + kres  (= vq + vres)
+  const float* suffix_k;     // [units][*][D] or null
+  const float* suffix_v;
+  uint64_t suffix_len;       // L
+  uint64_t suffix_stride;    // floats between units of suffix_k / suffix_v
+  const float* query;        // [batch][QH][D]
+  float* out;                // [batch][QH][D]
+  uint32_t qh;               // query heads
+  uint32_t heads;            // kv heads
+  uint32_t batch;
+  float scale;
+};
+
+// Workspace floats the attention needs for `p` (split-K partials).
+size_t attention_workspace_floats(const AttnProblem& p);
+hipError_t launch_attention(const AttnProblem& p, float* workspace, hipStream_t stream);
+
+// n sessions sharing one prefix: the prefix part of every session is computed in one pass
+// over the prefix; suffixes[i] (device, [units][L_i][D]) are per session.
+struct SessionsProblem {
+  CacheView cache;
+  SeqState st;
+  uint64_t seq;
+  uint32_t n;
+  const float* const* suffix_k;  // device array of n pointers
+  const float* const* suffix_v;
+  const uint64_t* suffix_len;    // device array of n lengths
+  uint64_t max_suffix;
+  const float* queries;  // [n][batch][QH][D]
+  float* out;            // [n][batch][QH][D]
+  uint32_t qh, heads, batch;
+  float scale;
+};
+size_t sessions_workspace_floats(const SessionsProblem& p);
+hipError_t launch_sessions_attention(const SessionsProblem& p, float* workspace,
+                                     hipStream_t stream);
+
+}  // namespace kivi

@@ -1,0 +1,1346 @@
+// host.cpp — host state machine of the MI355X KIVI cache and the C ABI (include/kivi.h).
+//
+// Mirrors the reference's KiviCache / SharedPrefix / RagSession / RuntimeKv /
+// QuantizedTensor (src/cache.rs, src/prefix.rs, src/runtime.rs, src/quant.rs) over device
+// arenas: the packed streams, the key residual and the value window live in HBM and every
+// transformation of KV data runs in the HIP kernels of kernels_*.hip. The host keeps only
+// the counters (seq, kq, vq, residual lengths, ring head) and validates arguments in the
+// reference's order. There is no CPU fallback: without a HIP device, entry points that
+// touch data return KIVI_ERR_DEVICE.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <memory>
+#include <mutex>
+#include <new>
+#include <numeric>
+#include <string>
+#include <vector>
+
+#include "../../include/kivi.h"
+#include "common.hpp"
+
+namespace kivi {
+namespace {
+
+// ---------------------------------------------------------------- status
+
+struct Status {
+  int code = KIVI_OK;
+  uint64_t a = 0, b = 0;
+  const char* name = nullptr;
+  std::string detail;  // device errors
+  bool ok() const { return code == KIVI_OK; }
+};
+
+Status Err(int code, uint64_t a = 0, uint64_t b = 0, const char* name = nullptr) {
+  Status s;
+  s.code = code;
+  s.a = a;
+  s.b = b;
+  s.name = name;
+  return s;
+}
+
+Status DevErr(hipError_t e, const char* what) {
+  Status s = Err(KIVI_ERR_DEVICE);
+  s.detail = std::string("HIP error in ") + what + ": " + hipGetErrorString(e);
+  return s;
+}
+
+#define KIVI_TRY(expr)               \
+  do {                               \
+    Status _s = (expr);              \
+    if (!_s.ok()) return _s;         \
+  } while (0)
+
+#define HIP_TRY(expr, what)                      \
+  do {                                           \
+    hipError_t _e = (expr);                      \
+    if (_e != hipSuccess) return DevErr(_e, what); \
+  } while (0)
+
+// Display text of KiviError (src/error.rs:47-95) and of the extensions.
+void format_error(const Status& s, kivi_error* e) {
+  std::memset(e, 0, sizeof(*e));
+  e->code = s.code;
+  e->a = s.a;
+  e->b = s.b;
+  if (s.name != nullptr) std::snprintf(e->name, sizeof(e->name), "%s", s.name);
+  char* m = e->message;
+  const size_t n = sizeof(e->message);
+  const unsigned long long A = s.a, B = s.b;
+  switch (s.code) {
+    case KIVI_ERR_INVALID_BITS:
+      std::snprintf(m, n, "bit width %llu is not supported; use 2, 4, or 8", A);
+      break;
+    case KIVI_ERR_MISALIGNED_GROUP:
+      std::snprintf(m, n, "group_size %llu * bits %llu must be a multiple of 32", A, B);
+      break;
+    case KIVI_ERR_RESIDUAL_LENGTH:
+      std::snprintf(m, n, "residual_length %llu must be a positive multiple of group_size %llu", A, B);
+      break;
+    case KIVI_ERR_HEAD_DIM:
+      std::snprintf(m, n, "head_dim %llu must be a positive multiple of group_size %llu", A, B);
+      break;
+    case KIVI_ERR_TOKEN_GROUP:
+      std::snprintf(m, n,
+                    "token count %llu must be a positive multiple of group_size %llu for "
+                    "per-channel quantization",
+                    A, B);
+      break;
+    case KIVI_ERR_ZERO_DIMENSION:
+      std::snprintf(m, n, "%s must be greater than zero", s.name ? s.name : "?");
+      break;
+    case KIVI_ERR_SHAPE:
+      std::snprintf(m, n, "expected %llu elements, got %llu", A, B);
+      break;
+    case KIVI_ERR_QUERY_HEADS:
+      std::snprintf(m, n, "num_q_heads %llu must be a positive multiple of num_kv_heads %llu", A, B);
+      break;
+    case KIVI_ERR_NULL_ARGUMENT:
+      std::snprintf(m, n, "%s must not be null", s.name ? s.name : "?");
+      break;
+    case KIVI_ERR_DEVICE:
+      std::snprintf(m, n, "%s", s.detail.empty() ? "HIP device error" : s.detail.c_str());
+      break;
+    case KIVI_ERR_CAPACITY:
+      std::snprintf(m, n, "size %llu exceeds the supported limit %llu", A, B);
+      break;
+    case KIVI_ERR_UNSUPPORTED:
+      std::snprintf(m, n, "%s %llu is outside this build's limit %llu", s.name ? s.name : "value", A, B);
+      break;
+    case KIVI_ERR_MISMATCHED_PREFIX:
+      std::snprintf(m, n, "session %llu does not share the first session's prefix", A);
+      break;
+    default:
+      std::snprintf(m, n, "error %d", s.code);
+      break;
+  }
+}
+
+kivi_status report(const Status& s, kivi_error* err) {
+  if (err != nullptr) {
+    if (s.ok())
+      std::memset(err, 0, sizeof(*err));
+    else
+      format_error(s, err);
+  }
+  return static_cast<kivi_status>(s.code);
+}
+
+template <class F>
+kivi_status guarded(kivi_error* err, F&& f) {
+  try {
+    return report(f(), err);
+  } catch (const std::bad_alloc&) {
+    return report(Err(KIVI_ERR_CAPACITY, 0, 0), err);
+  } catch (...) {
+    Status s = Err(KIVI_ERR_DEVICE);
+    s.detail = "unexpected exception";
+    return report(s, err);
+  }
+}
+
+Status need(const void* p, const char* name) {
+  return p == nullptr ? Err(KIVI_ERR_NULL_ARGUMENT, 0, 0, name) : Status{};
+}
+// A null pointer is an empty slice only when the length is 0.
+Status need_slice(const void* p, size_t len, const char* name) {
+  return (p == nullptr && len != 0) ? Err(KIVI_ERR_NULL_ARGUMENT, 0, 0, name) : Status{};
+}
+
+// Checked products for shape arithmetic (the reference would overflow silently).
+Status mul(size_t a, size_t b, size_t* out) {
+  if (__builtin_mul_overflow(a, b, out)) return Err(KIVI_ERR_CAPACITY, a, SIZE_MAX / (b ? b : 1));
+  return Status{};
+}
+Status mul4(size_t a, size_t b, size_t c, size_t d, size_t* out) {
+  size_t x, y;
+  KIVI_TRY(mul(a, b, &x));
+  KIVI_TRY(mul(x, c, &y));
+  return mul(y, d, out);
+}
+
+// ---------------------------------------------------------------- config checks
+
+// check_bits_group (src/config.rs:47-55) and try_new (src/config.rs:31-45).
+Status check_bits_group(uint8_t bits, size_t group_size) {
+  if (!(bits == 2 || bits == 4 || bits == 8)) return Err(KIVI_ERR_INVALID_BITS, bits);
+  if (group_size == 0 || (group_size * bits) % 32 != 0)
+    return Err(KIVI_ERR_MISALIGNED_GROUP, group_size, bits);
+  return Status{};
+}
+Status check_config(const kivi_config& c) {
+  KIVI_TRY(check_bits_group(c.bits, c.group_size));
+  if (c.residual_length == 0 || c.residual_length % c.group_size != 0)
+    return Err(KIVI_ERR_RESIDUAL_LENGTH, c.residual_length, c.group_size);
+  return Status{};
+}
+
+// Limits of this build (kernels index units and rows with 32-bit counters and stage one
+// group / one 64-token value block per workgroup in LDS).
+constexpr size_t kMaxHeadDim = 1024;
+constexpr size_t kMaxKeyTile = 65536;       // G * D bytes of key codes staged per workgroup
+constexpr size_t kMaxResidual = 1u << 20;
+constexpr size_t kMaxUnits = (size_t)1 << 30;
+constexpr size_t kMaxGqD = 8192;            // (num_q_heads/num_kv_heads) * head_dim
+
+Status check_limits(const kivi_config& c, size_t batch, size_t heads, size_t head_dim) {
+  if (head_dim > kMaxHeadDim) return Err(KIVI_ERR_UNSUPPORTED, head_dim, kMaxHeadDim, "head_dim");
+  if (c.group_size * head_dim > kMaxKeyTile)
+    return Err(KIVI_ERR_UNSUPPORTED, c.group_size * head_dim, kMaxKeyTile, "group_size*head_dim");
+  if (c.residual_length > kMaxResidual)
+    return Err(KIVI_ERR_UNSUPPORTED, c.residual_length, kMaxResidual, "residual_length");
+  size_t units;
+  KIVI_TRY(mul(batch, heads, &units));
+  if (units > kMaxUnits) return Err(KIVI_ERR_UNSUPPORTED, units, kMaxUnits, "batch*num_kv_heads");
+  return Status{};
+}
+
+// ---------------------------------------------------------------- device plumbing
+
+int device_count() {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+  return n;
+}
+
+Status current_device(int* dev) {
+  if (device_count() <= 0) {
+    Status s = Err(KIVI_ERR_DEVICE);
+    s.detail = "no HIP device is available (the library has no CPU path)";
+    return s;
+  }
+  HIP_TRY(hipGetDevice(dev), "hipGetDevice");
+  return Status{};
+}
+
+// Makes `dev` current for the scope and restores the caller's device.
+struct DeviceScope {
+  int prev = -1;
+  bool changed = false;
+  explicit DeviceScope(int dev) {
+    if (hipGetDevice(&prev) == hipSuccess && prev != dev) {
+      changed = hipSetDevice(dev) == hipSuccess;
+    }
+  }
+  ~DeviceScope() {
+    if (changed) (void)hipSetDevice(prev);
+  }
+};
+
+struct DevBuf {
+  void* p = nullptr;
+  size_t bytes = 0;
+  DevBuf() = default;
+  DevBuf(const DevBuf&) = delete;
+  DevBuf& operator=(const DevBuf&) = delete;
+  ~DevBuf() { release(); }
+  void release() {
+    if (p != nullptr) (void)hipFree(p);
+    p = nullptr;
+    bytes = 0;
+  }
+  template <class T>
+  T* as() const {
+    return static_cast<T*>(p);
+  }
+  Status alloc_zero(size_t n, hipStream_t s, const char* what) {
+    release();
+    if (n == 0) return Status{};
+    HIP_TRY(hipMalloc(&p, n), what);
+    bytes = n;
+    HIP_TRY(hipMemsetAsync(p, 0, n, s), what);
+    return Status{};
+  }
+};
+
+// Stream-ordered scratch for one call.
+struct Scratch {
+  void* p = nullptr;
+  hipStream_t s = nullptr;
+  ~Scratch() {
+    if (p != nullptr) (void)hipFreeAsync(p, s);
+  }
+  Status get(size_t bytes, hipStream_t stream, const char* what) {
+    s = stream;
+    if (bytes == 0) return Status{};
+    HIP_TRY(hipMallocAsync(&p, bytes, stream), what);
+    return Status{};
+  }
+  template <class T>
+  T* as() const {
+    return static_cast<T*>(p);
+  }
+};
+
+uint64_t lcm64(uint64_t a, uint64_t b) { return a / std::gcd(a, b) * b; }
+
+// ---------------------------------------------------------------- cache state
+
+struct CacheCore {
+  kivi_config cfg{};
+  size_t batch = 0, heads = 0, head_dim = 0;
+  int device = 0;
+  Geometry geo{};
+  DevBuf kcodes, kparams, vcodes, vparams, kres, vring;
+  uint64_t seq = 0, kq = 0, vq = 0;
+  uint32_t kres_len = 0, vres_len = 0, vhead = 0;
+  hipStream_t stream = nullptr;
+
+  uint32_t units() const { return geo.units; }
+  uint64_t granule() const { return lcm64(kValueBlock, cfg.group_size); }
+
+  CacheView view() const {
+    CacheView v;
+    v.geo = geo;
+    v.kcodes = kcodes.as<uint32_t>();
+    v.kparams = kparams.as<float>();
+    v.vcodes = vcodes.as<uint32_t>();
+    v.vparams = vparams.as<float>();
+    v.kres = kres.as<float>();
+    v.vring = vring.as<float>();
+    return v;
+  }
+  SeqState state() const {
+    SeqState s;
+    s.kq = kq;
+    s.vq = vq;
+    s.kres = kres_len;
+    s.vres = vres_len;
+    s.vhead = vhead;
+    return s;
+  }
+
+  // Allocate residual buffers (src/cache.rs:105-119 preallocates them too).
+  Status init(hipStream_t s) {
+    geo.bits = cfg.bits;
+    geo.G = static_cast<uint32_t>(cfg.group_size);
+    geo.R = static_cast<uint32_t>(cfg.residual_length);
+    geo.D = static_cast<uint32_t>(head_dim);
+    geo.units = static_cast<uint32_t>(batch * heads);
+    geo.cap = 0;
+    const size_t rbytes = (size_t)geo.units * geo.R * geo.D * sizeof(float);
+    KIVI_TRY(kres.alloc_zero(rbytes, s, "key residual"));
+    KIVI_TRY(vring.alloc_zero(rbytes, s, "value window"));
+    return Status{};
+  }
+
+  // Grow the packed arenas to hold `tokens` per unit, keeping their contents.
+  Status ensure_capacity(uint64_t tokens, hipStream_t s) {
+    if (tokens <= geo.cap) return Status{};
+    const uint64_t gran = granule();
+    uint64_t want = std::max<uint64_t>(tokens, geo.cap * 2);
+    want = std::max<uint64_t>(want, 256);
+    want = (want + gran - 1) / gran * gran;
+    Geometry ng = geo;
+    ng.cap = want;
+    DevBuf nkc, nkp, nvc, nvp;
+    KIVI_TRY(nkc.alloc_zero(ng.kcodes_unit() * ng.units * 4, s, "key codes"));
+    KIVI_TRY(nkp.alloc_zero(ng.kparams_unit() * ng.units * 4, s, "key params"));
+    KIVI_TRY(nvc.alloc_zero(ng.vcodes_unit() * ng.units * 4, s, "value codes"));
+    KIVI_TRY(nvp.alloc_zero(ng.vparams_unit() * ng.units * 4, s, "value params"));
+    if (geo.cap > 0) {
+      HIP_TRY(copy_units(nkc.p, ng.kcodes_unit() * 4, kcodes.p, geo.kcodes_unit() * 4,
+                         geo.kcodes_unit() * 4, geo.units, s), "grow key codes");
+      HIP_TRY(copy_units(nkp.p, ng.kparams_unit() * 4, kparams.p, geo.kparams_unit() * 4,
+                         geo.kparams_unit() * 4, geo.units, s), "grow key params");
+      HIP_TRY(copy_units(nvc.p, ng.vcodes_unit() * 4, vcodes.p, geo.vcodes_unit() * 4,
+                         geo.vcodes_unit() * 4, geo.units, s), "grow value codes");
+      HIP_TRY(copy_units(nvp.p, ng.vparams_unit() * 4, vparams.p, geo.vparams_unit() * 4,
+                         geo.vparams_unit() * 4, geo.units, s), "grow value params");
+      HIP_TRY(hipStreamSynchronize(s), "grow");
+    }
+    std::swap(kcodes.p, nkc.p);
+    std::swap(kcodes.bytes, nkc.bytes);
+    std::swap(kparams.p, nkp.p);
+    std::swap(kparams.bytes, nkp.bytes);
+    std::swap(vcodes.p, nvc.p);
+    std::swap(vcodes.bytes, nvc.bytes);
+    std::swap(vparams.p, nvp.p);
+    std::swap(vparams.bytes, nvp.bytes);
+    geo.cap = want;
+    return Status{};
+  }
+
+  // KiviCache::append on device rows (src/cache.rs:186-214, append_keys :382-430,
+  // append_values :432-484). keys/values are [units][n][D] device arrays.
+  Status append_rows(const float* keys, const float* values, uint64_t n, hipStream_t s) {
+    if (n == 0) return Status{};
+    const uint64_t R = cfg.residual_length, G = cfg.group_size, D = head_dim;
+    const uint64_t kq_after = kq + ((kres_len + n) / R) * R;
+    const uint64_t total = seq + n;
+    const uint64_t vq_after = total > R ? total - R : 0;
+    KIVI_TRY(ensure_capacity(std::max(kq_after, vq_after), s));
+    const CacheView cv = view();
+    const RowSource kin{keys, n * D, 0, 0};
+    // ---- keys: fill the residual, flush every R tokens, quantize whole R-blocks of the
+    // input in place (the same groups the reference forms by copy-then-flush).
+    uint64_t off = 0;
+    if (kres_len > 0) {
+      const uint64_t take = std::min<uint64_t>(R - kres_len, n);
+      HIP_TRY(launch_copy_rows(geo, RowSource{keys, n * D, 0, 0}, cv.kres, kres_len,
+                               static_cast<uint32_t>(take), s), "key residual copy");
+      kres_len += static_cast<uint32_t>(take);
+      off = take;
+      if (kres_len == R) {
+        HIP_TRY(launch_quant_keys(cv, RowSource{cv.kres, R * D, 0, 0}, kq / G,
+                                  static_cast<uint32_t>(R / G), s), "key flush");
+        kq += R;
+        kres_len = 0;
+      }
+    }
+    const uint64_t full = (n - off) / R;
+    if (full > 0) {
+      RowSource src = kin;
+      src.offset = off;
+      const uint64_t groups = full * R / G;
+      // keep one launch's grid within 2^31 workgroups
+      uint64_t done = 0;
+      while (done < groups) {
+        const uint64_t chunk = std::min<uint64_t>(groups - done, (1u << 30) / std::max<uint32_t>(geo.units, 1));
+        RowSource sc = src;
+        sc.offset = off + done * G;
+        HIP_TRY(launch_quant_keys(cv, sc, kq / G + done, static_cast<uint32_t>(chunk), s), "key quantize");
+        done += chunk;
+      }
+      kq += full * R;
+      off += full * R;
+    }
+    const uint64_t rem = n - off;
+    if (rem > 0) {
+      HIP_TRY(launch_copy_rows(geo, RowSource{keys, n * D, off, 0}, cv.kres, kres_len,
+                               static_cast<uint32_t>(rem), s), "key residual copy");
+      kres_len += static_cast<uint32_t>(rem);
+    }
+    // ---- values: sliding window of R tokens kept as a ring.
+    const RowSource ring{cv.vring, R * D, vhead, 1};
+    if (n >= R) {
+      const uint64_t quant_n = n - R;
+      HIP_TRY(launch_quant_values(cv, ring, vres_len, RowSource{values, n * D, 0, 0}, quant_n, vq, s),
+              "value quantize");
+      vq += vres_len + quant_n;
+      HIP_TRY(launch_copy_rows(geo, RowSource{values, n * D, quant_n, 0}, cv.vring, 0,
+                               static_cast<uint32_t>(R), s), "value window copy");
+      vhead = 0;
+      vres_len = static_cast<uint32_t>(R);
+    } else {
+      const uint64_t combined = vres_len + n;
+      const uint64_t drop = combined > R ? combined - R : 0;
+      if (drop > 0) {
+        HIP_TRY(launch_quant_values(cv, ring, static_cast<uint32_t>(drop), RowSource{nullptr, 0, 0, 0}, 0, vq, s),
+                "value evict");
+        vq += drop;
+        vhead = static_cast<uint32_t>((vhead + drop) % R);
+        vres_len -= static_cast<uint32_t>(drop);
+      }
+      HIP_TRY(launch_copy_rows(geo, RowSource{values, n * D, 0, 0}, cv.vring,
+                               static_cast<uint32_t>((vhead + vres_len) % R), static_cast<uint32_t>(n), s),
+              "value window copy");
+      vres_len += static_cast<uint32_t>(n);
+    }
+    seq += n;
+    return Status{};
+  }
+
+  // KiviCache::memory (src/cache.rs:362-380) from the counters.
+  kivi_memory_report memory() const {
+    kivi_memory_report r{};
+    const size_t u = units(), D = head_dim, G = cfg.group_size, b = cfg.bits;
+    r.tokens = seq;
+    r.key_code_bytes = u * kq * D * b / 8;
+    r.key_metadata_bytes = u * (kq / G) * D * 2 * 4;
+    r.value_code_bytes = u * vq * D * b / 8;
+    r.value_metadata_bytes = u * vq * (D / G) * 2 * 4;
+    const size_t elements = u * D;
+    r.key_residual_bytes = (size_t)kres_len * elements * 4;
+    r.value_residual_bytes = (size_t)vres_len * elements * 4;
+    r.residual_capacity_bytes = 2 * cfg.residual_length * elements * 4;
+    r.fp16_baseline_bytes = 2 * seq * elements * 2;
+    r.fp32_baseline_bytes = 2 * seq * elements * 4;
+    return r;
+  }
+
+  // Deep copy for SharedPrefix::from_cache (src/prefix.rs:74-92); the copy's arenas are
+  // sized to the frozen length.
+  Status copy_into(CacheCore& dst, hipStream_t s) const {
+    dst.cfg = cfg;
+    dst.batch = batch;
+    dst.heads = heads;
+    dst.head_dim = head_dim;
+    dst.device = device;
+    dst.seq = seq;
+    dst.kq = kq;
+    dst.vq = vq;
+    dst.kres_len = kres_len;
+    dst.vres_len = vres_len;
+    dst.vhead = vhead;
+    KIVI_TRY(dst.init(s));
+    const size_t rbytes = (size_t)geo.units * geo.R * geo.D * sizeof(float);
+    HIP_TRY(hipMemcpyAsync(dst.kres.p, kres.p, rbytes, hipMemcpyDeviceToDevice, s), "prefix copy");
+    HIP_TRY(hipMemcpyAsync(dst.vring.p, vring.p, rbytes, hipMemcpyDeviceToDevice, s), "prefix copy");
+    const uint64_t used = std::max(kq, vq);
+    if (used > 0) {
+      const uint64_t gran = granule();
+      Geometry ng = geo;
+      ng.cap = (used + gran - 1) / gran * gran;
+      KIVI_TRY(dst.kcodes.alloc_zero(ng.kcodes_unit() * ng.units * 4, s, "prefix key codes"));
+      KIVI_TRY(dst.kparams.alloc_zero(ng.kparams_unit() * ng.units * 4, s, "prefix key params"));
+      KIVI_TRY(dst.vcodes.alloc_zero(ng.vcodes_unit() * ng.units * 4, s, "prefix value codes"));
+      KIVI_TRY(dst.vparams.alloc_zero(ng.vparams_unit() * ng.units * 4, s, "prefix value params"));
+      HIP_TRY(copy_units(dst.kcodes.p, ng.kcodes_unit() * 4, kcodes.p, geo.kcodes_unit() * 4,
+                         ng.kcodes_unit() * 4, geo.units, s), "prefix copy");
+      HIP_TRY(copy_units(dst.kparams.p, ng.kparams_unit() * 4, kparams.p, geo.kparams_unit() * 4,
+                         ng.kparams_unit() * 4, geo.units, s), "prefix copy");
+      HIP_TRY(copy_units(dst.vcodes.p, ng.vcodes_unit() * 4, vcodes.p, geo.vcodes_unit() * 4,
+                         ng.vcodes_unit() * 4, geo.units, s), "prefix copy");
+      HIP_TRY(copy_units(dst.vparams.p, ng.vparams_unit() * 4, vparams.p, geo.vparams_unit() * 4,
+                         ng.vparams_unit() * 4, geo.units, s), "prefix copy");
+      dst.geo.cap = ng.cap;
+    }
+    return Status{};
+  }
+};
+
+size_t compressed_bytes(const kivi_memory_report& r) {
+  return r.key_code_bytes + r.key_metadata_bytes + r.value_code_bytes + r.value_metadata_bytes +
+         r.key_residual_bytes + r.value_residual_bytes;
+}
+
+// Attention over `core` plus an optional device suffix, writing `out` on the device.
+Status attend(const CacheCore& core, const float* suffix_k, const float* suffix_v, uint64_t L,
+              uint64_t suffix_stride, const float* query, size_t qh, float scale, float* out,
+              hipStream_t s) {
+  const size_t gq = qh / core.heads;
+  if (gq * core.head_dim > kMaxGqD)
+    return Err(KIVI_ERR_UNSUPPORTED, gq * core.head_dim, kMaxGqD, "(num_q_heads/num_kv_heads)*head_dim");
+  const size_t out_n = core.batch * qh * core.head_dim;
+  if (core.seq + L == 0) {
+    HIP_TRY(hipMemsetAsync(out, 0, out_n * sizeof(float), s), "attention zero output");
+    return Status{};
+  }
+  AttnProblem p{};
+  p.cache = core.view();
+  p.st = core.state();
+  p.seq = core.seq;
+  p.suffix_k = suffix_k;
+  p.suffix_v = suffix_v;
+  p.suffix_len = L;
+  p.suffix_stride = suffix_stride;
+  p.query = query;
+  p.out = out;
+  p.qh = static_cast<uint32_t>(qh);
+  p.heads = static_cast<uint32_t>(core.heads);
+  p.batch = static_cast<uint32_t>(core.batch);
+  p.scale = scale;
+  Scratch ws;
+  KIVI_TRY(ws.get(attention_workspace_floats(p) * sizeof(float), s, "attention workspace"));
+  HIP_TRY(launch_attention(p, ws.as<float>(), s), "attention");
+  return Status{};
+}
+
+// Shape checks of KiviCache::attention (src/cache.rs:230-242), then the out buffer.
+Status check_attention(size_t batch, size_t heads, size_t head_dim, size_t query_len,
+                       size_t num_q_heads, size_t out_len) {
+  if (num_q_heads == 0 || num_q_heads % heads != 0)
+    return Err(KIVI_ERR_QUERY_HEADS, num_q_heads, heads);
+  size_t expected;
+  KIVI_TRY(mul4(batch, num_q_heads, head_dim, 1, &expected));
+  if (query_len != expected) return Err(KIVI_ERR_SHAPE, expected, query_len);
+  if (out_len != expected) return Err(KIVI_ERR_SHAPE, expected, out_len);
+  return Status{};
+}
+
+Status sync(hipStream_t s, const char* what) {
+  HIP_TRY(hipStreamSynchronize(s), what);
+  HIP_TRY(hipGetLastError(), what);
+  return Status{};
+}
+
+}  // namespace
+}  // namespace kivi
+
+using namespace kivi;
+
+// ---------------------------------------------------------------- opaque handles
+
+struct kivi_cache {
+  CacheCore core;
+  std::mutex mu;  // one mutating call at a time (the reference's &mut self)
+};
+
+struct kivi_prefix_state {
+  CacheCore core;
+  size_t prefix_bytes = 0;
+};
+
+struct kivi_prefix {
+  std::shared_ptr<kivi_prefix_state> state;  // SharedPrefix = Arc<PrefixState>
+  std::atomic<int> refs{1};
+};
+
+struct kivi_session {
+  kivi_prefix* prefix = nullptr;  // holds one reference
+  DevBuf keys, values;            // [units][cap][D] fp32 suffix (the reference re-splices, src/prefix.rs:196-221)
+  uint64_t len = 0, cap = 0;
+};
+
+struct kivi_runtime {
+  kivi_cache cache;
+};
+
+struct kivi_quantized {
+  int device = 0;
+  int axis = 0;
+  uint8_t bits = 0;
+  size_t group_size = 0, batch = 0, heads = 0, tokens = 0, head_dim = 0;
+  DevBuf codes, params;  // reference PackedStream order, concatenated over units
+  size_t n_codes = 0, n_params = 0;
+};
+
+namespace {
+
+Status create_cache(const kivi_config* config, size_t batch, size_t heads, size_t head_dim,
+                    kivi_cache* c) {
+  KIVI_TRY(need(config, "config"));
+  KIVI_TRY(check_config(*config));
+  // KiviCache::new check order (src/cache.rs:93-104).
+  if (batch == 0) return Err(KIVI_ERR_ZERO_DIMENSION, 0, 0, "batch");
+  if (heads == 0) return Err(KIVI_ERR_ZERO_DIMENSION, 0, 0, "num_kv_heads");
+  if (head_dim == 0 || head_dim % config->group_size != 0)
+    return Err(KIVI_ERR_HEAD_DIM, head_dim, config->group_size);
+  KIVI_TRY(check_limits(*config, batch, heads, head_dim));
+  int dev = 0;
+  KIVI_TRY(current_device(&dev));
+  c->core.cfg = *config;
+  c->core.batch = batch;
+  c->core.heads = heads;
+  c->core.head_dim = head_dim;
+  c->core.device = dev;
+  KIVI_TRY(c->core.init(nullptr));
+  return sync(nullptr, "cache init");
+}
+
+Status cache_append(kivi_cache* c, const float* keys, size_t keys_len, const float* values,
+                    size_t values_len, size_t seq_len, bool device, hipStream_t stream) {
+  KIVI_TRY(need(c, "cache"));
+  CacheCore& core = c->core;
+  size_t expected;
+  KIVI_TRY(mul4(core.batch, core.heads, seq_len, core.head_dim, &expected));
+  if (keys_len != expected) return Err(KIVI_ERR_SHAPE, expected, keys_len);
+  if (values_len != expected) return Err(KIVI_ERR_SHAPE, expected, values_len);
+  if (seq_len == 0) return Status{};
+  KIVI_TRY(need_slice(keys, keys_len, "keys"));
+  KIVI_TRY(need_slice(values, values_len, "values"));
+  std::lock_guard<std::mutex> lock(c->mu);
+  DeviceScope scope(core.device);
+  if (device) return core.append_rows(keys, values, seq_len, stream);
+  hipStream_t s = core.stream;
+  Scratch dk, dv;
+  KIVI_TRY(dk.get(expected * 4, s, "append staging"));
+  KIVI_TRY(dv.get(expected * 4, s, "append staging"));
+  HIP_TRY(hipMemcpyAsync(dk.p, keys, expected * 4, hipMemcpyHostToDevice, s), "append H2D");
+  HIP_TRY(hipMemcpyAsync(dv.p, values, expected * 4, hipMemcpyHostToDevice, s), "append H2D");
+  KIVI_TRY(core.append_rows(dk.as<float>(), dv.as<float>(), seq_len, s));
+  return sync(s, "append");
+}
+
+Status cache_attention(const kivi_cache* c, const float* query, size_t query_len,
+                       size_t num_q_heads, float scale, float* out, size_t out_len, bool device,
+                       hipStream_t stream) {
+  KIVI_TRY(need(c, "cache"));
+  const CacheCore& core = c->core;
+  KIVI_TRY(check_attention(core.batch, core.heads, core.head_dim, query_len, num_q_heads, out_len));
+  KIVI_TRY(need_slice(query, query_len, "query"));
+  KIVI_TRY(need_slice(out, out_len, "out"));
+  DeviceScope scope(core.device);
+  if (device) return attend(core, nullptr, nullptr, 0, 0, query, num_q_heads, scale, out, stream);
+  hipStream_t s = core.stream;
+  Scratch dq, dout;
+  KIVI_TRY(dq.get(query_len * 4, s, "attention staging"));
+  KIVI_TRY(dout.get(out_len * 4, s, "attention staging"));
+  HIP_TRY(hipMemcpyAsync(dq.p, query, query_len * 4, hipMemcpyHostToDevice, s), "attention H2D");
+  KIVI_TRY(attend(core, nullptr, nullptr, 0, 0, dq.as<float>(), num_q_heads, scale, dout.as<float>(), s));
+  HIP_TRY(hipMemcpyAsync(out, dout.p, out_len * 4, hipMemcpyDeviceToHost, s), "attention D2H");
+  return sync(s, "attention");
+}
+
+Status session_attend(const kivi_session* se, const float* query, size_t query_len,
+                      size_t num_q_heads, float scale, float* out, size_t out_len, bool device,
+                      hipStream_t stream) {
+  KIVI_TRY(need(se, "session"));
+  const CacheCore& core = se->prefix->state->core;
+  KIVI_TRY(check_attention(core.batch, core.heads, core.head_dim, query_len, num_q_heads, out_len));
+  KIVI_TRY(need_slice(query, query_len, "query"));
+  KIVI_TRY(need_slice(out, out_len, "out"));
+  DeviceScope scope(core.device);
+  const uint64_t stride = se->cap * core.head_dim;
+  if (device)
+    return attend(core, se->keys.as<float>(), se->values.as<float>(), se->len, stride, query,
+                  num_q_heads, scale, out, stream);
+  hipStream_t s = nullptr;
+  Scratch dq, dout;
+  KIVI_TRY(dq.get(query_len * 4, s, "attention staging"));
+  KIVI_TRY(dout.get(out_len * 4, s, "attention staging"));
+  HIP_TRY(hipMemcpyAsync(dq.p, query, query_len * 4, hipMemcpyHostToDevice, s), "attention H2D");
+  KIVI_TRY(attend(core, se->keys.as<float>(), se->values.as<float>(), se->len, stride,
+                  dq.as<float>(), num_q_heads, scale, dout.as<float>(), s));
+  HIP_TRY(hipMemcpyAsync(out, dout.p, out_len * 4, hipMemcpyDeviceToHost, s), "attention D2H");
+  return sync(s, "session attention");
+}
+
+// RagSession::append (src/prefix.rs:173-223) into a capacity-managed device suffix.
+Status session_append(kivi_session* se, const float* keys, size_t keys_len, const float* values,
+                      size_t values_len, size_t seq_len, bool device, hipStream_t stream) {
+  KIVI_TRY(need(se, "session"));
+  const CacheCore& core = se->prefix->state->core;
+  size_t expected;
+  KIVI_TRY(mul4(core.batch, core.heads, seq_len, core.head_dim, &expected));
+  if (keys_len != expected) return Err(KIVI_ERR_SHAPE, expected, keys_len);
+  if (values_len != expected) return Err(KIVI_ERR_SHAPE, expected, values_len);
+  if (seq_len == 0) return Status{};
+  KIVI_TRY(need_slice(keys, keys_len, "keys"));
+  KIVI_TRY(need_slice(values, values_len, "values"));
+  DeviceScope scope(core.device);
+  hipStream_t s = device ? stream : nullptr;
+  const size_t units = core.batch * core.heads, D = core.head_dim;
+  const uint64_t new_len = se->len + seq_len;
+  if (new_len > se->cap) {
+    const uint64_t cap = std::max<uint64_t>(new_len, std::max<uint64_t>(2 * se->cap, 16));
+    DevBuf nk, nv;
+    KIVI_TRY(nk.alloc_zero(units * cap * D * 4, s, "session suffix"));
+    KIVI_TRY(nv.alloc_zero(units * cap * D * 4, s, "session suffix"));
+    if (se->len > 0) {
+      HIP_TRY(copy_units(nk.p, cap * D * 4, se->keys.p, se->cap * D * 4, se->len * D * 4, units, s), "suffix grow");
+      HIP_TRY(copy_units(nv.p, cap * D * 4, se->values.p, se->cap * D * 4, se->len * D * 4, units, s), "suffix grow");
+    }
+    HIP_TRY(hipStreamSynchronize(s), "suffix grow");
+    std::swap(se->keys.p, nk.p);
+    std::swap(se->keys.bytes, nk.bytes);
+    std::swap(se->values.p, nv.p);
+    std::swap(se->values.bytes, nv.bytes);
+    se->cap = cap;
+  }
+  const hipMemcpyKind kind = device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
+  const size_t row = seq_len * D * 4;
+  HIP_TRY(hipMemcpy2DAsync(se->keys.as<float>() + se->len * D, se->cap * D * 4, keys, row, row,
+                           units, kind, s), "suffix append");
+  HIP_TRY(hipMemcpy2DAsync(se->values.as<float>() + se->len * D, se->cap * D * 4, values, row, row,
+                           units, kind, s), "suffix append");
+  se->len = new_len;
+  if (!device) return sync(s, "session append");
+  return Status{};
+}
+
+Status batched_sessions(const kivi_session* const* sessions, size_t n, const float* queries,
+                        size_t queries_len, size_t num_q_heads, float scale, float* out,
+                        size_t out_len, bool device, hipStream_t stream) {
+  KIVI_TRY(need_slice(sessions, n, "sessions"));
+  if (n == 0) {
+    if (queries_len != 0) return Err(KIVI_ERR_SHAPE, 0, queries_len);
+    if (out_len != 0) return Err(KIVI_ERR_SHAPE, 0, out_len);
+    return Status{};
+  }
+  for (size_t i = 0; i < n; ++i) KIVI_TRY(need(sessions[i], "sessions[i]"));
+  const kivi_prefix_state* st = sessions[0]->prefix->state.get();
+  for (size_t i = 1; i < n; ++i)
+    if (sessions[i]->prefix->state.get() != st) return Err(KIVI_ERR_MISMATCHED_PREFIX, i, 0);
+  const CacheCore& core = st->core;
+  if (num_q_heads == 0 || num_q_heads % core.heads != 0)
+    return Err(KIVI_ERR_QUERY_HEADS, num_q_heads, core.heads);
+  size_t per, all;
+  KIVI_TRY(mul4(core.batch, num_q_heads, core.head_dim, 1, &per));
+  KIVI_TRY(mul(per, n, &all));
+  if (queries_len != all) return Err(KIVI_ERR_SHAPE, all, queries_len);
+  if (out_len != all) return Err(KIVI_ERR_SHAPE, all, out_len);
+  KIVI_TRY(need_slice(queries, queries_len, "queries"));
+  KIVI_TRY(need_slice(out, out_len, "out"));
+  DeviceScope scope(core.device);
+  hipStream_t s = device ? stream : nullptr;
+  const float* dq = queries;
+  float* dout = out;
+  Scratch sq, so;
+  if (!device) {
+    KIVI_TRY(sq.get(all * 4, s, "sessions staging"));
+    KIVI_TRY(so.get(all * 4, s, "sessions staging"));
+    HIP_TRY(hipMemcpyAsync(sq.p, queries, all * 4, hipMemcpyHostToDevice, s), "sessions H2D");
+    dq = sq.as<float>();
+    dout = so.as<float>();
+  }
+  for (size_t i = 0; i < n; ++i) {
+    const kivi_session* se = sessions[i];
+    KIVI_TRY(attend(core, se->keys.as<float>(), se->values.as<float>(), se->len, se->cap * core.head_dim,
+                    dq + i * per, num_q_heads, scale, dout + i * per, s));
+  }
+  if (!device) {
+    HIP_TRY(hipMemcpyAsync(out, dout, all * 4, hipMemcpyDeviceToHost, s), "sessions D2H");
+    return sync(s, "sessions attention");
+  }
+  return Status{};
+}
+
+// check_quant_args (src/quant.rs:235-273).
+Status check_quant_args(size_t data_len, size_t batch, size_t heads, size_t tokens,
+                        size_t head_dim, uint8_t bits, size_t group_size, bool per_channel) {
+  KIVI_TRY(check_bits_group(bits, group_size));
+  if (batch == 0) return Err(KIVI_ERR_ZERO_DIMENSION, 0, 0, "batch");
+  if (heads == 0) return Err(KIVI_ERR_ZERO_DIMENSION, 0, 0, "heads");
+  if (head_dim == 0) return Err(KIVI_ERR_ZERO_DIMENSION, 0, 0, "head_dim");
+  if (per_channel) {
+    if (tokens == 0 || tokens % group_size != 0) return Err(KIVI_ERR_TOKEN_GROUP, tokens, group_size);
+  } else if (head_dim % group_size != 0) {
+    return Err(KIVI_ERR_HEAD_DIM, head_dim, group_size);
+  }
+  size_t expected;
+  KIVI_TRY(mul4(batch, heads, tokens, head_dim, &expected));
+  if (data_len != expected) return Err(KIVI_ERR_SHAPE, expected, data_len);
+  return Status{};
+}
+
+Status quantize(const float* data, size_t data_len, size_t batch, size_t heads, size_t tokens,
+                size_t head_dim, uint8_t bits, size_t group_size, bool per_channel, bool device,
+                hipStream_t stream, kivi_quantized** out) {
+  KIVI_TRY(check_quant_args(data_len, batch, heads, tokens, head_dim, bits, group_size, per_channel));
+  KIVI_TRY(need(out, "out"));
+  KIVI_TRY(need_slice(data, data_len, "data"));
+  if (head_dim > kMaxHeadDim) return Err(KIVI_ERR_UNSUPPORTED, head_dim, kMaxHeadDim, "head_dim");
+  if (per_channel && group_size * head_dim > kMaxKeyTile)
+    return Err(KIVI_ERR_UNSUPPORTED, group_size * head_dim, kMaxKeyTile, "group_size*head_dim");
+  if (batch * heads > kMaxUnits) return Err(KIVI_ERR_UNSUPPORTED, batch * heads, kMaxUnits, "batch*heads");
+  int dev = 0;
+  KIVI_TRY(current_device(&dev));
+  auto q = std::make_unique<kivi_quantized>();
+  q->device = dev;
+  q->axis = per_channel ? KIVI_AXIS_PER_CHANNEL : KIVI_AXIS_PER_TOKEN;
+  q->bits = bits;
+  q->group_size = group_size;
+  q->batch = batch;
+  q->heads = heads;
+  q->tokens = tokens;
+  q->head_dim = head_dim;
+  const size_t units = batch * heads;
+  q->n_codes = units * tokens * head_dim / (32 / bits);
+  q->n_params = per_channel ? units * (tokens / group_size) * head_dim * 2
+                            : units * tokens * (head_dim / group_size) * 2;
+  hipStream_t s = device ? stream : nullptr;
+  KIVI_TRY(q->codes.alloc_zero(q->n_codes * 4, s, "quantized codes"));
+  KIVI_TRY(q->params.alloc_zero(q->n_params * 4, s, "quantized params"));
+  const float* src = data;
+  Scratch staging;
+  if (!device) {
+    KIVI_TRY(staging.get(data_len * 4, s, "quantize staging"));
+    HIP_TRY(hipMemcpyAsync(staging.p, data, data_len * 4, hipMemcpyHostToDevice, s), "quantize H2D");
+    src = staging.as<float>();
+  }
+  if (per_channel) {
+    HIP_TRY(launch_quant_ref_keys(src, static_cast<uint32_t>(units), tokens, static_cast<uint32_t>(head_dim),
+                                  bits, static_cast<uint32_t>(group_size), q->codes.as<uint32_t>(),
+                                  q->params.as<float>(), s), "quantize_per_channel");
+  } else {
+    HIP_TRY(launch_quant_ref_values(src, static_cast<uint32_t>(units), tokens, static_cast<uint32_t>(head_dim),
+                                    bits, static_cast<uint32_t>(group_size), q->codes.as<uint32_t>(),
+                                    q->params.as<float>(), s), "quantize_per_token");
+  }
+  if (!device) KIVI_TRY(sync(s, "quantize"));
+  *out = q.release();
+  return Status{};
+}
+
+Status quantized_read(const kivi_quantized* q, void* out, size_t out_len, size_t want,
+                      int what /*0 codes 1 pytorch 2 params 3 dequant*/) {
+  KIVI_TRY(need(q, "quantized"));
+  if (out_len != want) return Err(KIVI_ERR_SHAPE, want, out_len);
+  if (want == 0) return Status{};
+  KIVI_TRY(need(out, "out"));
+  DeviceScope scope(q->device);
+  hipStream_t s = nullptr;
+  const uint32_t units = static_cast<uint32_t>(q->batch * q->heads);
+  if (what == 0 || what == 2) {
+    const void* src = what == 0 ? q->codes.p : q->params.p;
+    HIP_TRY(hipMemcpyAsync(out, src, want * 4, hipMemcpyDeviceToHost, s), "quantized D2H");
+    return sync(s, "quantized read");
+  }
+  Scratch tmp;
+  KIVI_TRY(tmp.get(want * 4, s, "quantized read"));
+  if (what == 1) {
+    HIP_TRY(launch_pytorch_order(q->codes.as<uint32_t>(), units, q->tokens, static_cast<uint32_t>(q->head_dim),
+                                 q->bits, static_cast<uint32_t>(q->group_size),
+                                 q->axis == KIVI_AXIS_PER_CHANNEL, tmp.as<uint32_t>(), s), "pytorch_codes");
+  } else {
+    HIP_TRY(launch_dequant_ref(q->codes.as<uint32_t>(), q->params.as<float>(), units, q->tokens,
+                               static_cast<uint32_t>(q->head_dim), q->bits,
+                               static_cast<uint32_t>(q->group_size), q->axis == KIVI_AXIS_PER_CHANNEL,
+                               tmp.as<float>(), s), "dequantize");
+  }
+  HIP_TRY(hipMemcpyAsync(out, tmp.p, want * 4, hipMemcpyDeviceToHost, s), "quantized D2H");
+  return sync(s, "quantized read");
+}
+
+}  // namespace
+
+// ================================================================= C ABI
+extern "C" {
+
+void kivi_config_default(kivi_config* out) {
+  if (out == nullptr) return;
+  out->bits = 2;
+  out->group_size = 32;
+  out->residual_length = 128;
+}
+
+kivi_status kivi_config_try_new(uint8_t bits, size_t group_size, size_t residual_length,
+                                kivi_config* out, kivi_error* err) {
+  return guarded(err, [&] {
+    kivi_config c{bits, group_size, residual_length};
+    KIVI_TRY(check_config(c));
+    KIVI_TRY(need(out, "out"));
+    *out = c;
+    return Status{};
+  });
+}
+
+size_t kivi_memory_compressed_bytes(const kivi_memory_report* r) { return r ? compressed_bytes(*r) : 0; }
+
+double kivi_memory_compression_ratio_vs_fp16(const kivi_memory_report* r) {
+  if (r == nullptr) return 1.0;
+  const size_t c = compressed_bytes(*r);
+  return c == 0 ? 1.0 : static_cast<double>(r->fp16_baseline_bytes) / static_cast<double>(c);
+}
+
+double kivi_footprint_savings_vs_fp16(const kivi_prefix_footprint* f) {
+  if (f == nullptr || f->shared_total_bytes == 0) return 1.0;
+  return static_cast<double>(f->fp16_all_users_bytes) / static_cast<double>(f->shared_total_bytes);
+}
+
+kivi_status kivi_cache_new(const kivi_config* config, size_t batch, size_t num_kv_heads,
+                           size_t head_dim, kivi_cache** out, kivi_error* err) {
+  return guarded(err, [&] {
+    auto c = std::make_unique<kivi_cache>();
+    KIVI_TRY(create_cache(config, batch, num_kv_heads, head_dim, c.get()));
+    KIVI_TRY(need(out, "out"));
+    *out = c.release();
+    return Status{};
+  });
+}
+
+void kivi_cache_free(kivi_cache* cache) {
+  if (cache == nullptr) return;
+  DeviceScope scope(cache->core.device);
+  (void)hipStreamSynchronize(cache->core.stream);
+  delete cache;
+}
+
+kivi_status kivi_cache_set_stream(kivi_cache* cache, void* stream, kivi_error* err) {
+  return guarded(err, [&] {
+    KIVI_TRY(need(cache, "cache"));
+    cache->core.stream = static_cast<hipStream_t>(stream);
+    return Status{};
+  });
+}
+
+kivi_config kivi_cache_config(const kivi_cache* c) { return c->core.cfg; }
+size_t kivi_cache_batch_size(const kivi_cache* c) { return c->core.batch; }
+size_t kivi_cache_num_kv_heads(const kivi_cache* c) { return c->core.heads; }
+size_t kivi_cache_head_dim(const kivi_cache* c) { return c->core.head_dim; }
+size_t kivi_cache_sequence_length(const kivi_cache* c) { return c->core.seq; }
+size_t kivi_cache_key_residual_len(const kivi_cache* c) { return c->core.kres_len; }
+size_t kivi_cache_value_residual_len(const kivi_cache* c) { return c->core.vres_len; }
+size_t kivi_cache_quantized_key_tokens(const kivi_cache* c) { return c->core.kq; }
+size_t kivi_cache_quantized_value_tokens(const kivi_cache* c) { return c->core.vq; }
+size_t kivi_cache_tokens_until_key_flush(const kivi_cache* c) {
+  const size_t r = c->core.cfg.residual_length;
+  return r > c->core.kres_len ? r - c->core.kres_len : 0;
+}
+size_t kivi_cache_value_residual_slots_remaining(const kivi_cache* c) {
+  const size_t r = c->core.cfg.residual_length;
+  return r > c->core.vres_len ? r - c->core.vres_len : 0;
+}
+
+kivi_status kivi_cache_append(kivi_cache* cache, const float* keys, size_t keys_len,
+                              const float* values, size_t values_len, size_t seq_len,
+                              kivi_error* err) {
+  return guarded(err, [&] {
+    return cache_append(cache, keys, keys_len, values, values_len, seq_len, false, nullptr);
+  });
+}
+
+kivi_status kivi_cache_append_device(kivi_cache* cache, const float* keys, size_t keys_len,
+                                     const float* values, size_t values_len, size_t seq_len,
+                                     void* stream, kivi_error* err) {
+  return guarded(err, [&] {
+    return cache_append(cache, keys, keys_len, values, values_len, seq_len, true,
+                        static_cast<hipStream_t>(stream));
+  });
+}
+
+kivi_status kivi_cache_attention(const kivi_cache* cache, const float* query, size_t query_len,
+                                 size_t num_q_heads, float scale, float* out, size_t out_len,
+                                 kivi_error* err) {
+  return guarded(err, [&] {
+    return cache_attention(cache, query, query_len, num_q_heads, scale, out, out_len, false, nullptr);
+  });
+}
+
+kivi_status kivi_cache_attention_device(const kivi_cache* cache, const float* query,
+                                        size_t query_len, size_t num_q_heads, float scale,
+                                        float* out, size_t out_len, void* stream,
+                                        kivi_error* err) {
+  return guarded(err, [&] {
+    return cache_attention(cache, query, query_len, num_q_heads, scale, out, out_len, true,
+                           static_cast<hipStream_t>(stream));
+  });
+}
+
+kivi_status kivi_cache_dequantize(const kivi_cache* cache, float* keys, size_t keys_len,
+                                  float* values, size_t values_len, kivi_error* err) {
+  return guarded(err, [&] {
+    KIVI_TRY(need(cache, "cache"));
+    const CacheCore& core = cache->core;
+    size_t n;
+    KIVI_TRY(mul4(core.batch, core.heads, core.seq, core.head_dim, &n));
+    if (keys_len != n) return Err(KIVI_ERR_SHAPE, n, keys_len);
+    if (values_len != n) return Err(KIVI_ERR_SHAPE, n, values_len);
+    if (n == 0) return Status{};
+    KIVI_TRY(need(keys, "keys"));
+    KIVI_TRY(need(values, "values"));
+    DeviceScope scope(core.device);
+    hipStream_t s = core.stream;
+    Scratch dk, dv;
+    KIVI_TRY(dk.get(n * 4, s, "dequantize"));
+    KIVI_TRY(dv.get(n * 4, s, "dequantize"));
+    HIP_TRY(launch_dequant_cache(core.view(), core.state(), dk.as<float>(), dv.as<float>(), s), "dequantize");
+    HIP_TRY(hipMemcpyAsync(keys, dk.p, n * 4, hipMemcpyDeviceToHost, s), "dequantize D2H");
+    HIP_TRY(hipMemcpyAsync(values, dv.p, n * 4, hipMemcpyDeviceToHost, s), "dequantize D2H");
+    return sync(s, "dequantize");
+  });
+}
+
+kivi_memory_report kivi_cache_memory(const kivi_cache* cache) { return cache->core.memory(); }
+
+kivi_status kivi_cache_export_streams(const kivi_cache* cache, uint32_t* key_codes,
+                                      size_t key_codes_len, float* key_params,
+                                      size_t key_params_len, uint32_t* value_codes,
+                                      size_t value_codes_len, float* value_params,
+                                      size_t value_params_len, kivi_error* err) {
+  return guarded(err, [&] {
+    KIVI_TRY(need(cache, "cache"));
+    const CacheCore& core = cache->core;
+    const size_t u = core.units(), D = core.head_dim, G = core.cfg.group_size;
+    const size_t nkc = u * core.kq * D / (32 / core.cfg.bits);
+    const size_t nkp = u * (core.kq / G) * D * 2;
+    const size_t nvc = u * core.vq * D / (32 / core.cfg.bits);
+    const size_t nvp = u * core.vq * (D / G) * 2;
+    if (key_codes && key_codes_len != nkc) return Err(KIVI_ERR_SHAPE, nkc, key_codes_len);
+    if (key_params && key_params_len != nkp) return Err(KIVI_ERR_SHAPE, nkp, key_params_len);
+    if (value_codes && value_codes_len != nvc) return Err(KIVI_ERR_SHAPE, nvc, value_codes_len);
+    if (value_params && value_params_len != nvp) return Err(KIVI_ERR_SHAPE, nvp, value_params_len);
+    DeviceScope scope(core.device);
+    hipStream_t s = core.stream;
+    const CacheView cv = core.view();
+    Scratch a, b, c, d;
+    if (key_codes && nkc) KIVI_TRY(a.get(nkc * 4, s, "export"));
+    if (key_params && nkp) KIVI_TRY(b.get(nkp * 4, s, "export"));
+    if (value_codes && nvc) KIVI_TRY(c.get(nvc * 4, s, "export"));
+    if (value_params && nvp) KIVI_TRY(d.get(nvp * 4, s, "export"));
+    HIP_TRY(launch_export_keys(cv, core.kq, a.as<uint32_t>(), b.as<float>(), s), "export keys");
+    HIP_TRY(launch_export_values(cv, core.vq, c.as<uint32_t>(), d.as<float>(), s), "export values");
+    if (a.p) HIP_TRY(hipMemcpyAsync(key_codes, a.p, nkc * 4, hipMemcpyDeviceToHost, s), "export D2H");
+    if (b.p) HIP_TRY(hipMemcpyAsync(key_params, b.p, nkp * 4, hipMemcpyDeviceToHost, s), "export D2H");
+    if (c.p) HIP_TRY(hipMemcpyAsync(value_codes, c.p, nvc * 4, hipMemcpyDeviceToHost, s), "export D2H");
+    if (d.p) HIP_TRY(hipMemcpyAsync(value_params, d.p, nvp * 4, hipMemcpyDeviceToHost, s), "export D2H");
+    return sync(s, "export");
+  });
+}
+
+kivi_status kivi_cache_reserve(kivi_cache* cache, size_t tokens, kivi_error* err) {
+  return guarded(err, [&] {
+    KIVI_TRY(need(cache, "cache"));
+    std::lock_guard<std::mutex> lock(cache->mu);
+    DeviceScope scope(cache->core.device);
+    KIVI_TRY(cache->core.ensure_capacity(tokens, cache->core.stream));
+    return sync(cache->core.stream, "reserve");
+  });
+}
+
+kivi_status kivi_cache_share_prefix(const kivi_cache* cache, kivi_prefix** out, kivi_error* err) {
+  return guarded(err, [&] {
+    KIVI_TRY(need(cache, "cache"));
+    KIVI_TRY(need(out, "out"));
+    DeviceScope scope(cache->core.device);
+    auto st = std::make_shared<kivi_prefix_state>();
+    KIVI_TRY(cache->core.copy_into(st->core, cache->core.stream));
+    KIVI_TRY(sync(cache->core.stream, "share_prefix"));
+    st->prefix_bytes = compressed_bytes(st->core.memory());
+    auto p = std::make_unique<kivi_prefix>();
+    p->state = std::move(st);
+    *out = p.release();
+    return Status{};
+  });
+}
+
+kivi_prefix* kivi_prefix_retain(kivi_prefix* prefix) {
+  if (prefix != nullptr) prefix->refs.fetch_add(1, std::memory_order_relaxed);
+  return prefix;
+}
+
+void kivi_prefix_release(kivi_prefix* prefix) {
+  if (prefix == nullptr) return;
+  if (prefix->refs.fetch_sub(1, std::memory_order_acq_rel) == 1) {
+    DeviceScope scope(prefix->state->core.device);
+    (void)hipDeviceSynchronize();
+    delete prefix;
+  }
+}
+
+kivi_config kivi_prefix_config(const kivi_prefix* p) { return p->state->core.cfg; }
+size_t kivi_prefix_batch_size(const kivi_prefix* p) { return p->state->core.batch; }
+size_t kivi_prefix_num_kv_heads(const kivi_prefix* p) { return p->state->core.heads; }
+size_t kivi_prefix_head_dim(const kivi_prefix* p) { return p->state->core.head_dim; }
+size_t kivi_prefix_prefix_tokens(const kivi_prefix* p) { return p->state->core.seq; }
+size_t kivi_prefix_prefix_bytes(const kivi_prefix* p) { return p->state->prefix_bytes; }
+int kivi_prefix_shares_allocation_with(const kivi_prefix* a, const kivi_prefix* b) {
+  return (a != nullptr && b != nullptr && a->state.get() == b->state.get()) ? 1 : 0;
+}
+
+// SharedPrefix::footprint (src/prefix.rs:136-152).
+kivi_prefix_footprint kivi_prefix_footprint_of(const kivi_prefix* p, size_t sessions,
+                                               size_t question_tokens) {
+  const CacheCore& c = p->state->core;
+  const size_t elements = c.batch * c.heads * c.head_dim;
+  const size_t question_bytes = sessions * question_tokens * elements * 2 * 4;
+  const size_t fp16_per_user = 2 * (c.seq + question_tokens) * elements * 2;
+  kivi_prefix_footprint f{};
+  f.prefix_tokens = c.seq;
+  f.question_tokens = question_tokens;
+  f.sessions = sessions;
+  f.prefix_bytes = p->state->prefix_bytes;
+  f.question_bytes = question_bytes;
+  f.shared_total_bytes = p->state->prefix_bytes + question_bytes;
+  f.fp16_per_user_bytes = fp16_per_user;
+  f.fp16_all_users_bytes = sessions * fp16_per_user;
+  return f;
+}
+
+kivi_status kivi_prefix_session(kivi_prefix* prefix, kivi_session** out, kivi_error* err) {
+  return guarded(err, [&] {
+    KIVI_TRY(need(prefix, "prefix"));
+    KIVI_TRY(need(out, "out"));
+    auto s = std::make_unique<kivi_session>();
+    s->prefix = kivi_prefix_retain(prefix);
+    *out = s.release();
+    return Status{};
+  });
+}
+
+void kivi_session_free(kivi_session* s) {
+  if (s == nullptr) return;
+  kivi_prefix* p = s->prefix;
+  {
+    DeviceScope scope(p->state->core.device);
+    (void)hipDeviceSynchronize();
+    delete s;
+  }
+  kivi_prefix_release(p);
+}
+
+kivi_prefix* kivi_session_prefix(const kivi_session* s) { return s->prefix; }
+size_t kivi_session_prefix_tokens(const kivi_session* s) { return s->prefix->state->core.seq; }
+size_t kivi_session_question_tokens(const kivi_session* s) { return s->len; }
+size_t kivi_session_sequence_length(const kivi_session* s) { return s->prefix->state->core.seq + s->len; }
+
+kivi_status kivi_session_append(kivi_session* session, const float* keys, size_t keys_len,
+                                const float* values, size_t values_len, size_t seq_len,
+                                kivi_error* err) {
+  return guarded(err, [&] {
+    return session_append(session, keys, keys_len, values, values_len, seq_len, false, nullptr);
+  });
+}
+
+kivi_status kivi_session_append_device(kivi_session* session, const float* keys,
+                                       size_t keys_len, const float* values, size_t values_len,
+                                       size_t seq_len, void* stream, kivi_error* err) {
+  return guarded(err, [&] {
+    return session_append(session, keys, keys_len, values, values_len, seq_len, true,
+                          static_cast<hipStream_t>(stream));
+  });
+}
+
+kivi_status kivi_session_attention(const kivi_session* session, const float* query,
+                                   size_t query_len, size_t num_q_heads, float scale, float* out,
+                                   size_t out_len, kivi_error* err) {
+  return guarded(err, [&] {
+    return session_attend(session, query, query_len, num_q_heads, scale, out, out_len, false, nullptr);
+  });
+}
+
+kivi_status kivi_sessions_attention_device(const kivi_session* const* sessions, size_t n,
+                                           const float* queries, size_t queries_len,
+                                           size_t num_q_heads, float scale, float* out,
+                                           size_t out_len, void* stream, kivi_error* err) {
+  return guarded(err, [&] {
+    return batched_sessions(sessions, n, queries, queries_len, num_q_heads, scale, out, out_len,
+                            true, static_cast<hipStream_t>(stream));
+  });
+}
+
+kivi_status kivi_sessions_attention(const kivi_session* const* sessions, size_t n,
+                                    const float* queries, size_t queries_len,
+                                    size_t num_q_heads, float scale, float* out, size_t out_len,
+                                    kivi_error* err) {
+  return guarded(err, [&] {
+    return batched_sessions(sessions, n, queries, queries_len, num_q_heads, scale, out, out_len,
+                            false, nullptr);
+  });
+}
+
+kivi_status kivi_runtime_new(const kivi_config* config, size_t batch, size_t num_kv_heads,
+                             size_t head_dim, kivi_runtime** out, kivi_error* err) {
+  return guarded(err, [&] {
+    auto rt = std::make_unique<kivi_runtime>();
+    KIVI_TRY(create_cache(config, batch, num_kv_heads, head_dim, &rt->cache));
+    KIVI_TRY(need(out, "out"));
+    *out = rt.release();
+    return Status{};
+  });
+}
+
+void kivi_runtime_free(kivi_runtime* rt) {
+  if (rt == nullptr) return;
+  DeviceScope scope(rt->cache.core.device);
+  (void)hipStreamSynchronize(rt->cache.core.stream);
+  delete rt;
+}
+
+kivi_cache* kivi_runtime_cache(kivi_runtime* rt) { return rt ? &rt->cache : nullptr; }
+
+kivi_status kivi_runtime_prefill(kivi_runtime* rt, const float* keys, size_t keys_len,
+                                 const float* values, size_t values_len, size_t seq_len,
+                                 kivi_error* err) {
+  return kivi_cache_append(rt ? &rt->cache : nullptr, keys, keys_len, values, values_len, seq_len, err);
+}
+
+// RuntimeKv::decode (src/runtime.rs:46-56): append(key, value, 1), then attention.
+kivi_status kivi_runtime_decode(kivi_runtime* rt, const float* key, size_t key_len,
+                                const float* value, size_t value_len, const float* query,
+                                size_t query_len, size_t num_q_heads, float scale, float* out,
+                                size_t out_len, kivi_error* err) {
+  kivi_status st = kivi_cache_append(rt ? &rt->cache : nullptr, key, key_len, value, value_len, 1, err);
+  if (st != KIVI_OK) return st;
+  return kivi_cache_attention(&rt->cache, query, query_len, num_q_heads, scale, out, out_len, err);
+}
+
+kivi_status kivi_runtime_decode_device(kivi_runtime* rt, const float* key, size_t key_len,
+                                       const float* value, size_t value_len, const float* query,
+                                       size_t query_len, size_t num_q_heads, float scale,
+                                       float* out, size_t out_len, void* stream,
+                                       kivi_error* err) {
+  kivi_status st = kivi_cache_append_device(rt ? &rt->cache : nullptr, key, key_len, value,
+                                            value_len, 1, stream, err);
+  if (st != KIVI_OK) return st;
+  return kivi_cache_attention_device(&rt->cache, query, query_len, num_q_heads, scale, out,
+                                     out_len, stream, err);
+}
+
+kivi_status kivi_quantize_per_channel(const float* data, size_t data_len, size_t batch,
+                                      size_t heads, size_t tokens, size_t head_dim, uint8_t bits,
+                                      size_t group_size, kivi_quantized** out, kivi_error* err) {
+  return guarded(err, [&] {
+    return quantize(data, data_len, batch, heads, tokens, head_dim, bits, group_size, true, false,
+                    nullptr, out);
+  });
+}
+
+kivi_status kivi_quantize_per_token(const float* data, size_t data_len, size_t batch,
+                                    size_t heads, size_t tokens, size_t head_dim, uint8_t bits,
+                                    size_t group_size, kivi_quantized** out, kivi_error* err) {
+  return guarded(err, [&] {
+    return quantize(data, data_len, batch, heads, tokens, head_dim, bits, group_size, false, false,
+                    nullptr, out);
+  });
+}
+
+kivi_status kivi_quantize_per_channel_device(const float* data, size_t data_len, size_t batch,
+                                             size_t heads, size_t tokens, size_t head_dim,
+                                             uint8_t bits, size_t group_size, void* stream,
+                                             kivi_quantized** out, kivi_error* err) {
+  return guarded(err, [&] {
+    return quantize(data, data_len, batch, heads, tokens, head_dim, bits, group_size, true, true,
+                    static_cast<hipStream_t>(stream), out);
+  });
+}
+
+kivi_status kivi_quantize_per_token_device(const float* data, size_t data_len, size_t batch,
+                                           size_t heads, size_t tokens, size_t head_dim,
+                                           uint8_t bits, size_t group_size, void* stream,
+                                           kivi_quantized** out, kivi_error* err) {
+  return guarded(err, [&] {
+    return quantize(data, data_len, batch, heads, tokens, head_dim, bits, group_size, false, true,
+                    static_cast<hipStream_t>(stream), out);
+  });
+}
+
+void kivi_quantized_free(kivi_quantized* q) {
+  if (q == nullptr) return;
+  DeviceScope scope(q->device);
+  (void)hipDeviceSynchronize();
+  delete q;
+}
+
+int kivi_quantized_axis(const kivi_quantized* q) { return q->axis; }
+uint8_t kivi_quantized_bits(const kivi_quantized* q) { return q->bits; }
+size_t kivi_quantized_group_size(const kivi_quantized* q) { return q->group_size; }
+size_t kivi_quantized_num_tokens(const kivi_quantized* q) { return q->tokens; }
+size_t kivi_quantized_code_bytes(const kivi_quantized* q) { return q->n_codes * 4; }
+size_t kivi_quantized_metadata_bytes(const kivi_quantized* q) { return q->n_params * 4; }
+
+kivi_status kivi_quantized_codes(const kivi_quantized* q, uint32_t* out, size_t out_len,
+                                 kivi_error* err) {
+  return guarded(err, [&] { return quantized_read(q, out, out_len, q ? q->n_codes : 0, 0); });
+}
+kivi_status kivi_quantized_pytorch_codes(const kivi_quantized* q, uint32_t* out, size_t out_len,
+                                         kivi_error* err) {
+  return guarded(err, [&] { return quantized_read(q, out, out_len, q ? q->n_codes : 0, 1); });
+}
+kivi_status kivi_quantized_scale_zero(const kivi_quantized* q, float* out, size_t out_len,
+                                      kivi_error* err) {
+  return guarded(err, [&] { return quantized_read(q, out, out_len, q ? q->n_params : 0, 2); });
+}
+kivi_status kivi_quantized_dequantize(const kivi_quantized* q, float* out, size_t out_len,
+                                      kivi_error* err) {
+  return guarded(err, [&] {
+    const size_t n = q ? q->batch * q->heads * q->tokens * q->head_dim : 0;
+    return quantized_read(q, out, out_len, n, 3);
+  });
+}
+
+const char* kivi_status_name(int32_t code) {
+  switch (code) {
+    case KIVI_OK: return "Ok";
+    case KIVI_ERR_INVALID_BITS: return "InvalidBits";
+    case KIVI_ERR_MISALIGNED_GROUP: return "MisalignedGroup";
+    case KIVI_ERR_RESIDUAL_LENGTH: return "ResidualLength";
+    case KIVI_ERR_HEAD_DIM: return "HeadDim";
+    case KIVI_ERR_TOKEN_GROUP: return "TokenGroup";
+    case KIVI_ERR_ZERO_DIMENSION: return "ZeroDimension";
+    case KIVI_ERR_SHAPE: return "Shape";
+    case KIVI_ERR_QUERY_HEADS: return "QueryHeads";
+    case KIVI_ERR_EARLY_LAYERS: return "EarlyLayers";
+    case KIVI_ERR_NULL_ARGUMENT: return "NullArgument";
+    case KIVI_ERR_DEVICE: return "Device";
+    case KIVI_ERR_CAPACITY: return "Capacity";
+    case KIVI_ERR_UNSUPPORTED: return "Unsupported";
+    case KIVI_ERR_MISMATCHED_PREFIX: return "MismatchedPrefix";
+    default: return "Unknown";
+  }
+}
+
+int32_t kivi_abi_version(void) { return KIVI_ABI_VERSION; }
+
+int32_t kivi_device_count(void) { return device_count(); }
+
+}  // extern "C"

@@ -1,0 +1,532 @@
+// kernels_quant.hip — KIVI quantization, residual/ring copies, stream export and
+// dequantization on CDNA4 (gfx950).
+//
+// Bit-exactness with the reference (src/quant.rs:453-485): scale = span/levels and
+// code = clamp(rint((x - zero)/scale), 0, levels) use IEEE-correct f32 division (hipcc's
+// default; -ffast-math and reciprocal-multiply are never used) and v_rndne (round half to
+// even, equal to the reference's floor-based rounding for every finite input). min/max are
+// order independent, so the reduction order is free.
+#include "common.hpp"
+
+namespace kivi {
+namespace {
+
+constexpr int kThreads = 256;
+
+__device__ __forceinline__ float scale_of(float span, float levels) {
+  return span == 0.0f ? 0.0f : span / levels;
+}
+
+__device__ __forceinline__ uint32_t quant_code(float x, float zero, float scale, float levels) {
+  if (scale == 0.0f) return 0u;
+  float r = rintf((x - zero) / scale);
+  if (r < 0.0f) {
+    r = 0.0f;
+  } else if (r > levels) {
+    r = levels;
+  }
+  return static_cast<uint32_t>(r);
+}
+
+__device__ __forceinline__ const float* source_row(const RowSource& s, uint32_t unit, uint64_t i,
+                                                   uint32_t R, uint32_t D) {
+  uint64_t tok = s.offset + i;
+  if (s.ring) tok %= R;
+  return s.base + unit * s.stride_unit + tok * D;
+}
+
+unsigned grid_for(uint64_t work, unsigned per_block = kThreads) {
+  uint64_t b = (work + per_block - 1) / per_block;
+  if (b > (1u << 20)) b = 1u << 20;  // grid-stride loops cover the rest
+  if (b == 0) b = 1;
+  return static_cast<unsigned>(b);
+}
+
+// ------------------------------------------------------------------ row copies
+
+template <int VEC>
+__global__ void __launch_bounds__(kThreads)
+    k_copy_rows(RowSource src, float* dst, uint32_t R, uint32_t D, uint32_t units,
+                uint32_t dst_slot, uint32_t count) {
+  const uint32_t per_row = D / VEC;
+  const uint64_t total = (uint64_t)units * count * per_row;
+  for (uint64_t idx = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; idx < total;
+       idx += (uint64_t)gridDim.x * blockDim.x) {
+    const uint32_t c = idx % per_row;
+    const uint64_t r = idx / per_row;
+    const uint32_t i = r % count;
+    const uint32_t unit = r / count;
+    const float* s = source_row(src, unit, i, R, D) + c * VEC;
+    float* d = dst + ((uint64_t)unit * R + (dst_slot + i) % R) * D + c * VEC;
+    if constexpr (VEC == 4) {
+      *reinterpret_cast<float4*>(d) = *reinterpret_cast<const float4*>(s);
+    } else {
+      *d = *s;
+    }
+  }
+}
+
+// ------------------------------------------------------------------ keys (native layout)
+// One workgroup per (unit, group): per-channel min/max over the group's G tokens
+// (src/quant.rs:296-306), (scale, zero) per channel (:307-311), codes for every token
+// (:312-323), then token-major words.
+__global__ void __launch_bounds__(kThreads)
+    k_quant_keys(CacheView c, RowSource src, uint64_t g0, uint32_t ngroups) {
+  extern __shared__ uint8_t codes_lds[];  // [G][D]
+  const Geometry& geo = c.geo;
+  const uint32_t G = geo.G, D = geo.D, bits = geo.bits;
+  const float levels = static_cast<float>(geo.levels());
+  const uint32_t unit = blockIdx.x / ngroups;
+  const uint32_t g = blockIdx.x % ngroups;
+  const float* rows = src.base + unit * src.stride_unit + (src.offset + (uint64_t)g * G) * D;
+  float2* params = reinterpret_cast<float2*>(c.kparams + unit * geo.kparams_unit() + (g0 + g) * D * 2);
+  for (uint32_t d = threadIdx.x; d < D; d += blockDim.x) {
+    float mn = INFINITY, mx = -INFINITY;
+    for (uint32_t t = 0; t < G; ++t) {
+      const float x = rows[(uint64_t)t * D + d];
+      mn = fminf(mn, x);
+      mx = fmaxf(mx, x);
+    }
+    const float zero = mn;
+    const float scale = scale_of(mx - zero, levels);
+    params[d] = make_float2(scale, zero);
+    for (uint32_t t = 0; t < G; ++t)
+      codes_lds[t * D + d] = static_cast<uint8_t>(quant_code(rows[(uint64_t)t * D + d], zero, scale, levels));
+  }
+  __syncthreads();
+  const uint32_t ppw = geo.ppw();
+  const uint32_t kw = geo.kwords_per_token();
+  uint32_t* words = c.kcodes + unit * geo.kcodes_unit() + (g0 + g) * G * kw;
+  for (uint32_t w = threadIdx.x; w < G * kw; w += blockDim.x) {
+    const uint32_t t = w / kw, j = w % kw;
+    const uint8_t* cc = codes_lds + t * D + j * ppw;
+    uint32_t word = 0;
+    for (uint32_t i = 0; i < ppw; ++i) word |= static_cast<uint32_t>(cc[i]) << (bits * i);
+    words[w] = word;
+  }
+}
+
+// ------------------------------------------------------------------ values (native layout)
+// One workgroup per (unit, 64-token block touched). Phase 1: one thread per (token,
+// channel group) computes min/max, (scale, zero) and codes (src/quant.rs:349-375).
+// Phase 2: one thread per channel-major word; words that already hold earlier tokens
+// of the block are read, OR-ed and written back (blocks fill across appends).
+__global__ void __launch_bounds__(kThreads)
+    k_quant_values(CacheView c, RowSource ring, uint32_t n_ring, RowSource in, uint64_t vq0,
+                   uint64_t n, uint64_t blk0, uint32_t nblk) {
+  extern __shared__ uint8_t codes_lds[];  // [64][D]
+  const Geometry& geo = c.geo;
+  const uint32_t G = geo.G, D = geo.D, bits = geo.bits, R = geo.R, ncg = geo.ncg();
+  const float levels = static_cast<float>(geo.levels());
+  const uint32_t unit = blockIdx.x / nblk;
+  const uint64_t tb = blk0 + blockIdx.x % nblk;
+  const uint64_t t_lo = vq0 > tb * kValueBlock ? vq0 : tb * kValueBlock;
+  const uint64_t t_end = vq0 + n;
+  const uint64_t t_hi = t_end < (tb + 1) * kValueBlock ? t_end : (tb + 1) * kValueBlock;
+  const uint32_t ntok = static_cast<uint32_t>(t_hi - t_lo);
+  float2* params = reinterpret_cast<float2*>(c.vparams + unit * geo.vparams_unit());
+  for (uint32_t p = threadIdx.x; p < ntok * ncg; p += blockDim.x) {
+    const uint32_t k = p / ncg, cg = p % ncg;
+    const uint64_t t = t_lo + k;
+    const uint64_t i = t - vq0;
+    const float* row = i < n_ring ? source_row(ring, unit, i, R, D)
+                                  : source_row(in, unit, i - n_ring, R, D);
+    const float* grp = row + cg * G;
+    float mn = INFINITY, mx = -INFINITY;
+    for (uint32_t e = 0; e < G; ++e) {
+      mn = fminf(mn, grp[e]);
+      mx = fmaxf(mx, grp[e]);
+    }
+    const float scale = scale_of(mx - mn, levels);
+    const uint32_t tt = static_cast<uint32_t>(t % kValueBlock);
+    params[(tb * ncg + cg) * kValueBlock + tt] = make_float2(scale, mn);
+    uint8_t* dst = codes_lds + tt * D + cg * G;
+    for (uint32_t e = 0; e < G; ++e) dst[e] = static_cast<uint8_t>(quant_code(grp[e], mn, scale, levels));
+  }
+  __syncthreads();
+  const uint32_t ppw = geo.ppw();
+  const uint32_t vw = geo.vwords_per_channel();
+  const uint32_t w_lo = static_cast<uint32_t>(t_lo % kValueBlock) / ppw;
+  const uint32_t w_hi = static_cast<uint32_t>((t_hi - 1) % kValueBlock) / ppw + 1;
+  const uint32_t nw = w_hi - w_lo;
+  uint32_t* base = c.vcodes + unit * geo.vcodes_unit() + tb * D * vw;
+  for (uint32_t idx = threadIdx.x; idx < D * nw; idx += blockDim.x) {
+    const uint32_t d = idx / nw, w = w_lo + idx % nw;
+    uint32_t word = 0;
+    bool keep_old = false;
+    for (uint32_t i = 0; i < ppw; ++i) {
+      const uint64_t t = tb * kValueBlock + w * ppw + i;
+      if (t >= t_lo && t < t_hi) {
+        word |= static_cast<uint32_t>(codes_lds[(t % kValueBlock) * D + d]) << (bits * i);
+      } else if (t < t_lo) {
+        keep_old = true;
+      }
+    }
+    uint32_t* dst = base + (uint64_t)d * vw + w;
+    if (keep_old) word |= *dst;
+    *dst = word;
+  }
+}
+
+// ------------------------------------------------------------------ export to reference order
+
+// Key words (g*D + d)*ipc + w hold tokens g*G + w*ppw + i of channel d (src/quant.rs:312-323).
+__global__ void __launch_bounds__(kThreads)
+    k_export_keys(CacheView c, uint64_t kq, uint32_t* out) {
+  const Geometry& geo = c.geo;
+  const uint32_t G = geo.G, D = geo.D, bits = geo.bits, ppw = geo.ppw(), kw = geo.kwords_per_token();
+  const uint32_t ipc = G / ppw;
+  const uint32_t mask = geo.levels();
+  const uint64_t per_unit = (kq / G) * D * ipc;
+  const uint64_t total = per_unit * geo.units;
+  for (uint64_t idx = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; idx < total;
+       idx += (uint64_t)gridDim.x * blockDim.x) {
+    const uint32_t unit = idx / per_unit;
+    const uint64_t r = idx % per_unit;
+    const uint32_t w = r % ipc;
+    const uint32_t d = (r / ipc) % D;
+    const uint64_t g = r / ((uint64_t)ipc * D);
+    const uint32_t* src = c.kcodes + unit * geo.kcodes_unit();
+    uint32_t word = 0;
+    for (uint32_t i = 0; i < ppw; ++i) {
+      const uint64_t t = g * G + w * ppw + i;
+      const uint32_t code = (src[t * kw + d / ppw] >> (bits * (d % ppw))) & mask;
+      word |= code << (bits * i);
+    }
+    out[idx] = word;
+  }
+}
+
+// Value words (t*(D/G) + cg)*ipg + w = t*(D/ppw) + j hold channels j*ppw + i of token t
+// (src/quant.rs:362-372); params (t*(D/G) + cg)*2 (src/quant.rs:360-361).
+__global__ void __launch_bounds__(kThreads)
+    k_export_values(CacheView c, uint64_t vq, uint32_t* out_codes, float* out_params) {
+  const Geometry& geo = c.geo;
+  const uint32_t D = geo.D, bits = geo.bits, ppw = geo.ppw(), vw = geo.vwords_per_channel();
+  const uint32_t ncg = geo.ncg();
+  const uint32_t mask = geo.levels();
+  const uint32_t wpt = D / ppw;
+  const uint64_t per_unit = vq * wpt;
+  const uint64_t total = per_unit * geo.units;
+  for (uint64_t idx = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; idx < total;
+       idx += (uint64_t)gridDim.x * blockDim.x) {
+    const uint32_t unit = idx / per_unit;
+    const uint64_t r = idx % per_unit;
+    const uint64_t t = r / wpt;
+    const uint32_t j = r % wpt;
+    const uint64_t tb = t / kValueBlock;
+    const uint32_t tt = t % kValueBlock;
+    const uint32_t* src = c.vcodes + unit * geo.vcodes_unit() + tb * D * vw;
+    uint32_t word = 0;
+    for (uint32_t i = 0; i < ppw; ++i) {
+      const uint32_t d = j * ppw + i;
+      const uint32_t code = (src[(uint64_t)d * vw + tt / ppw] >> (bits * (tt % ppw))) & mask;
+      word |= code << (bits * i);
+    }
+    out_codes[idx] = word;
+    if (out_params != nullptr && j < ncg) {
+      const float2 sz = reinterpret_cast<const float2*>(c.vparams + unit * geo.vparams_unit())
+          [(tb * ncg + j) * kValueBlock + tt];
+      reinterpret_cast<float2*>(out_params)[(unit * vq + t) * ncg + j] = sz;
+    }
+  }
+}
+
+// ------------------------------------------------------------------ dense reconstruction
+
+// KiviCache::dequantize (src/cache.rs:282-325): packed tokens as fma(code, scale, zero)
+// (src/quant.rs:406, 443), residual tokens copied.
+__global__ void __launch_bounds__(kThreads)
+    k_dequant_cache(CacheView c, SeqState s, uint64_t seq, float* keys, float* values) {
+  const Geometry& geo = c.geo;
+  const uint32_t D = geo.D, G = geo.G, R = geo.R, bits = geo.bits, ppw = geo.ppw();
+  const uint32_t kw = geo.kwords_per_token(), vw = geo.vwords_per_channel(), ncg = geo.ncg();
+  const uint32_t mask = geo.levels();
+  const uint64_t per_unit = seq * D;
+  const uint64_t total = per_unit * geo.units;
+  for (uint64_t idx = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; idx < total;
+       idx += (uint64_t)gridDim.x * blockDim.x) {
+    const uint32_t unit = idx / per_unit;
+    const uint64_t r = idx % per_unit;
+    const uint64_t t = r / D;
+    const uint32_t d = r % D;
+    float k, v;
+    if (t < s.kq) {
+      const uint32_t word = c.kcodes[unit * geo.kcodes_unit() + t * kw + d / ppw];
+      const float code = static_cast<float>((word >> (bits * (d % ppw))) & mask);
+      const float2 sz = reinterpret_cast<const float2*>(c.kparams + unit * geo.kparams_unit())[(t / G) * D + d];
+      k = fmaf(code, sz.x, sz.y);
+    } else {
+      k = c.kres[((uint64_t)unit * R + (t - s.kq)) * D + d];
+    }
+    if (t < s.vq) {
+      const uint64_t tb = t / kValueBlock;
+      const uint32_t tt = t % kValueBlock;
+      const uint32_t word = c.vcodes[unit * geo.vcodes_unit() + (tb * D + d) * vw + tt / ppw];
+      const float code = static_cast<float>((word >> (bits * (tt % ppw))) & mask);
+      const float2 sz = reinterpret_cast<const float2*>(c.vparams + unit * geo.vparams_unit())
+          [(tb * ncg + d / G) * kValueBlock + tt];
+      v = fmaf(code, sz.x, sz.y);
+    } else {
+      v = c.vring[((uint64_t)unit * R + (s.vhead + (t - s.vq)) % R) * D + d];
+    }
+    keys[idx] = k;
+    values[idx] = v;
+  }
+}
+
+// ------------------------------------------------------------------ standalone codec (reference order)
+
+// quantize_per_channel (src/quant.rs:153-191 -> append_key_block :275-328), one workgroup per
+// (unit, group), words (g*D + d)*ipc + w.
+__global__ void __launch_bounds__(kThreads)
+    k_quant_ref_keys(const float* data, uint64_t tokens, uint32_t D, uint32_t bits, uint32_t G,
+                     uint32_t* codes, float* params) {
+  extern __shared__ uint8_t codes_lds[];  // [G][D]
+  const uint64_t ngroups = tokens / G;
+  const uint32_t unit = blockIdx.x / ngroups;
+  const uint64_t g = blockIdx.x % ngroups;
+  const float levels = static_cast<float>((1u << bits) - 1u);
+  const float* rows = data + (unit * tokens + g * G) * D;
+  float2* pp = reinterpret_cast<float2*>(params) + (unit * ngroups + g) * D;
+  for (uint32_t d = threadIdx.x; d < D; d += blockDim.x) {
+    float mn = INFINITY, mx = -INFINITY;
+    for (uint32_t t = 0; t < G; ++t) {
+      const float x = rows[(uint64_t)t * D + d];
+      mn = fminf(mn, x);
+      mx = fmaxf(mx, x);
+    }
+    const float scale = scale_of(mx - mn, levels);
+    pp[d] = make_float2(scale, mn);
+    for (uint32_t t = 0; t < G; ++t)
+      codes_lds[t * D + d] = static_cast<uint8_t>(quant_code(rows[(uint64_t)t * D + d], mn, scale, levels));
+  }
+  __syncthreads();
+  const uint32_t ppw = 32 / bits, ipc = G / ppw;
+  uint32_t* out = codes + (unit * ngroups + g) * D * ipc;
+  for (uint32_t idx = threadIdx.x; idx < D * ipc; idx += blockDim.x) {
+    const uint32_t d = idx / ipc, w = idx % ipc;
+    uint32_t word = 0;
+    for (uint32_t i = 0; i < ppw; ++i)
+      word |= static_cast<uint32_t>(codes_lds[(w * ppw + i) * D + d]) << (bits * i);
+    out[idx] = word;
+  }
+}
+
+// quantize_per_token (src/quant.rs:193-233 -> append_value_block :330-377): one thread per
+// (unit, token, channel group) owns its ipg words.
+__global__ void __launch_bounds__(kThreads)
+    k_quant_ref_values(const float* data, uint32_t units, uint64_t tokens, uint32_t D,
+                       uint32_t bits, uint32_t G, uint32_t* codes, float* params) {
+  const uint32_t ncg = D / G, ppw = 32 / bits, ipg = G / ppw;
+  const float levels = static_cast<float>((1u << bits) - 1u);
+  const uint64_t total = (uint64_t)units * tokens * ncg;
+  for (uint64_t idx = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; idx < total;
+       idx += (uint64_t)gridDim.x * blockDim.x) {
+    const float* grp = data + idx * G;  // (unit*tokens + t)*D + cg*G == idx*G
+    float mn = INFINITY, mx = -INFINITY;
+    for (uint32_t e = 0; e < G; ++e) {
+      mn = fminf(mn, grp[e]);
+      mx = fmaxf(mx, grp[e]);
+    }
+    const float scale = scale_of(mx - mn, levels);
+    reinterpret_cast<float2*>(params)[idx] = make_float2(scale, mn);
+    for (uint32_t w = 0; w < ipg; ++w) {
+      uint32_t word = 0;
+      for (uint32_t i = 0; i < ppw; ++i)
+        word |= quant_code(grp[w * ppw + i], mn, scale, levels) << (bits * i);
+      codes[idx * ipg + w] = word;
+    }
+  }
+}
+
+// QuantizedTensor::dequantize (src/quant.rs:124-150 via dequant_keys/values :379-451).
+__global__ void __launch_bounds__(kThreads)
+    k_dequant_ref(const uint32_t* codes, const float* params, uint32_t units, uint64_t tokens,
+                  uint32_t D, uint32_t bits, uint32_t G, int per_channel, float* out) {
+  const uint32_t ppw = 32 / bits, mask = (1u << bits) - 1u, ncg = D / G, ipg = G / ppw;
+  const uint64_t total = (uint64_t)units * tokens * D;
+  for (uint64_t idx = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; idx < total;
+       idx += (uint64_t)gridDim.x * blockDim.x) {
+    const uint64_t ut = idx / D;  // unit*tokens + t
+    const uint32_t d = idx % D;
+    const uint32_t unit = ut / tokens;
+    const uint64_t t = ut % tokens;
+    uint32_t word, shift;
+    float2 sz;
+    if (per_channel) {
+      const uint64_t g = t / G;
+      const uint32_t tg = t % G;
+      const uint64_t base = (unit * (tokens / G) + g) * D + d;  // (g*D + d) within the unit
+      word = codes[base * ipg + tg / ppw];
+      shift = bits * (tg % ppw);
+      sz = reinterpret_cast<const float2*>(params)[base];
+    } else {
+      const uint64_t gi = ut * ncg + d / G;
+      word = codes[gi * ipg + (d % G) / ppw];
+      shift = bits * (d % ppw);
+      sz = reinterpret_cast<const float2*>(params)[gi];
+    }
+    out[idx] = fmaf(static_cast<float>((word >> shift) & mask), sz.x, sz.y);
+  }
+}
+
+// QuantizedTensor::pytorch_codes for keys (src/quant.rs:81-94): out[tp][d] = word (g, d, w)
+// with tp = g*ipc + w. Values are already in that order (src/quant.rs:95-109).
+__global__ void __launch_bounds__(kThreads)
+    k_pytorch_keys(const uint32_t* codes, uint32_t units, uint64_t tokens, uint32_t D, uint32_t bits,
+                   uint32_t G, uint32_t* out) {
+  const uint32_t ppw = 32 / bits, ipc = G / ppw;
+  const uint64_t t_pack = tokens / ppw;
+  const uint64_t total = (uint64_t)units * t_pack * D;
+  for (uint64_t idx = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; idx < total;
+       idx += (uint64_t)gridDim.x * blockDim.x) {
+    const uint64_t ut = idx / D;
+    const uint32_t d = idx % D;
+    const uint32_t unit = ut / t_pack;
+    const uint64_t tp = ut % t_pack;
+    const uint64_t g = tp / ipc;
+    const uint32_t w = tp % ipc;
+    out[idx] = codes[unit * (t_pack * D) + (g * D + d) * ipc + w];
+  }
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------ launchers
+
+hipError_t launch_copy_rows(const Geometry& g, RowSource src, float* dst, uint32_t dst_slot,
+                            uint32_t count, hipStream_t stream) {
+  if (count == 0) return hipSuccess;
+  const bool vec = (reinterpret_cast<uintptr_t>(src.base) % 16 == 0) &&
+                   (reinterpret_cast<uintptr_t>(dst) % 16 == 0) && (g.D % 4 == 0) &&
+                   (src.stride_unit % 4 == 0);
+  if (vec) {
+    const uint64_t work = (uint64_t)g.units * count * (g.D / 4);
+    k_copy_rows<4><<<grid_for(work), kThreads, 0, stream>>>(src, dst, g.R, g.D, g.units, dst_slot, count);
+  } else {
+    const uint64_t work = (uint64_t)g.units * count * g.D;
+    k_copy_rows<1><<<grid_for(work), kThreads, 0, stream>>>(src, dst, g.R, g.D, g.units, dst_slot, count);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_quant_keys(const CacheView& c, RowSource src, uint64_t g0, uint32_t ngroups,
+                             hipStream_t stream) {
+  if (ngroups == 0) return hipSuccess;
+  const uint64_t blocks = (uint64_t)c.geo.units * ngroups;
+  const size_t lds = (size_t)c.geo.G * c.geo.D;
+  k_quant_keys<<<static_cast<unsigned>(blocks), kThreads, lds, stream>>>(c, src, g0, ngroups);
+  return hipGetLastError();
+}
+
+hipError_t launch_quant_values(const CacheView& c, RowSource ring, uint32_t n_ring, RowSource in,
+                               uint64_t n_in, uint64_t vq0, hipStream_t stream) {
+  const uint64_t n = n_ring + n_in;
+  if (n == 0) return hipSuccess;
+  const uint64_t blk0 = vq0 / kValueBlock;
+  const uint64_t blk1 = (vq0 + n - 1) / kValueBlock;
+  const uint32_t nblk = static_cast<uint32_t>(blk1 - blk0 + 1);
+  const uint64_t blocks = (uint64_t)c.geo.units * nblk;
+  const size_t lds = (size_t)kValueBlock * c.geo.D;
+  k_quant_values<<<static_cast<unsigned>(blocks), kThreads, lds, stream>>>(c, ring, n_ring, in, vq0, n,
+                                                                         blk0, nblk);
+  return hipGetLastError();
+}
+
+hipError_t launch_export_keys(const CacheView& c, uint64_t kq, uint32_t* codes, float* params,
+                              hipStream_t stream) {
+  const Geometry& g = c.geo;
+  if (kq == 0) return hipSuccess;
+  if (codes != nullptr) {
+    const uint64_t work = (uint64_t)g.units * kq * g.D / g.ppw();
+    k_export_keys<<<grid_for(work), kThreads, 0, stream>>>(c, kq, codes);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  if (params != nullptr) {
+    const size_t bytes = (kq / g.G) * g.D * 2 * sizeof(float);
+    return copy_units(params, bytes, c.kparams, g.kparams_unit() * sizeof(float), bytes, g.units, stream);
+  }
+  return hipSuccess;
+}
+
+hipError_t launch_export_values(const CacheView& c, uint64_t vq, uint32_t* codes, float* params,
+                                hipStream_t stream) {
+  const Geometry& g = c.geo;
+  if (vq == 0) return hipSuccess;
+  // Codes and params come out of one pass; a null codes array still needs the pass.
+  uint32_t* tmp = nullptr;
+  if (codes == nullptr) {
+    if (params == nullptr) return hipSuccess;
+    hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&tmp), g.units * vq * (g.D / g.ppw()) * 4, stream);
+    if (e != hipSuccess) return e;
+    codes = tmp;
+  }
+  const uint64_t work = (uint64_t)g.units * vq * (g.D / g.ppw());
+  k_export_values<<<grid_for(work), kThreads, 0, stream>>>(c, vq, codes, params);
+  hipError_t e = hipGetLastError();
+  if (tmp != nullptr) {
+    hipError_t f = hipFreeAsync(tmp, stream);
+    if (e == hipSuccess) e = f;
+  }
+  return e;
+}
+
+hipError_t launch_dequant_cache(const CacheView& c, const SeqState& s, float* keys, float* values,
+                                hipStream_t stream) {
+  const uint64_t seq = s.kq + s.kres;
+  const uint64_t work = (uint64_t)c.geo.units * seq * c.geo.D;
+  if (work == 0) return hipSuccess;
+  k_dequant_cache<<<grid_for(work), kThreads, 0, stream>>>(c, s, seq, keys, values);
+  return hipGetLastError();
+}
+
+hipError_t copy_units(void* dst, size_t dst_pitch, const void* src, size_t src_pitch, size_t bytes,
+                      uint32_t units, hipStream_t stream) {
+  if (bytes == 0 || units == 0) return hipSuccess;
+  return hipMemcpy2DAsync(dst, dst_pitch, src, src_pitch, bytes, units, hipMemcpyDeviceToDevice,
+                          stream);
+}
+
+hipError_t launch_quant_ref_keys(const float* data, uint32_t units, uint64_t tokens, uint32_t D,
+                                 uint32_t bits, uint32_t G, uint32_t* codes, float* params,
+                                 hipStream_t stream) {
+  const uint64_t blocks = (uint64_t)units * (tokens / G);
+  if (blocks == 0) return hipSuccess;
+  k_quant_ref_keys<<<static_cast<unsigned>(blocks), kThreads, (size_t)G * D, stream>>>(
+      data, tokens, D, bits, G, codes, params);
+  return hipGetLastError();
+}
+
+hipError_t launch_quant_ref_values(const float* data, uint32_t units, uint64_t tokens, uint32_t D,
+                                   uint32_t bits, uint32_t G, uint32_t* codes, float* params,
+                                   hipStream_t stream) {
+  const uint64_t work = (uint64_t)units * tokens * (D / G);
+  if (work == 0) return hipSuccess;
+  k_quant_ref_values<<<grid_for(work), kThreads, 0, stream>>>(data, units, tokens, D, bits, G, codes, params);
+  return hipGetLastError();
+}
+
+hipError_t launch_dequant_ref(const uint32_t* codes, const float* params, uint32_t units,
+                              uint64_t tokens, uint32_t D, uint32_t bits, uint32_t G,
+                              int per_channel, float* out, hipStream_t stream) {
+  const uint64_t work = (uint64_t)units * tokens * D;
+  if (work == 0) return hipSuccess;
+  k_dequant_ref<<<grid_for(work), kThreads, 0, stream>>>(codes, params, units, tokens, D, bits, G,
+                                                        per_channel, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_pytorch_order(const uint32_t* codes, uint32_t units, uint64_t tokens, uint32_t D,
+                                uint32_t bits, uint32_t G, int per_channel, uint32_t* out,
+                                hipStream_t stream) {
+  const uint64_t words = (uint64_t)units * tokens * D / (32 / bits);
+  if (words == 0) return hipSuccess;
+  if (!per_channel)
+    return hipMemcpyAsync(out, codes, words * 4, hipMemcpyDeviceToDevice, stream);
+  k_pytorch_keys<<<grid_for(words), kThreads, 0, stream>>>(codes, units, tokens, D, bits, G, out);
+  return hipGetLastError();
+}
+
+}  // namespace kivi

@@ -1,0 +1,186 @@
+"""Parity of the HIP library with the oracle on identical seeded inputs (``-m gpu``).
+
+* Packed codes and (scale, zero) values: bit-exact, compared in the reference's PackedStream
+  order (kivi_cache_export_streams) after every append of a randomized append schedule.
+* Dense reconstruction (dequantize): bit-exact.
+* Attention: |got - oracle| <= ATOL + RTOL*|oracle| with the north-star tolerance
+  (max-abs 1e-3, relative 1e-4 in f32), and within the reference's own 1e-4 of an f64
+  dense brute force on the dequantized cache (tests/attention.rs:59).
+"""
+
+import numpy as np
+import pytest
+
+import kivi
+from kivi import KiviCache, KiviConfig, RuntimeKv
+from helpers import dense_attend, fill, max_abs
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 1e-3, 1e-4
+
+
+def assert_close(got, want, what=""):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    bound = ATOL + RTOL * np.abs(want)
+    bad = np.abs(got - want) > bound
+    assert not bad.any(), f"{what}: {bad.sum()} elements beyond tolerance, max err {max_abs(got, want):.3g}"
+
+
+def assert_same_state(a, o):
+    assert a.sequence_length() == o.sequence_length()
+    assert a.quantized_key_tokens() == o.quantized_key_tokens()
+    assert a.quantized_value_tokens() == o.quantized_value_tokens()
+    assert a.key_residual_len() == o.key_residual_len()
+    assert a.value_residual_len() == o.value_residual_len()
+    ma, mo = a.memory(), o.memory()
+    for f, _ in kivi._MemoryReport._fields_:
+        assert getattr(ma, f) == getattr(mo, f), f
+
+
+def assert_streams_equal(a, o):
+    for x, y, name in zip(a.export_streams(), o.export_streams(),
+                          ("key codes", "key params", "value codes", "value params")):
+        assert x.shape == y.shape, name
+        if x.dtype == np.float32:
+            assert np.array_equal(x.view(np.uint32), y.view(np.uint32)), name
+        else:
+            assert np.array_equal(x, y), name
+
+
+SCHEDULES = {
+    "decode": [5] + [1] * 70,
+    "chunks": [1, 50, 7, 12, 200, 3, 64, 1, 1, 130],
+    "bulk": [333],
+    "exact_r": [64, 64, 32, 32, 1],
+}
+
+
+@pytest.mark.parametrize("bits", [2, 4, 8])
+@pytest.mark.parametrize("group,residual,dim", [(32, 64, 128), (16, 32, 32), (32, 32, 64),
+                                               (64, 128, 128)])
+@pytest.mark.parametrize("schedule", list(SCHEDULES))
+def test_streaming_cache_parity(amd, oracle, bits, group, residual, dim, schedule):
+    if group * bits % 32:
+        pytest.skip("invalid group for bits")
+    chunks = SCHEDULES[schedule]
+    batch, heads, qh = 2, 2, 4
+    total = sum(chunks)
+    rng = np.random.default_rng(1000 * bits + group + dim)
+    keys = rng.standard_normal(batch * heads * total * dim).astype(np.float32)
+    keys.reshape(batch, heads, total, dim)[:, :, :, 3] *= 10  # outlier channel
+    values = rng.standard_normal(batch * heads * total * dim).astype(np.float32)
+    cfg = KiviConfig(bits, group, residual)
+    a = KiviCache(amd, cfg, batch, heads, dim)
+    o = KiviCache(oracle, cfg, batch, heads, dim)
+    off = 0
+    for step, n in enumerate(chunks):
+        k = keys.reshape(batch, heads, total, dim)[:, :, off:off + n].copy()
+        v = values.reshape(batch, heads, total, dim)[:, :, off:off + n].copy()
+        a.append(k, v, n)
+        o.append(k, v, n)
+        off += n
+        assert_same_state(a, o)
+        if step % 7 == 0 or step == len(chunks) - 1:
+            assert_streams_equal(a, o)
+            q = rng.standard_normal(batch * qh * dim).astype(np.float32)
+            scale = np.float32(1.0) / np.sqrt(np.float32(dim))
+            assert_close(a.attention(q, qh, scale), o.attention(q, qh, scale), f"step {step}")
+    ka, va = a.dequantize()
+    ko, vo = o.dequantize()
+    assert np.array_equal(ka.view(np.uint32), ko.view(np.uint32))
+    assert np.array_equal(va.view(np.uint32), vo.view(np.uint32))
+
+
+@pytest.mark.parametrize("bits", [2, 4, 8])
+@pytest.mark.parametrize("gqa", [1, 4, 8])
+def test_attention_parity_long(amd, oracle, bits, gqa):
+    """Several thousand tokens, many splits, every GQA grouping the configs use."""
+    batch, heads, dim, seq = 1, 2, 128, 3000 + 17 * bits
+    rng = np.random.default_rng(bits * 10 + gqa)
+    k = rng.standard_normal(batch * heads * seq * dim).astype(np.float32)
+    v = rng.standard_normal(batch * heads * seq * dim).astype(np.float32)
+    cfg = KiviConfig(bits, 32, 128)
+    a = KiviCache(amd, cfg, batch, heads, dim)
+    o = KiviCache(oracle, cfg, batch, heads, dim)
+    a.append(k, v, seq)
+    o.append(k, v, seq)
+    assert_streams_equal(a, o)
+    q = rng.standard_normal(batch * heads * gqa * dim).astype(np.float32)
+    scale = np.float32(1 / np.sqrt(128))
+    got = a.attention(q, heads * gqa, scale)
+    assert_close(got, o.attention(q, heads * gqa, scale))
+    kh, vh = a.dequantize()
+    assert max_abs(got, dense_attend(kh, vh, q, batch, heads, heads * gqa, seq, dim, scale)) < 1e-4
+
+
+@pytest.mark.parametrize("bits,group", [(2, 32), (4, 32), (8, 32), (2, 16), (4, 64), (8, 4)])
+@pytest.mark.parametrize("dim", [32, 128])
+def test_standalone_quantize_parity(amd, oracle, bits, group, dim):
+    if dim % group:
+        pytest.skip("head_dim not a multiple of group")
+    batch, heads, tokens = 2, 3, 4 * group
+    data = fill(batch * heads * tokens * dim, bits * 7 + group)
+    data[::97] = 0.5  # half ties
+    for fn in (kivi.quantize_per_channel, kivi.quantize_per_token):
+        qa = fn(amd, data, batch, heads, tokens, dim, bits, group)
+        qo = fn(oracle, data, batch, heads, tokens, dim, bits, group)
+        assert np.array_equal(qa.codes(), qo.codes())
+        assert np.array_equal(qa.scale_zero().view(np.uint32), qo.scale_zero().view(np.uint32))
+        assert np.array_equal(qa.pytorch_codes(), qo.pytorch_codes())
+        assert np.array_equal(qa.dequantize().view(np.uint32), qo.dequantize().view(np.uint32))
+        assert (qa.code_bytes(), qa.metadata_bytes()) == (qo.code_bytes(), qo.metadata_bytes())
+
+
+def test_session_parity(amd, oracle):
+    """Prefix + private suffixes (src/prefix.rs:173-289) against the oracle."""
+    batch, heads, dim, doc, qh = 2, 2, 64, 700, 8
+    rng = np.random.default_rng(7)
+    k = rng.standard_normal(batch * heads * doc * dim).astype(np.float32)
+    v = rng.standard_normal(batch * heads * doc * dim).astype(np.float32)
+    cfg = KiviConfig(2, 32, 128)
+    ca, co = KiviCache(amd, cfg, batch, heads, dim), KiviCache(oracle, cfg, batch, heads, dim)
+    ca.append(k, v, doc)
+    co.append(k, v, doc)
+    pa, po = ca.share_prefix(), co.share_prefix()
+    assert pa.prefix_bytes() == po.prefix_bytes()
+    sa, so = pa.session(), po.session()
+    for n in (3, 1, 40):
+        sk = rng.standard_normal(batch * heads * n * dim).astype(np.float32)
+        sv = rng.standard_normal(batch * heads * n * dim).astype(np.float32)
+        sa.append(sk, sv, n)
+        so.append(sk, sv, n)
+        q = rng.standard_normal(batch * qh * dim).astype(np.float32)
+        assert_close(sa.attention(q, qh, 0.125), so.attention(q, qh, 0.125))
+    # batched entry point == per-session calls
+    sessions_a = [pa.session() for _ in range(5)]
+    for i, s in enumerate(sessions_a):
+        n = 1 + 7 * i
+        s.append(rng.standard_normal(batch * heads * n * dim).astype(np.float32),
+                 rng.standard_normal(batch * heads * n * dim).astype(np.float32), n)
+    qs = rng.standard_normal(5 * batch * qh * dim).astype(np.float32)
+    batched = kivi.sessions_attention(amd, sessions_a, qs, qh, 0.125)
+    per = np.concatenate([s.attention(qs[i * batch * qh * dim:(i + 1) * batch * qh * dim], qh, 0.125)
+                          for i, s in enumerate(sessions_a)])
+    assert_close(batched, per)
+
+
+def test_runtime_decode_parity(amd, oracle):
+    """512-step streaming decode shape of config 1, scaled down: prefill, then decode steps
+    crossing key flushes and window evictions, compared with the oracle each step."""
+    heads, qh, dim, prefill, steps = 8, 32, 128, 640, 140
+    cfg = KiviConfig(2, 32, 128)
+    rng = np.random.default_rng(11)
+    ra, ro = RuntimeKv(amd, cfg, 1, heads, dim), RuntimeKv(oracle, cfg, 1, heads, dim)
+    k = rng.standard_normal(heads * prefill * dim).astype(np.float32)
+    v = rng.standard_normal(heads * prefill * dim).astype(np.float32)
+    ra.prefill(k, v, prefill)
+    ro.prefill(k, v, prefill)
+    scale = np.float32(1 / np.sqrt(128))
+    for step in range(steps):
+        kk = rng.standard_normal(heads * dim).astype(np.float32)
+        vv = rng.standard_normal(heads * dim).astype(np.float32)
+        q = rng.standard_normal(qh * dim).astype(np.float32)
+        assert_close(ra.decode(kk, vv, q, qh, scale), ro.decode(kk, vv, q, qh, scale), f"step {step}")
+    assert_streams_equal(ra.cache(), ro.cache())
