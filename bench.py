@@ -9,7 +9,16 @@ tokens/s = 16 * steps / time. The cache build (prefill quantization) is timed on
 reported as quantize GB/s. The CPU baseline is the oracle (C++ restatement of the
 reference CPU path, 1 core) on one of the 16 sequences.
 
+The roofline object is for the dominant kernel (the packed-chunk attention kernel): its
+algorithmic bytes per launch (packed codes + (scale, zero) of the chunks it covers, plus the
+query) over its mean launch duration, both measured live by the library's HIP-event launch
+timing (kivi_timing_*) on the launch stream during the timed region. `traffic` is the HBM
+bytes per launch of that kernel from rocprofv3 FETCH_SIZE + WRITE_SIZE runs, calibrated on a
+plain copy kernel (--copy-calibration), as recorded in profiles/traffic.json; null when no
+record matches this kernel, workload and byte count.
+
 Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--config c2] [--no-cpu]
+                       [--copy-calibration MIB]
 """
 
 import argparse
@@ -109,6 +118,21 @@ def _cpu_model():
     return "unknown"
 
 
+def recorded_traffic(kernel, workload, bytes_per_launch):
+    """HBM bytes per launch of `kernel` on `workload` from profiles/traffic.json, if that
+    record was measured at the same algorithmic bytes per launch."""
+    path = ROOT / "profiles" / "traffic.json"
+    try:
+        records = json.loads(path.read_text())
+    except (OSError, ValueError):
+        return None
+    for r in records.get("records", []):
+        if (r.get("kernel") == kernel and r.get("workload") == workload
+                and abs(r.get("algorithmic_bytes_per_launch", -1) - bytes_per_launch) < 1.0):
+            return r
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -116,6 +140,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="after the timed region, copy MIB MiB device-to-device 3 times (a plain "
+                         "copy kernel of known size for calibrating rocprofv3 byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus "
@@ -139,14 +166,22 @@ def main():
     cache = kivi.KiviCache(amd, kivi.KiviConfig(bits, G, R), batch, heads, dim)
     cache.reserve(seq)
     torch.cuda.synchronize()
-    # Prefill quantization, timed once on the library's stream.
+    # Prefill quantization, timed once on the library's stream (whole append, and per
+    # quantize kernel with the library's launch timing).
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    kivi.timing_enable(amd, True)
     with torch.cuda.stream(stream):
         e0.record(stream)
         cache.append_device(k.data_ptr(), k.numel(), v.data_ptr(), v.numel(), seq, sp)
         e1.record(stream)
     stream.synchronize()
     t_quant = e0.elapsed_time(e1) / 1e3
+    quant_kernels = {}
+    for fam in ("quant_keys", "quant_values"):
+        n, ms, by = kivi.timing_read(amd, fam)
+        if n:
+            quant_kernels[fam] = {"launches": n, "ms": ms, "gbps": by / (ms / 1e3) / 1e9}
+    kivi.timing_enable(amd, False)
     mem = cache.memory()
     quant_bytes = 2 * k.numel() * 4 + mem.compressed_bytes()
     log(f"[bench] prefill quantize {quant_bytes / t_quant / 1e9:.1f} GB/s ({t_quant * 1e3:.2f} ms)")
@@ -164,21 +199,68 @@ def main():
             step()
     stream.synchronize()
     torch.cuda.synchronize()
-    t_start = torch.cuda.Event(enable_timing=True)
-    t_end = torch.cuda.Event(enable_timing=True)
-    with torch.cuda.stream(stream):
-        t_start.record(stream)
-        for _ in range(args.steps):
-            step()
-        t_end.record(stream)
-    stream.synchronize()
-    torch.cuda.synchronize()
-    per_step = t_start.elapsed_time(t_end) / 1e3 / args.steps
+    def timed_steps():
+        t_start = torch.cuda.Event(enable_timing=True)
+        t_end = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            t_start.record(stream)
+            for _ in range(args.steps):
+                step()
+            t_end.record(stream)
+        stream.synchronize()
+        torch.cuda.synchronize()
+        return t_start.elapsed_time(t_end) / 1e3 / args.steps
+
+    # Timed region 1: the K steps as they run in service (no per-launch events).
+    per_step = timed_steps()
+    # Timed region 2: the same K steps with the library's per-launch HIP events, for the
+    # per-kernel durations (the event records add a few microseconds between launches).
+    kivi.timing_enable(amd, True)
+    per_step_evented = timed_steps()
+    kernels = {}
+    for fam in ("attn_packed", "attn_tail", "attn_merge"):
+        n, ms, by = kivi.timing_read(amd, fam)
+        if n:
+            kernels[fam] = {"launches": n, "mean_us": ms * 1e3 / n, "bytes_per_launch": by / n,
+                            "gbps": by / (ms / 1e3) / 1e9}
+    kivi.timing_enable(amd, False)
+    log(f"[bench] timed region with per-launch events: {per_step_evented * 1e6:.1f} us/step")
+    for fam, r in kernels.items():
+        log(f"[bench] {fam}: {r['mean_us']:.1f} us/launch, {r['bytes_per_launch'] / 1e6:.2f} MB, "
+            f"{r['gbps']:.0f} GB/s")
+    if args.copy_calibration > 0:
+        n = args.copy_calibration * (1 << 20) // 4
+        src = torch.ones(n, device="cuda", dtype=torch.float32)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"[bench] copy calibration: 3 x {args.copy_calibration} MiB device copies")
+        del src, dst
     algo_bytes = mem.compressed_bytes() + 2 * out.numel() * 4  # KV bytes + query + output
     eff_gbps = algo_bytes / per_step / 1e9
     tokens_per_s = batch / per_step
     log(f"[bench] attention {per_step * 1e6:.1f} us/step, {eff_gbps:.0f} GB/s effective")
 
+    dom = kernels.get("attn_packed") or kernels.get("attn_tail")
+    dom_name = "k_attn_mfma" if "attn_packed" in kernels else "k_attn_generic"
+    achieved = dom["gbps"] if dom else eff_gbps
+    rec = recorded_traffic(dom_name, args.config, dom["bytes_per_launch"]) if dom else None
+    roofline = {
+        "bound": "hbm",
+        "achieved": achieved,
+        "peak": HBM_PEAK_GBPS,
+        "unit": "GB/s",
+        "frac": achieved / HBM_PEAK_GBPS,
+        "traffic": rec["hbm_bytes_per_launch"] if rec else None,
+        "kernel": dom_name,
+        "algorithmic_bytes_per_launch": dom["bytes_per_launch"] if dom else algo_bytes,
+        "mean_launch_us": dom["mean_us"] if dom else per_step * 1e6,
+        "timing": "HIP events around each launch on its stream (kivi_timing_*), second timed "
+                  "region of the same steps",
+        "traffic_source": rec["source"] if rec else None,
+    }
     result = {
         "metric": METRIC,
         "value": tokens_per_s,
@@ -198,16 +280,9 @@ def main():
         "effective_hbm_gbps": eff_gbps,
         "hbm_fraction": eff_gbps / HBM_PEAK_GBPS,
         "quantize_gbps": quant_bytes / t_quant / 1e9,
-        "roofline": {
-            "bound": "hbm",
-            "achieved": eff_gbps,
-            "peak": HBM_PEAK_GBPS,
-            "unit": "GB/s",
-            "frac": eff_gbps / HBM_PEAK_GBPS,
-            "traffic": None,
-            "algorithmic_bytes": algo_bytes,
-            "kernel": "attention step (split kernel + merge), HIP events on the launch stream",
-        },
+        "roofline": roofline,
+        "kernels": kernels,
+        "quantize_kernels": quant_kernels,
     }
     if not args.no_cpu:
         log("[bench] CPU baseline (oracle, 1 thread) ...")

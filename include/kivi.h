@@ -338,6 +338,34 @@ int32_t kivi_abi_version(void);
 /* Number of usable HIP devices (0 when none); never fails. */
 int32_t kivi_device_count(void);
 
+/* ---------------------------------------------------------------- kernel timing
+ * Measurement hooks for benchmark harnesses; no counterpart in the reference, whose path
+ * runs on the CPU. While enabled, every launch of a timed kernel family is bracketed by a
+ * pair of HIP events on its launch stream and the launch's algorithmic bytes are recorded:
+ * the packed and fp32 KV bytes plus the query bytes an attention launch must read, the
+ * partials read and outputs written by the merge, and the fp32 rows read plus codes and
+ * (scale, zero) written by a quantize launch. kivi_timing_read waits for the pending
+ * events and returns the totals since the last kivi_timing_enable call. */
+typedef enum kivi_kernel_family {
+  KIVI_KERNEL_ATTN_PACKED = 0,  /* attention over 64-token chunks with packed keys and values */
+  KIVI_KERNEL_ATTN_TAIL = 1,    /* attention over the rest: windows, residuals, suffixes */
+  KIVI_KERNEL_ATTN_MERGE = 2,   /* log-sum-exp merge of the split partials */
+  KIVI_KERNEL_QUANT_KEYS = 3,   /* per-channel key quantization into the cache */
+  KIVI_KERNEL_QUANT_VALUES = 4, /* per-token value quantization into the cache */
+  KIVI_KERNEL_FAMILIES = 5
+} kivi_kernel_family;
+
+typedef struct kivi_kernel_timing {
+  uint64_t launches;
+  double total_ms;  /* sum of launch durations */
+  double bytes;     /* sum of algorithmic bytes */
+} kivi_kernel_timing;
+
+/* Enable (non-zero) or disable timing; either way the totals are reset. */
+void kivi_timing_enable(int32_t enable);
+/* Totals of one kernel family (kivi_kernel_family). */
+kivi_status kivi_timing_read(int32_t family, kivi_kernel_timing* out, kivi_error* err);
+
 #ifdef __cplusplus
 }
 #endif

@@ -84,6 +84,25 @@ struct RowSource {
   uint32_t ring;         // 1: slot = (offset + i) % R
 };
 
+// ---------------------------------------------------------------- launch timing (timing.cpp)
+// Brackets the launches made during its lifetime with HIP events on `stream` when timing
+// is enabled (kivi_timing_enable); `family` is a kivi_kernel_family, `bytes` the
+// algorithmic bytes of the launch.
+class TimedLaunch {
+ public:
+  TimedLaunch(int family, hipStream_t stream, double bytes);
+  ~TimedLaunch();
+  TimedLaunch(const TimedLaunch&) = delete;
+  TimedLaunch& operator=(const TimedLaunch&) = delete;
+
+ private:
+  int family_;
+  hipStream_t stream_;
+  double bytes_;
+  int device_ = 0;
+  hipEvent_t start_ = nullptr, end_ = nullptr;
+};
+
 // ---------------------------------------------------------------- launches (kernels_quant.hip)
 // All return hipSuccess or the launch error; all enqueue on `stream`.
 

@@ -23,6 +23,7 @@
 //    thread per token in the reference's operation order (recon = fma(code, scale, zero);
 //    logit = fma(recon, q, logit), channels ascending, src/attention.rs:143-177, 289-300).
 #include "common.hpp"
+#include "kivi.h"
 
 #include <algorithm>
 
@@ -751,18 +752,36 @@ size_t attention_workspace_floats(const AttnProblem& p) {
 hipError_t launch_attention(const AttnProblem& p, float* workspace, hipStream_t stream) {
   const AttnArgs a = make_args(p, workspace);
   if (a.total == 0) return hipSuccess;
-  const uint32_t units = p.cache.geo.units;
+  const Geometry& g = p.cache.geo;
+  const uint32_t units = g.units;
+  // algorithmic bytes per token of one unit: packed codes + (scale, zero), or fp32 rows
+  const double key_tok = g.D * g.bits / 8.0 + g.D * 8.0 / g.G;
+  const double val_tok = g.D * g.bits / 8.0 + g.ncg() * 8.0;
+  const double row = g.D * 4.0;
+  const double q_bytes = (double)units * a.gq * g.D * 4.0;
   if (a.nsplit_fast > 0) {
+    const double tokens = (double)(a.chunk_end - a.chunk_begin) * 64;
+    TimedLaunch timed(KIVI_KERNEL_ATTN_PACKED, stream, units * tokens * (key_tok + val_tok) + q_bytes);
     hipError_t e = dispatch_fast(a, stream);
     if (e != hipSuccess) return e;
   }
   if (a.nsplit_gen > 0) {
+    const uint64_t t0 = a.t_begin, kq = p.st.kq, vq = p.st.vq;
+    const double kp = kq > t0 ? (double)(kq - t0) : 0.0, vp = vq > t0 ? (double)(vq - t0) : 0.0;
+    const double kd = (double)(p.seq - std::max(kq, t0)), vd = (double)(p.seq - std::max(vq, t0));
+    const double bytes =
+        units * (kp * key_tok + vp * val_tok + (kd + vd + 2.0 * p.suffix_len) * row) + q_bytes;
+    TimedLaunch timed(KIVI_KERNEL_ATTN_TAIL, stream, bytes);
     hipError_t e = dispatch_generic(a, fast_eligible(p), stream);
     if (e != hipSuccess) return e;
   }
   const size_t merge_lds = ((size_t)a.nsplit_total + 8) * sizeof(float);
-  k_attn_merge<<<units * a.gq, kThreads, merge_lds, stream>>>(workspace, a.nsplit_total, a.gq,
-                                                              p.cache.geo.D, p.heads, p.qh, p.out);
+  {
+    const double bytes = (double)units * a.gq * ((double)a.nsplit_total * (g.D + 2) + g.D) * 4.0;
+    TimedLaunch timed(KIVI_KERNEL_ATTN_MERGE, stream, bytes);
+    k_attn_merge<<<units * a.gq, kThreads, merge_lds, stream>>>(workspace, a.nsplit_total, a.gq,
+                                                                g.D, p.heads, p.qh, p.out);
+  }
   return hipGetLastError();
 }
 

@@ -7,6 +7,7 @@
 // even, equal to the reference's floor-based rounding for every finite input). min/max are
 // order independent, so the reduction order is free.
 #include "common.hpp"
+#include "kivi.h"
 
 namespace kivi {
 namespace {
@@ -416,6 +417,9 @@ hipError_t launch_quant_keys(const CacheView& c, RowSource src, uint64_t g0, uin
   if (ngroups == 0) return hipSuccess;
   const uint64_t blocks = (uint64_t)c.geo.units * ngroups;
   const size_t lds = (size_t)c.geo.G * c.geo.D;
+  const double rows = (double)blocks * c.geo.G;
+  TimedLaunch timed(KIVI_KERNEL_QUANT_KEYS, stream,
+                    rows * c.geo.D * (4.0 + c.geo.bits / 8.0) + (double)blocks * c.geo.D * 8.0);
   k_quant_keys<<<static_cast<unsigned>(blocks), kThreads, lds, stream>>>(c, src, g0, ngroups);
   return hipGetLastError();
 }
@@ -429,6 +433,9 @@ hipError_t launch_quant_values(const CacheView& c, RowSource ring, uint32_t n_ri
   const uint32_t nblk = static_cast<uint32_t>(blk1 - blk0 + 1);
   const uint64_t blocks = (uint64_t)c.geo.units * nblk;
   const size_t lds = (size_t)kValueBlock * c.geo.D;
+  const double rows = (double)c.geo.units * n;
+  TimedLaunch timed(KIVI_KERNEL_QUANT_VALUES, stream,
+                    rows * (c.geo.D * (4.0 + c.geo.bits / 8.0) + c.geo.ncg() * 8.0));
   k_quant_values<<<static_cast<unsigned>(blocks), kThreads, lds, stream>>>(c, ring, n_ring, in, vq0, n,
                                                                          blk0, nblk);
   return hipGetLastError();

@@ -60,6 +60,10 @@ class _MemoryReport(C.Structure):
     ]
 
 
+class _KernelTiming(C.Structure):
+    _fields_ = [("launches", C.c_uint64), ("total_ms", C.c_double), ("bytes", C.c_double)]
+
+
 class _Footprint(C.Structure):
     _fields_ = [
         (n, C.c_size_t)
@@ -228,6 +232,8 @@ _SIGS = {
 # Entry points only the HIP library has (device pointers, streams, device queries).
 _DEVICE_SIGS = {
     "device_count": (C.c_int32, []),
+    "timing_enable": (None, [C.c_int32]),
+    "timing_read": (C.c_int, [C.c_int32, C.POINTER(_KernelTiming), _ERRP]),
     "status_name": (C.c_char_p, [C.c_int32]),
     "cache_set_stream": (C.c_int, [_P, _P, _ERRP]),
     "cache_append_device": (C.c_int, [_P, _P, _SZ, _P, _SZ, _SZ, _P, _ERRP]),
@@ -585,6 +591,24 @@ class RagSession:
         return out
 
 
+# kivi_kernel_family (include/kivi.h)
+KERNEL_FAMILIES = {"attn_packed": 0, "attn_tail": 1, "attn_merge": 2, "quant_keys": 3,
+                   "quant_values": 4}
+
+
+def timing_enable(backend, on=True):
+    """Start (or stop) per-launch HIP-event timing of the library's kernels; resets totals."""
+    backend["timing_enable"](1 if on else 0)
+
+
+def timing_read(backend, family):
+    """(launches, total_ms, algorithmic bytes) of one kernel family since timing_enable."""
+    t = _KernelTiming()
+    backend.call("timing_read", KERNEL_FAMILIES[family] if isinstance(family, str) else family,
+                 C.byref(t))
+    return t.launches, t.total_ms, t.bytes
+
+
 def sessions_attention(backend, sessions, queries, num_q_heads, scale):
     """Batched ``RagSession::attention`` over sessions of one prefix (C-ABI extension)."""
     q = _f32(queries)
@@ -723,9 +747,8 @@ def quantize_per_token(backend, data, batch, heads, tokens, head_dim, bits, grou
 def lcg_fill(n, seed):
     """The reference tests' LCG (tests/attention.rs:3-11): exact in f32 on any IEEE host."""
     out = np.empty(n, dtype=np.float32)
-    state = np.uint64(seed & 0xFFFFFFFF)
-    # Vectorised form of state = state*1664525 + 1013904223 (mod 2^32), via jump-ahead
-    # in blocks: keep it simple and exact with Python ints for small n, numpy for large.
+    # state = state*1664525 + 1013904223 (mod 2^32): Python ints for small n, a blocked
+    # jump-ahead in numpy for large n.
     if n <= 4096:
         s = int(seed) & 0xFFFFFFFF
         vals = []
@@ -735,7 +758,6 @@ def lcg_fill(n, seed):
         u = np.asarray(vals, dtype=np.float32)
     else:
         u = _lcg_states(seed, n).astype(np.float32)
-    del state
     u = u / np.float32(1 << 24)
     out[:] = u * np.float32(2.0) - np.float32(1.0)
     return out
