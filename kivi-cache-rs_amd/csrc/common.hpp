@@ -6,19 +6,21 @@
 //
 //   key codes    u32 [cap][D/ppw]           token-major: word (t, j) holds channels
 //                                           j*ppw .. j*ppw+ppw-1 of token t, channel
-//                                           j*ppw+i at bits [b*i, b*i+b)
+//                                           j*ppw+i at bit code_shift(b, i)
 //   key params   f32 [cap/G][D][2]          (scale, zero) per (group, channel) — the
 //                                           reference PackedStream order (src/quant.rs:307-311)
 //   value codes  u32 [cap/64][D][64/ppw]    channel-major in 64-token blocks: word (blk, d, w)
-//                                           holds tokens blk*64 + w*ppw + i of channel d
+//                                           holds tokens blk*64 + w*ppw + i of channel d,
+//                                           token w*ppw+i at bit code_shift(b, i)
 //   value params f32 [cap/64][D/G][64][2]   (scale, zero) per (token, channel group)
 //
-// with ppw = 32/bits codes per word. Keys are packed along channels and values along
-// tokens — the axis each is reduced over in attention — so a lane that owns a token
-// (keys) or a channel (values) unpacks whole words of its own codes. The reference packs
-// the other way (keys along tokens, values along channels, src/quant.rs:312-323, 362-372);
-// the quantized codes and (scale, zero) values are identical, and
-// kivi_cache_export_streams re-packs into the reference order bit for bit.
+// with ppw = 32/bits codes per word. Element i of a word sits at bit code_shift(bits, i):
+// 4-bit and 8-bit words are byte-sliced (element i in byte i % 4, at bit offset
+// bits*(i/4) of that byte), 2-bit words nibble-sliced (element i in nibble i % 8, at bit
+// offset 2*(i/8) of that nibble). One shift-and-mask then leaves four (4-bit) or eight
+// (2-bit) consecutive elements one per byte or nibble, which the attention kernels convert
+// into MFMA operands with the packed fp8 / fp4 converters and no further shuffling.
+// Per unit, smax[2] holds the largest key and value scale quantized so far (see CacheView).
 //
 // fp32 state per unit: key residual [R][D] (linear, token kq+i in slot i) and the value
 // window [R][D] as a ring (token vq+i in slot (vhead+i) % R), so a decode step evicts one
@@ -33,6 +35,11 @@
 namespace kivi {
 
 constexpr uint32_t kValueBlock = 64;  // tokens per value code block
+
+// Bit offset of element i (0 <= i < 32/bits) inside a native code word.
+__host__ __device__ inline uint32_t code_shift(uint32_t bits, uint32_t i) {
+  return bits == 2 ? 4u * (i & 7u) + 2u * (i >> 3) : 8u * (i & 3u) + bits * (i >> 2);
+}
 
 struct Geometry {
   uint32_t bits;  // 2, 4, 8
@@ -64,6 +71,10 @@ struct CacheView {
   float* vparams;
   float* kres;   // [units][R][D]
   float* vring;  // [units][R][D]
+  // [units][2]: running maxima of the key and of the value scales ever quantized into each
+  // unit (f32 bit patterns; scales are >= 0, so unsigned order is float order). The
+  // attention kernels derive power-of-two operand ranges from them.
+  uint32_t* smax;
 };
 
 // Sequence state of a cache at one instant.
@@ -168,6 +179,9 @@ struct AttnProblem {
   uint32_t heads;            // kv heads
   uint32_t batch;
   float scale;
+  // [units] split counters, zero between calls (calls sharing them must not overlap on the
+  // device), or null to merge in a separate launch
+  uint32_t* counters;
 };
 
 // Workspace floats the attention needs for `p` (split-K partials).

@@ -288,7 +288,7 @@ struct CacheCore {
   size_t batch = 0, heads = 0, head_dim = 0;
   int device = 0;
   Geometry geo{};
-  DevBuf kcodes, kparams, vcodes, vparams, kres, vring;
+  DevBuf kcodes, kparams, vcodes, vparams, kres, vring, smax;
   uint64_t seq = 0, kq = 0, vq = 0;
   uint32_t kres_len = 0, vres_len = 0, vhead = 0;
   hipStream_t stream = nullptr;
@@ -305,6 +305,7 @@ struct CacheCore {
     v.vparams = vparams.as<float>();
     v.kres = kres.as<float>();
     v.vring = vring.as<float>();
+    v.smax = smax.as<uint32_t>();
     return v;
   }
   SeqState state() const {
@@ -328,6 +329,7 @@ struct CacheCore {
     const size_t rbytes = (size_t)geo.units * geo.R * geo.D * sizeof(float);
     KIVI_TRY(kres.alloc_zero(rbytes, s, "key residual"));
     KIVI_TRY(vring.alloc_zero(rbytes, s, "value window"));
+    KIVI_TRY(smax.alloc_zero((size_t)geo.units * 2 * sizeof(uint32_t), s, "scale maxima"));
     return Status{};
   }
 
@@ -484,6 +486,7 @@ struct CacheCore {
     const size_t rbytes = (size_t)geo.units * geo.R * geo.D * sizeof(float);
     HIP_TRY(hipMemcpyAsync(dst.kres.p, kres.p, rbytes, hipMemcpyDeviceToDevice, s), "prefix copy");
     HIP_TRY(hipMemcpyAsync(dst.vring.p, vring.p, rbytes, hipMemcpyDeviceToDevice, s), "prefix copy");
+    HIP_TRY(hipMemcpyAsync(dst.smax.p, smax.p, smax.bytes, hipMemcpyDeviceToDevice, s), "prefix copy");
     const uint64_t used = std::max(kq, vq);
     if (used > 0) {
       const uint64_t gran = granule();
@@ -512,10 +515,43 @@ size_t compressed_bytes(const kivi_memory_report& r) {
          r.key_residual_bytes + r.value_residual_bytes;
 }
 
+// Split counters of one attention target (a cache or a session): the last split workgroup
+// of a unit merges it and re-arms its counter, so two calls sharing the counters must not
+// overlap on the device. Calls on one stream are ordered by the stream; a call on another
+// stream waits for the event recorded after the previous call.
+struct AttnSync {
+  DevBuf counters;
+  hipEvent_t done = nullptr;
+  bool pending = false;
+  hipStream_t last = nullptr;
+  std::mutex mu;
+  AttnSync() = default;
+  AttnSync(const AttnSync&) = delete;
+  AttnSync& operator=(const AttnSync&) = delete;
+  ~AttnSync() {
+    if (done != nullptr) (void)hipEventDestroy(done);
+  }
+  Status init(size_t units, hipStream_t s) {
+    KIVI_TRY(counters.alloc_zero(units * sizeof(uint32_t), s, "attention counters"));
+    HIP_TRY(hipEventCreateWithFlags(&done, hipEventDisableTiming), "attention event");
+    return Status{};
+  }
+  Status before(hipStream_t s) {
+    if (pending && s != last) HIP_TRY(hipStreamWaitEvent(s, done, 0), "attention ordering");
+    return Status{};
+  }
+  Status after(hipStream_t s) {
+    HIP_TRY(hipEventRecord(done, s), "attention ordering");
+    pending = true;
+    last = s;
+    return Status{};
+  }
+};
+
 // Attention over `core` plus an optional device suffix, writing `out` on the device.
-Status attend(const CacheCore& core, const float* suffix_k, const float* suffix_v, uint64_t L,
-              uint64_t suffix_stride, const float* query, size_t qh, float scale, float* out,
-              hipStream_t s) {
+Status attend(const CacheCore& core, AttnSync& sync, const float* suffix_k, const float* suffix_v,
+              uint64_t L, uint64_t suffix_stride, const float* query, size_t qh, float scale,
+              float* out, hipStream_t s) {
   const size_t gq = qh / core.heads;
   if (gq * core.head_dim > kMaxGqD)
     return Err(KIVI_ERR_UNSUPPORTED, gq * core.head_dim, kMaxGqD, "(num_q_heads/num_kv_heads)*head_dim");
@@ -538,9 +574,13 @@ Status attend(const CacheCore& core, const float* suffix_k, const float* suffix_
   p.heads = static_cast<uint32_t>(core.heads);
   p.batch = static_cast<uint32_t>(core.batch);
   p.scale = scale;
+  p.counters = sync.counters.as<uint32_t>();
   Scratch ws;
   KIVI_TRY(ws.get(attention_workspace_floats(p) * sizeof(float), s, "attention workspace"));
+  std::lock_guard<std::mutex> lock(sync.mu);
+  KIVI_TRY(sync.before(s));
   HIP_TRY(launch_attention(p, ws.as<float>(), s), "attention");
+  KIVI_TRY(sync.after(s));
   return Status{};
 }
 
@@ -571,6 +611,7 @@ using namespace kivi;
 
 struct kivi_cache {
   CacheCore core;
+  AttnSync attn;
   std::mutex mu;  // one mutating call at a time (the reference's &mut self)
 };
 
@@ -586,6 +627,7 @@ struct kivi_prefix {
 
 struct kivi_session {
   kivi_prefix* prefix = nullptr;  // holds one reference
+  AttnSync attn;
   DevBuf keys, values;            // [units][cap][D] fp32 suffix (the reference re-splices, src/prefix.rs:196-221)
   uint64_t len = 0, cap = 0;
 };
@@ -623,6 +665,7 @@ Status create_cache(const kivi_config* config, size_t batch, size_t heads, size_
   c->core.head_dim = head_dim;
   c->core.device = dev;
   KIVI_TRY(c->core.init(nullptr));
+  KIVI_TRY(c->attn.init(c->core.units(), nullptr));
   return sync(nullptr, "cache init");
 }
 
@@ -659,13 +702,15 @@ Status cache_attention(const kivi_cache* c, const float* query, size_t query_len
   KIVI_TRY(need_slice(query, query_len, "query"));
   KIVI_TRY(need_slice(out, out_len, "out"));
   DeviceScope scope(core.device);
-  if (device) return attend(core, nullptr, nullptr, 0, 0, query, num_q_heads, scale, out, stream);
+  kivi_cache* mc = const_cast<kivi_cache*>(c);  // counters only; the cache itself is read
+  if (device) return attend(core, mc->attn, nullptr, nullptr, 0, 0, query, num_q_heads, scale, out, stream);
   hipStream_t s = core.stream;
   Scratch dq, dout;
   KIVI_TRY(dq.get(query_len * 4, s, "attention staging"));
   KIVI_TRY(dout.get(out_len * 4, s, "attention staging"));
   HIP_TRY(hipMemcpyAsync(dq.p, query, query_len * 4, hipMemcpyHostToDevice, s), "attention H2D");
-  KIVI_TRY(attend(core, nullptr, nullptr, 0, 0, dq.as<float>(), num_q_heads, scale, dout.as<float>(), s));
+  KIVI_TRY(attend(core, mc->attn, nullptr, nullptr, 0, 0, dq.as<float>(), num_q_heads, scale,
+                  dout.as<float>(), s));
   HIP_TRY(hipMemcpyAsync(out, dout.p, out_len * 4, hipMemcpyDeviceToHost, s), "attention D2H");
   return sync(s, "attention");
 }
@@ -680,15 +725,16 @@ Status session_attend(const kivi_session* se, const float* query, size_t query_l
   KIVI_TRY(need_slice(out, out_len, "out"));
   DeviceScope scope(core.device);
   const uint64_t stride = se->cap * core.head_dim;
+  kivi_session* ms = const_cast<kivi_session*>(se);  // counters only
   if (device)
-    return attend(core, se->keys.as<float>(), se->values.as<float>(), se->len, stride, query,
-                  num_q_heads, scale, out, stream);
+    return attend(core, ms->attn, se->keys.as<float>(), se->values.as<float>(), se->len, stride,
+                  query, num_q_heads, scale, out, stream);
   hipStream_t s = nullptr;
   Scratch dq, dout;
   KIVI_TRY(dq.get(query_len * 4, s, "attention staging"));
   KIVI_TRY(dout.get(out_len * 4, s, "attention staging"));
   HIP_TRY(hipMemcpyAsync(dq.p, query, query_len * 4, hipMemcpyHostToDevice, s), "attention H2D");
-  KIVI_TRY(attend(core, se->keys.as<float>(), se->values.as<float>(), se->len, stride,
+  KIVI_TRY(attend(core, ms->attn, se->keys.as<float>(), se->values.as<float>(), se->len, stride,
                   dq.as<float>(), num_q_heads, scale, dout.as<float>(), s));
   HIP_TRY(hipMemcpyAsync(out, dout.p, out_len * 4, hipMemcpyDeviceToHost, s), "attention D2H");
   return sync(s, "session attention");
@@ -773,9 +819,9 @@ Status batched_sessions(const kivi_session* const* sessions, size_t n, const flo
     dout = so.as<float>();
   }
   for (size_t i = 0; i < n; ++i) {
-    const kivi_session* se = sessions[i];
-    KIVI_TRY(attend(core, se->keys.as<float>(), se->values.as<float>(), se->len, se->cap * core.head_dim,
-                    dq + i * per, num_q_heads, scale, dout + i * per, s));
+    kivi_session* se = const_cast<kivi_session*>(sessions[i]);  // counters only
+    KIVI_TRY(attend(core, se->attn, se->keys.as<float>(), se->values.as<float>(), se->len,
+                    se->cap * core.head_dim, dq + i * per, num_q_heads, scale, dout + i * per, s));
   }
   if (!device) {
     HIP_TRY(hipMemcpyAsync(out, dout, all * 4, hipMemcpyDeviceToHost, s), "sessions D2H");
@@ -932,6 +978,7 @@ void kivi_cache_free(kivi_cache* cache) {
   if (cache == nullptr) return;
   DeviceScope scope(cache->core.device);
   (void)hipStreamSynchronize(cache->core.stream);
+  if (cache->attn.pending) (void)hipEventSynchronize(cache->attn.done);
   delete cache;
 }
 
@@ -1131,6 +1178,11 @@ kivi_status kivi_prefix_session(kivi_prefix* prefix, kivi_session** out, kivi_er
     KIVI_TRY(need(prefix, "prefix"));
     KIVI_TRY(need(out, "out"));
     auto s = std::make_unique<kivi_session>();
+    {
+      DeviceScope scope(prefix->state->core.device);
+      KIVI_TRY(s->attn.init(prefix->state->core.units(), nullptr));
+      KIVI_TRY(sync(nullptr, "session init"));
+    }
     s->prefix = kivi_prefix_retain(prefix);
     *out = s.release();
     return Status{};
@@ -1213,6 +1265,7 @@ void kivi_runtime_free(kivi_runtime* rt) {
   if (rt == nullptr) return;
   DeviceScope scope(rt->cache.core.device);
   (void)hipStreamSynchronize(rt->cache.core.stream);
+  if (rt->cache.attn.pending) (void)hipEventSynchronize(rt->cache.attn.done);
   delete rt;
 }
 

@@ -52,15 +52,20 @@ struct AttnArgs {
   uint64_t t_begin;
   uint32_t S;
   uint32_t nsplit_gen;
-  // MFMA splits: chunks [chunk_begin, chunk_end) in workgroups of 4 waves x CPW chunks,
-  // written to workspace splits split_base .. split_base + nsplit_launch - 1
+  // MFMA splits: packed chunks [chunk_begin, chunk_end) in workgroups of 4 waves x kFastCpw
+  // chunks (workspace splits 0 .. nsplit_fast-1), then window / suffix chunks
+  // [win_begin, win_end), one per workgroup (splits nsplit_fast .. +nsplit_win-1); generic
+  // splits, if any, follow.
   uint32_t chunk_begin;
   uint32_t chunk_end;
-  uint32_t nsplit_launch;
-  uint32_t split_base;
-  uint32_t nsplit_fast;    // MFMA splits of both launches (generic splits follow them)
+  uint32_t nsplit_fast;
+  uint32_t win_begin, win_end;
+  uint32_t nsplit_win;
   uint32_t nsplit_total;   // splits per unit in the workspace
   float* ws;               // [units][nsplit_total][gq][D+2]
+  uint32_t* counters;      // [units] finished splits (0 between calls), or null: separate merge
+  float* out;              // [batch][QH][D]
+  uint32_t units;
 };
 
 // Key / value element (token t, channel d) of one unit, wherever it lives. BITS, DD, GG are
@@ -89,7 +94,7 @@ __device__ __forceinline__ float key_at(const AttnArgs& a, uint32_t unit, uint64
   const uint32_t word = *wp;
   const float2 sz = *sp;
   const float dense = *dp;
-  const float code = static_cast<float>((word >> (bits * (d % ppw))) & ((1u << bits) - 1u));
+  const float code = static_cast<float>((word >> code_shift(bits, d % ppw)) & ((1u << bits) - 1u));
   // arithmetic blend (not a select) so the compiler cannot sink either load into a branch
   const float m = t < kq ? 1.f : 0.f;
   return fmaf(fmaf(code, sz.x, sz.y), m, dense * (1.f - m));  // exact for m in {0, 1}
@@ -118,7 +123,7 @@ __device__ __forceinline__ float value_at(const AttnArgs& a, uint32_t unit, uint
   const uint32_t word = *wp;
   const float2 sz = *sp;
   const float dense = *dp;
-  const float code = static_cast<float>((word >> (bits * (tt % ppw))) & ((1u << bits) - 1u));
+  const float code = static_cast<float>((word >> code_shift(bits, tt % ppw)) & ((1u << bits) - 1u));
   const float m = t < vq ? 1.f : 0.f;
   return fmaf(fmaf(code, sz.x, sz.y), m, dense * (1.f - m));  // exact for m in {0, 1}
 }
@@ -137,12 +142,10 @@ __device__ __forceinline__ float warp_sum(float v) {
 // [gq][S]. Instantiated for every shape (BITS = DD = GG = 0) and, with the shape fixed, for the
 // tail of the MFMA path (the fp32 window, the session suffix and a partial last chunk).
 template <int BITS, int DD, int GG>
-__global__ void __launch_bounds__(kThreads) k_attn_generic(AttnArgs a) {
-  extern __shared__ float lds[];
+__device__ __forceinline__ void generic_split(const AttnArgs& a, uint32_t unit, uint32_t split,
+                                              float* lds) {
   const Geometry& g = a.c.geo;
   const uint32_t D = DD ? DD : g.D, gq = a.gq, S = a.S;
-  const uint32_t unit = blockIdx.x / a.nsplit_gen;
-  const uint32_t split = blockIdx.x % a.nsplit_gen;
   const uint32_t b = unit / a.heads, kvh = unit % a.heads;
   float* q_lds = lds;               // [gq][D], pre-scaled to base-2 logits
   float* w_lds = lds + gq * D;      // [gq][S]
@@ -192,7 +195,7 @@ __global__ void __launch_bounds__(kThreads) k_attn_generic(AttnArgs a) {
   __syncthreads();
 
   // Per-head max and exp2-sum over the split (one wavefront per head).
-  float* part = a.ws + ((uint64_t)unit * a.nsplit_total + a.nsplit_fast + split) * gq * (D + 2);
+  float* part = a.ws + ((uint64_t)unit * a.nsplit_total + a.nsplit_fast + a.nsplit_win + split) * gq * (D + 2);
   for (uint32_t h = wave; h < gq; h += blockDim.x / 64) {
     float m = -INFINITY;
     for (uint32_t k = lane; k < ntok; k += 64) m = fmaxf(m, w_lds[h * S + k]);
@@ -235,9 +238,73 @@ __global__ void __launch_bounds__(kThreads) k_attn_generic(AttnArgs a) {
   }
 }
 
+// Log-sum-exp merge of one unit's split partials into out, one head at a time (LDS: nsplit
+// factors + 8 reduction slots).
+__device__ void merge_unit(const float* ws, uint32_t unit, uint32_t nsplit, uint32_t gq, uint32_t D,
+                           uint32_t heads, uint32_t qh, float* out, float* f_lds) {
+  float* red = f_lds + nsplit;
+  const uint32_t b = unit / heads, kvh = unit % heads;
+  const uint32_t lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+  const uint64_t stride = (uint64_t)gq * (D + 2);
+  for (uint32_t h = 0; h < gq; ++h) {
+    const float* base = ws + (uint64_t)unit * nsplit * stride + h * (D + 2);
+    float m = -INFINITY;
+    for (uint32_t s = threadIdx.x; s < nsplit; s += blockDim.x) m = fmaxf(m, base[s * stride + D]);
+    m = warp_max(m);
+    if (lane == 0) red[wave] = m;
+    __syncthreads();
+    const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float l = 0.f;
+    for (uint32_t s = threadIdx.x; s < nsplit; s += blockDim.x) {
+      const float ms = base[s * stride + D];
+      const float f = ms == -INFINITY ? 0.f : exp2f(ms - M);
+      f_lds[s] = f;
+      l += base[s * stride + D + 1] * f;
+    }
+    l = warp_sum(l);
+    if (lane == 0) red[4 + wave] = l;
+    __syncthreads();
+    const float inv = 1.0f / (red[4] + red[5] + red[6] + red[7]);
+    float* o = out + ((uint64_t)b * qh + kvh * gq + h) * D;
+    for (uint32_t d = threadIdx.x; d < D; d += blockDim.x) {
+      float acc = 0.f;
+      for (uint32_t s = 0; s < nsplit; ++s) acc = fmaf(base[s * stride + d], f_lds[s], acc);
+      o[d] = acc * inv;
+    }
+    __syncthreads();  // f_lds and red are reused by the next head
+  }
+}
+
+// Called by every split workgroup after its partial is written: the last of the unit's
+// splits to finish (device-scope counter) merges the unit and re-arms the counter.
+__device__ void finish_split(const AttnArgs& a, uint32_t unit, float* lds) {
+  __shared__ uint32_t is_last;
+  __threadfence();  // release this workgroup's partial
+  __syncthreads();
+  if (threadIdx.x == 0) is_last = atomicAdd(&a.counters[unit], 1u) == a.nsplit_total - 1 ? 1u : 0u;
+  __syncthreads();
+  if (is_last == 0u) return;
+  __threadfence();  // acquire every split's partial
+  merge_unit(a.ws, unit, a.nsplit_total, a.gq, a.c.geo.D, a.heads, a.qh, a.out, lds);
+  if (threadIdx.x == 0) atomicExch(&a.counters[unit], 0u);
+}
+
+template <int BITS, int DD, int GG>
+__global__ void __launch_bounds__(kThreads) k_attn_generic(AttnArgs a) {
+  extern __shared__ float lds[];
+  const uint32_t unit = blockIdx.x / a.nsplit_gen;
+  generic_split<BITS, DD, GG>(a, unit, blockIdx.x % a.nsplit_gen, lds);
+  if (a.counters != nullptr) {
+    __syncthreads();
+    finish_split(a, unit, lds);
+  }
+}
+
 // ------------------------------------------------------------------ MFMA splits
 
+constexpr int kFastCpw = 8;  // chunks (64 tokens) per wave in the MFMA kernel
 constexpr int kRowPad = 4;  // floats of padding per logit row (LDS bank spread)
+constexpr int kRowStride1 = 64 + kRowPad;  // logits row stride of the one-chunk (MIXED) path
 
 // v_mfma_f32_4x4x1_16B with CBSZ=3: blocks 0-7 take A from block ABID, blocks 8-15 from
 // block 8+ABID. ABID must be an immediate; the switch folds away once loops are unrolled.
@@ -263,40 +330,74 @@ __device__ __forceinline__ float sum_over_blocks(float v) {
   return v;
 }
 
-// Codes of one packed word as MFMA B operands: out[p] = code at bits [b*p, b*p+b) times
-// `unit`. 2- and 4-bit codes are masked one per byte; a byte p < 16 read as fp8 e4m3 is
-// exactly p*unit (subnormals and the first binade are linear), so v_cvt_pk_f32_fp8 turns
-// two codes into two f32 per instruction. 8-bit codes use v_cvt_f32_ubyte0..3 (unit 1).
-typedef float v2f __attribute__((ext_vector_type(2)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+
+// v_mfma_f32_4x4x4_16b_f16 with CBSZ=3: 16 blocks of D[4x4] += A[4x4] * B[4x4] (K = 4),
+// blocks 0-7 taking A from block ABID and blocks 8-15 from block 8+ABID. Lane l holds
+// B[k][l%4] of block l/4 for k = 0..3 and gets D[i][l%4] of its block in register i.
+__device__ __forceinline__ v4f mfma16(h4 a, h4 b, v4f c, int abid) {
+  switch (abid) {
+    case 0: return __builtin_amdgcn_mfma_f32_4x4x4f16(a, b, c, 3, 0, 0);
+    case 1: return __builtin_amdgcn_mfma_f32_4x4x4f16(a, b, c, 3, 1, 0);
+    case 2: return __builtin_amdgcn_mfma_f32_4x4x4f16(a, b, c, 3, 2, 0);
+    case 3: return __builtin_amdgcn_mfma_f32_4x4x4f16(a, b, c, 3, 3, 0);
+    case 4: return __builtin_amdgcn_mfma_f32_4x4x4f16(a, b, c, 3, 4, 0);
+    case 5: return __builtin_amdgcn_mfma_f32_4x4x4f16(a, b, c, 3, 5, 0);
+    case 6: return __builtin_amdgcn_mfma_f32_4x4x4f16(a, b, c, 3, 6, 0);
+    default: return __builtin_amdgcn_mfma_f32_4x4x4f16(a, b, c, 3, 7, 0);
+  }
+}
+
 template <int BITS>
-__device__ __forceinline__ void unpack_word(uint32_t w, float* out) {
+struct CodeUnit {
+  static constexpr int kExp = BITS == 2 ? -1 : BITS == 4 ? -9 : 0;
+};
+
+// Elements 4k .. 4k+3 of a native code word (layout of code_shift) as an exact f16 MFMA
+// operand times 2^kExp. 2-bit: masking with 0x33333333 (and after a shift by 2) leaves one
+// code per nibble, elements 0-7 (8-15) in nibble order; a nibble p < 4 read as fp4 e2m1 is
+// exactly p/2, and v_cvt_scalef32_pk_f16_fp4 converts the two nibbles of one byte. 4-bit:
+// masking with 0x0F0F0F0F after a shift by 4k leaves elements 4k..4k+3 one per byte; a byte
+// p < 16 read as fp8 e4m3 is exactly p * 2^-9 (subnormals and the first binade are evenly
+// spaced). 8-bit: v_perm_b32 places each byte under the f16 exponent of 1024 (0x64), giving
+// 1024 + p exactly, and a packed f16 subtraction removes the 1024.
+template <int BITS>
+__device__ __forceinline__ h4 codes4(uint32_t w, int k) {
   if constexpr (BITS == 2) {
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int m = static_cast<int>((w >> (2 * k)) & 0x03030303u);  // positions k, k+4, k+8, k+12
-      const v2f lo = __builtin_amdgcn_cvt_pk_f32_fp8(m, false);
-      const v2f hi = __builtin_amdgcn_cvt_pk_f32_fp8(m, true);
-      out[k] = lo.x;
-      out[k + 4] = lo.y;
-      out[k + 8] = hi.x;
-      out[k + 12] = hi.y;
+    const uint32_t m = k < 2 ? (w & 0x33333333u) : ((w >> 2) & 0x33333333u);
+    h2 a, b;
+    if (k % 2 == 0) {
+      a = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(m, 1.0f, 0);
+      b = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(m, 1.0f, 1);
+    } else {
+      a = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(m, 1.0f, 2);
+      b = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(m, 1.0f, 3);
     }
+    return h4{a.x, a.y, b.x, b.y};
   } else if constexpr (BITS == 4) {
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      const int m = static_cast<int>((w >> (4 * k)) & 0x0F0F0F0Fu);  // positions k, k+2, k+4, k+6
-      const v2f lo = __builtin_amdgcn_cvt_pk_f32_fp8(m, false);
-      const v2f hi = __builtin_amdgcn_cvt_pk_f32_fp8(m, true);
-      out[k] = lo.x;
-      out[k + 2] = lo.y;
-      out[k + 4] = hi.x;
-      out[k + 6] = hi.y;
-    }
+    const int m = static_cast<int>((w >> (4 * k)) & 0x0F0F0F0Fu);
+    const h2 a = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(m, 1.0f, false);
+    const h2 b = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(m, 1.0f, true);
+    return h4{a.x, a.y, b.x, b.y};
   } else {
-    out[0] = static_cast<float>(w & 0xFFu);
-    out[1] = static_cast<float>((w >> 8) & 0xFFu);
-    out[2] = static_cast<float>((w >> 16) & 0xFFu);
-    out[3] = static_cast<float>(w >> 24);
+    const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, w, 0x04010400u);  // bytes 0, 1
+    const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, w, 0x04030402u);  // bytes 2, 3
+    const h2 bias = {(_Float16)1024.0f, (_Float16)1024.0f};
+    const h2 x = __builtin_bit_cast(h2, lo) - bias;
+    const h2 y = __builtin_bit_cast(h2, hi) - bias;
+    return h4{x.x, x.y, y.x, y.y};
+  }
+}
+
+// x = hi + lo with hi = f16(x) and lo = f16(x - hi): 22 significant bits in two f16 operands
+// (x must be below 2^15 in magnitude; the callers scale their operands by a power of two).
+__device__ __forceinline__ void split4(const float* x, h4& hi, h4& lo) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const _Float16 h = (_Float16)x[i];
+    hi[i] = h;
+    lo[i] = (_Float16)(x[i] - (float)h);
   }
 }
 
@@ -313,75 +414,96 @@ __device__ __forceinline__ void load_words(const uint32_t* p, uint32_t* w) {
   }
 }
 
-// Everything one chunk's logits read from HBM: the lane token's code words and the
-// (scale, zero) pairs of its group half for channels 16*la .. +15.
+// One chunk's key data for the lane's token: its code words, and the (scale, zero) pairs of
+// its group (half lc) for channels 16*la .. +15.
 template <int BITS>
-struct KeyData {
-  uint32_t kw[128 * BITS / 32];
+struct KeyWords {
+  uint32_t w[128 * BITS / 32];
+};
+struct KeyParams {
   float4 sz[8];
 };
-
-// Everything one chunk's value mix reads from HBM: the lane channel's code words for both
-// channel halves, and (scale, zero) of tokens 8*la .. +7 for channel groups lc, lc+2.
+// One chunk's value data: the code words of channels lane and 64+lane, and (scale, zero) of
+// tokens 8*la .. +7 for channel groups lc and lc+2.
 template <int BITS>
-struct ValueData {
-  uint32_t vw[2][64 * BITS / 32];
+struct ValueWords {
+  uint32_t w[2][64 * BITS / 32];
+};
+struct ValueParams {
   float4 sz[2][4];
 };
 
 template <int BITS>
-__device__ __forceinline__ void load_key_data(const AttnArgs& a, uint32_t unit, uint32_t ch,
-                                              uint32_t lane, uint32_t la, uint32_t lc,
-                                              KeyData<BITS>& kd) {
+__device__ __forceinline__ void load_key_words(const AttnArgs& a, uint32_t unit, uint32_t ch,
+                                               uint32_t lane, KeyWords<BITS>& kw) {
   constexpr int KW = 128 * BITS / 32;
-  const Geometry& g = a.c.geo;
-  const float4* pp = reinterpret_cast<const float4*>(
-      a.c.kparams + unit * g.kparams_unit() + ((uint64_t)(2 * ch + lc) * 128 + 16 * la) * 2);
-#pragma unroll
-  for (int j = 0; j < 8; ++j) kd.sz[j] = pp[j];
-  load_words<KW>(a.c.kcodes + unit * g.kcodes_unit() + ((uint64_t)ch * 64 + lane) * KW, kd.kw);
+  load_words<KW>(a.c.kcodes + unit * a.c.geo.kcodes_unit() + ((uint64_t)ch * 64 + lane) * KW, kw.w);
 }
-
+__device__ __forceinline__ void load_key_params(const AttnArgs& a, uint32_t unit, uint32_t ch,
+                                                uint32_t la, uint32_t lc, KeyParams& kp) {
+  const float4* pp = reinterpret_cast<const float4*>(
+      a.c.kparams + unit * a.c.geo.kparams_unit() + ((uint64_t)(2 * ch + lc) * 128 + 16 * la) * 2);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) kp.sz[j] = pp[j];
+}
 template <int BITS>
-__device__ __forceinline__ void load_value_data(const AttnArgs& a, uint32_t unit, uint32_t tb,
-                                                uint32_t lane, uint32_t la, uint32_t lc,
-                                                ValueData<BITS>& vd) {
+__device__ __forceinline__ void load_value_words(const AttnArgs& a, uint32_t unit, uint32_t tb,
+                                                 uint32_t lane, ValueWords<BITS>& vw) {
   constexpr int VW = 64 * BITS / 32;
-  const Geometry& g = a.c.geo;
+#pragma unroll
+  for (int hv = 0; hv < 2; ++hv)
+    load_words<VW>(a.c.vcodes + unit * a.c.geo.vcodes_unit() + ((uint64_t)tb * 128 + lane + 64 * hv) * VW,
+                   vw.w[hv]);
+}
+__device__ __forceinline__ void load_value_params(const AttnArgs& a, uint32_t unit, uint32_t tb,
+                                                  uint32_t la, uint32_t lc, ValueParams& vp) {
 #pragma unroll
   for (int hv = 0; hv < 2; ++hv) {
-    load_words<VW>(a.c.vcodes + unit * g.vcodes_unit() + ((uint64_t)tb * 128 + lane + 64 * hv) * VW, vd.vw[hv]);
     const float4* pp = reinterpret_cast<const float4*>(
-        a.c.vparams + unit * g.vparams_unit() + (((uint64_t)tb * 4 + lc + 2 * hv) * 64 + 8 * la) * 2);
+        a.c.vparams + unit * a.c.geo.vparams_unit() + (((uint64_t)tb * 4 + lc + 2 * hv) * 64 + 8 * la) * 2);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) vd.sz[hv][j] = pp[j];
+    for (int j = 0; j < 4; ++j) vp.sz[hv][j] = pp[j];
   }
 }
 
-// Logits of one packed 64-token chunk for the lane's token (lane = token within the chunk).
-// On gfx950 the 4x4 f32 MFMAs do not overlap VALU work, so each 16-channel step unpacks its
-// codes (VALU block) and then issues its 16 MFMAs back to back (sched_barrier).
-template <int BITS, int NRS>
-__device__ __forceinline__ void chunk_logits(const KeyData<BITS>& kd, const float (&qv)[NRS][16],
-                                             float unit_scale, float (&lg)[NRS][4]) {
-  constexpr int PPW = 32 / BITS;
-  float qp[NRS][16];
+// Key-side A operands of one chunk: q * scale (already times 2^e) per (head, channel) of the
+// lane's group, split hi/lo, for K-groups of channels 16*la + 4k .. +3; bias[h] = sum_d q*zero
+// summed over the 8 blocks of the half, times 2^kExp (it enters through an f32 MFMA).
+template <int NRS>
+struct KeyA {
+  h4 hi[NRS][4], lo[NRS][4];
   float bias[NRS];
+};
+
+template <int BITS, int NRS>
+__device__ __forceinline__ void key_operands(const KeyParams& kp, const float (&qv)[NRS][16],
+                                             KeyA<NRS>& A) {
+  constexpr float kUnit = CodeUnit<BITS>::kExp == 0 ? 1.0f : CodeUnit<BITS>::kExp == -1 ? 0.5f : 0.001953125f;
 #pragma unroll
-  for (int rs = 0; rs < NRS; ++rs) bias[rs] = 0.f;
+  for (int rs = 0; rs < NRS; ++rs) {
+    float p[16];
+    float bias = 0.f;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const float4 sz = kd.sz[j];  // (s, z) of channels 2j, 2j+1
-#pragma unroll
-    for (int rs = 0; rs < NRS; ++rs) {
-      qp[rs][2 * j] = qv[rs][2 * j] * sz.x;
-      qp[rs][2 * j + 1] = qv[rs][2 * j + 1] * sz.z;
-      bias[rs] = fmaf(qv[rs][2 * j], sz.y, bias[rs]);
-      bias[rs] = fmaf(qv[rs][2 * j + 1], sz.w, bias[rs]);
+    for (int j = 0; j < 8; ++j) {
+      const float4 sz = kp.sz[j];  // (s, z) of channels 2j, 2j+1
+      p[2 * j] = qv[rs][2 * j] * sz.x;
+      p[2 * j + 1] = qv[rs][2 * j + 1] * sz.z;
+      bias = fmaf(qv[rs][2 * j], sz.y, bias);
+      bias = fmaf(qv[rs][2 * j + 1], sz.w, bias);
     }
-  }
 #pragma unroll
-  for (int rs = 0; rs < NRS; ++rs) bias[rs] = sum_over_blocks(bias[rs]) * unit_scale;
+    for (int k = 0; k < 4; ++k) split4(p + 4 * k, A.hi[rs][k], A.lo[rs][k]);
+    A.bias[rs] = sum_over_blocks(bias) * kUnit;
+  }
+}
+
+// Logits of one chunk for the lane's token (lane = token within the chunk), scaled by
+// 2^(e + kExp). Block a2's lanes hold A for channels 16*a2 .. +15, so ABID = a2 broadcasts it
+// to the 8 token blocks of each half; B = the lane token's codes (exact).
+template <int BITS, int NRS>
+__device__ __forceinline__ void key_mfma(const KeyWords<BITS>& kw, const KeyA<NRS>& A,
+                                         float (&lg)[NRS][4]) {
+  constexpr int PPW = 32 / BITS;
   v4f acc[NRS][2];
 #pragma unroll
   for (int rs = 0; rs < NRS; ++rs) {
@@ -390,77 +512,196 @@ __device__ __forceinline__ void chunk_logits(const KeyData<BITS>& kd, const floa
   }
 #pragma unroll
   for (int a2 = 0; a2 < 8; ++a2) {
-    float code[16];
 #pragma unroll
-    for (int q = 0; q < 16 / PPW; ++q) unpack_word<BITS>(kd.kw[a2 * (16 / PPW) + q], code + q * PPW);
-    __builtin_amdgcn_sched_barrier(0);
+    for (int k = 0; k < 4; ++k) {
+      const int c0 = 16 * a2 + 4 * k;  // first channel of the K-group
+      const h4 b = codes4<BITS>(kw.w[c0 / PPW], (c0 % PPW) / 4);
 #pragma unroll
-    for (int r = 0; r < 16; ++r)
-#pragma unroll
-      for (int rs = 0; rs < NRS; ++rs) acc[rs][r & 1] = mfma_bcast(qp[rs][r], code[r], acc[rs][r & 1], a2);
-    __builtin_amdgcn_sched_barrier(0);
+      for (int rs = 0; rs < NRS; ++rs) {
+        acc[rs][0] = mfma16(A.hi[rs][k], b, acc[rs][0], a2);
+        acc[rs][1] = mfma16(A.lo[rs][k], b, acc[rs][1], a2);
+      }
+    }
   }
 #pragma unroll
   for (int rs = 0; rs < NRS; ++rs) {
-    acc[rs][0] = mfma_bcast(bias[rs], 1.0f, acc[rs][0], 0);
+    acc[rs][0] = mfma_bcast(A.bias[rs], 1.0f, acc[rs][0], 0);
 #pragma unroll
     for (int i = 0; i < 4; ++i) lg[rs][i] = acc[rs][0][i] + acc[rs][1][i];
   }
 }
 
-// Value mix of one packed 64-token chunk into vacc (lane = channel lane and 64+lane); w holds
-// the lane's weights of tokens 8*la .. 8*la+7.
-template <int BITS, int NRS>
-__device__ __forceinline__ void chunk_values(const ValueData<BITS>& vd, const float (&w)[NRS][8],
-                                             float inv_unit, v4f (&vacc)[NRS][2],
-                                             float (&zacc)[NRS][2]) {
-  constexpr int VW = 64 * BITS / 32, PPW = 32 / BITS;
-  // A operands: w * scale / unit (the zero term is accumulated apart)
-  float av[NRS][2][8];
+// Value-side A operands of one chunk: w * scale * 2^e per (head, token) of the lane's tokens
+// 8*la .. +7 and channel group (lc + 2*hv), split hi/lo into K-groups of 4 tokens. The zero
+// term sum_t w*zero accumulates into zacc (f32 VALU, unscaled).
+template <int NRS>
+struct ValueA {
+  h4 hi[NRS][2][2], lo[NRS][2][2];  // [rs][hv][tokens 8*la + 4j ..]
+};
+
+template <int NRS>
+__device__ __forceinline__ void value_operands(const ValueParams& vp, const float (&w)[NRS][8],
+                                               float vfac, ValueA<NRS>& A, float (&zacc)[NRS][2]) {
 #pragma unroll
-  for (int hv = 0; hv < 2; ++hv) {
+  for (int rs = 0; rs < NRS; ++rs) {
+    float wv[8];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float4 sz = vd.sz[hv][j];  // tokens 8*la + 2j, +1
+    for (int r = 0; r < 8; ++r) wv[r] = w[rs][r] * vfac;
 #pragma unroll
-      for (int rs = 0; rs < NRS; ++rs) {
-        av[rs][hv][2 * j] = w[rs][2 * j] * inv_unit * sz.x;
-        av[rs][hv][2 * j + 1] = w[rs][2 * j + 1] * inv_unit * sz.z;
+    for (int hv = 0; hv < 2; ++hv) {
+      float p[8];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float4 sz = vp.sz[hv][j];  // tokens 8*la + 2j, +1
+        p[2 * j] = wv[2 * j] * sz.x;
+        p[2 * j + 1] = wv[2 * j + 1] * sz.z;
         zacc[rs][hv] = fmaf(w[rs][2 * j], sz.y, zacc[rs][hv]);
         zacc[rs][hv] = fmaf(w[rs][2 * j + 1], sz.w, zacc[rs][hv]);
       }
+      split4(p, A.hi[rs][hv][0], A.lo[rs][hv][0]);
+      split4(p + 4, A.hi[rs][hv][1], A.lo[rs][hv][1]);
     }
-  }
-  // both channel halves interleaved: two independent accumulation chains
-#pragma unroll
-  for (int q = 0; q < VW; ++q) {
-    float code[2][PPW];
-    unpack_word<BITS>(vd.vw[0][q], code[0]);
-    unpack_word<BITS>(vd.vw[1][q], code[1]);
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int p = 0; p < PPW; ++p) {
-      const int tt = q * PPW + p;  // token within the chunk: 8*a2 + r
-      const int a2 = tt / 8, r = tt % 8;
-#pragma unroll
-      for (int hv = 0; hv < 2; ++hv)
-#pragma unroll
-        for (int rs = 0; rs < NRS; ++rs) vacc[rs][hv] = mfma_bcast(av[rs][hv][r], code[hv][p], vacc[rs][hv], a2);
-    }
-    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
+// Value mix of one chunk into vacc (lane = channels lane and 64+lane, scaled by 2^(e+kExp)).
+// K-group (word q, k) covers tokens q*PPW + 4k .. +3, whose A lives in block t0/8.
+template <int BITS, int NRS>
+__device__ __forceinline__ void value_mfma(const ValueWords<BITS>& vw, const ValueA<NRS>& A,
+                                           v4f (&vacc)[NRS][2]) {
+  constexpr int VW = 64 * BITS / 32, PPW = 32 / BITS;
+#pragma unroll
+  for (int q = 0; q < VW; ++q) {
+#pragma unroll
+    for (int k = 0; k < PPW / 4; ++k) {
+      const int t0 = q * PPW + 4 * k;
+      const int a2 = t0 / 8, j = (t0 / 4) % 2;
+      const h4 b0 = codes4<BITS>(vw.w[0][q], k);
+      const h4 b1 = codes4<BITS>(vw.w[1][q], k);
+#pragma unroll
+      for (int rs = 0; rs < NRS; ++rs) {
+        vacc[rs][0] = mfma16(A.hi[rs][0][j], b0, vacc[rs][0], a2);
+        vacc[rs][1] = mfma16(A.hi[rs][1][j], b1, vacc[rs][1], a2);
+        vacc[rs][0] = mfma16(A.lo[rs][0][j], b0, vacc[rs][0], a2);
+        vacc[rs][1] = mfma16(A.lo[rs][1][j], b1, vacc[rs][1], a2);
+      }
+    }
+  }
+}
+
+// fp32 rows of the chunk path: token t's key row (key residual for kq <= t < seq, session
+// suffix for seq <= t < total) and value row (value window ring for vq <= t < seq, suffix
+// after). Every other t maps to a valid row whose contribution the caller masks to zero.
+__device__ __forceinline__ const float* key_row(const AttnArgs& a, uint32_t unit, uint64_t t) {
+  const uint32_t D = a.c.geo.D;
+  if (t >= a.seq && t < a.total && a.suffix_k != nullptr)
+    return a.suffix_k + unit * a.suffix_stride + (t - a.seq) * D;
+  const uint64_t r = t >= a.st.kq && t < a.seq ? t - a.st.kq : 0;
+  return a.c.kres + ((uint64_t)unit * a.c.geo.R + r) * D;
+}
+__device__ __forceinline__ const float* value_row(const AttnArgs& a, uint32_t unit, uint64_t t) {
+  const uint32_t D = a.c.geo.D, R = a.c.geo.R;
+  if (t >= a.seq && t < a.total && a.suffix_v != nullptr)
+    return a.suffix_v + unit * a.suffix_stride + (t - a.seq) * D;
+  uint32_t slot = a.st.vhead + (t >= a.st.vq && t < a.seq ? static_cast<uint32_t>(t - a.st.vq) : 0u);
+  if (slot >= R) slot -= R;
+  return a.c.vring + ((uint64_t)unit * R + slot) * D;
+}
+
+// Logit contribution of the chunk's fp32 keys (tokens kq <= t < total) for the lane's token,
+// added to lg in the packed pass's units: f32 MFMAs (v_mfma_f32_4x4x1_16B), A = q * 2^e
+// broadcast from block a2 (channels 16*a2 + r), B = the token's key row times
+// unit_scale = 2^kExp (0 for other tokens), accumulated onto lg.
+template <int NRS>
+__device__ __forceinline__ void key_fp32(const AttnArgs& a, uint32_t unit, uint64_t t0, uint32_t lane,
+                                         const float (&qv)[NRS][16], float unit_scale,
+                                         float (&lg)[NRS][4]) {
+  const uint64_t t = t0 + lane;
+  const float m = t >= a.st.kq && t < a.total ? unit_scale : 0.f;  // mask times 2^kExp
+  const float4* row = reinterpret_cast<const float4*>(key_row(a, unit, t));
+  v4f acc[NRS];
+#pragma unroll
+  for (int rs = 0; rs < NRS; ++rs) acc[rs] = v4f{lg[rs][0], lg[rs][1], lg[rs][2], lg[rs][3]};
+  // channels 16*a2 .. +15 per step; the next step's row segment is in flight meanwhile
+  float4 cur[4], nxt[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) cur[j] = row[j];
+#pragma unroll
+  for (int a2 = 0; a2 < 8; ++a2) {
+    if (a2 + 1 < 8) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) nxt[j] = row[4 * (a2 + 1) + j];
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float x[4] = {cur[j].x * m, cur[j].y * m, cur[j].z * m, cur[j].w * m};
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int rs = 0; rs < NRS; ++rs) acc[rs] = mfma_bcast(qv[rs][4 * j + r], x[r], acc[rs], a2);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) cur[j] = nxt[j];
+  }
+#pragma unroll
+  for (int rs = 0; rs < NRS; ++rs)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) lg[rs][i] = acc[rs][i];
+}
+
+// Value contribution of the chunk's fp32 values (tokens vq <= t < total) among tokens
+// 16*quarter .. +15, for channels lane and 64+lane, in the packed pass's units: A = w * wscale
+// for the lane's tokens 8*la + r (0 for other tokens), broadcast from block t/8; B = the
+// token's value row.
+template <int NRS>
+__device__ __forceinline__ void value_fp32(const AttnArgs& a, uint32_t unit, uint64_t t0,
+                                           uint32_t quarter, uint32_t lane, uint32_t la,
+                                           const float* wrow, const float (&moff)[NRS],
+                                           float kout, float wscale, v4f (&vacc)[NRS][2]) {
+  // A: lanes of block la hold the weights of tokens 16*quarter + 8*(la%2) + r, so the
+  // quarter's 16 tokens sit in blocks 0 and 1 (ABID 0, 1) whatever the quarter
+  const uint32_t tq = 16 * quarter + 8 * (la % 2);
+  float am[NRS][8];
+#pragma unroll
+  for (int rs = 0; rs < NRS; ++rs) {
+    const float4* lp = reinterpret_cast<const float4*>(wrow + rs * 4 * kRowStride1 + tq);
+    const float4 x0 = lp[0], x1 = lp[1];
+    const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const uint64_t t = t0 + tq + r;
+      const float m = t >= a.st.vq && t < a.total ? wscale : 0.f;
+      am[rs][r] = __builtin_amdgcn_exp2f(fmaf(xs[r], kout, -moff[rs])) * m;
+    }
+  }
+  // tokens 16*quarter .. +15, all 32 values in flight at once
+  float b[16][2];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const float* row = value_row(a, unit, t0 + 16 * quarter + r);
+    b[r][0] = row[lane];
+    b[r][1] = row[lane + 64];
+  }
+#pragma unroll
+  for (int r = 0; r < 16; ++r)
+#pragma unroll
+    for (int rs = 0; rs < NRS; ++rs) {
+      vacc[rs][0] = mfma_bcast(am[rs][r % 8], b[r][0], vacc[rs][0], r / 8);
+      vacc[rs][1] = mfma_bcast(am[rs][r % 8], b[r][1], vacc[rs][1], r / 8);
+    }
+}
+
 // One workgroup = 4 waves; wave w of split s owns packed chunks [s*4*CPW + w*CPW, +CPW) of its
-// unit (chunks whose 64 keys and 64 values are all packed). D = 128, G = 32.
-template <int BITS, int NRS, int CPW>
-__global__ void __launch_bounds__(kThreads) k_attn_mfma(AttnArgs a) {
+// unit (chunks whose 64 keys and 64 values are all packed). D = 128, G = 32. Per chunk the
+// operands are prepared from the (scale, zero) registers first, then the next chunk's data
+// is requested into the same registers while this chunk's MFMAs run (code words are
+// double-buffered).
+template <int BITS, int NRS, int CPW, bool MIXED>
+__device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uint32_t split,
+                                           float* lds) {
   constexpr int D = 128;
   constexpr int ROW = CPW * 64 + kRowPad;  // logits row stride (floats)
   constexpr int NH = 4 * NRS;              // padded heads per unit
-  extern __shared__ float lds[];
-  const uint32_t unit = blockIdx.x / a.nsplit_launch;
-  const uint32_t split = blockIdx.x % a.nsplit_launch;
   const uint32_t b = unit / a.heads, kvh = unit % a.heads;
   const uint32_t lane = threadIdx.x % 64, wave = threadIdx.x / 64;
   const uint32_t la = (lane % 32) / 4;  // block within a half-wave
@@ -469,20 +710,29 @@ __global__ void __launch_bounds__(kThreads) k_attn_mfma(AttnArgs a) {
   const uint32_t gq = a.gq;
   float* wl = lds + wave * NH * ROW;    // this wave's logits [NH][ROW]
 
-  // A byte p < 16 converted as fp8 is p * unit (unit = 2^-9 for OCP e4m3).
-  const float unit_scale = BITS == 8 ? 1.f : __builtin_amdgcn_cvt_f32_fp8(1, 0);
-  const float inv_unit = 1.f / unit_scale;  // exact power of two
+  // Packed launch: chunks are dealt round-robin over the unit's waves (wave slot =
+  // split*4 + wave, stride = all slots). MIXED launch (CPW = 1): workgroup `split` takes one
+  // chunk and wave w its tokens 16w .. 16w+15 (the other tokens' logits are masked), so the
+  // latency-bound fp32 rows are spread over four waves.
+  const uint32_t c_lo = MIXED ? a.win_begin : a.chunk_begin;
+  const uint32_t c_hi = MIXED ? a.win_end : a.chunk_end;
+  const uint32_t nsplit = MIXED ? a.nsplit_win : a.nsplit_fast;
+  const uint32_t split_base = MIXED ? a.nsplit_fast : 0u;
+  const int32_t slots = MIXED ? static_cast<int32_t>(nsplit) : static_cast<int32_t>(nsplit * 4);
+  const int32_t slot = MIXED ? static_cast<int32_t>(split) : static_cast<int32_t>(split * 4 + wave);
+  const int32_t span = static_cast<int32_t>(c_hi - c_lo);
+  const int32_t nch = std::min<int32_t>(CPW, std::max<int32_t>(0, (span - slot + slots - 1) / slots));
+  auto chunk_of = [&](int32_t k) { return static_cast<int32_t>(c_lo) + slot + k * slots; };
+  const uint32_t quarter = MIXED ? wave : 0;
 
-  const int32_t c_begin = static_cast<int32_t>(a.chunk_begin + (split * 4 + wave) * CPW);
-  const int32_t nch = std::max<int32_t>(0, std::min<int32_t>(CPW, static_cast<int32_t>(a.chunk_end) - c_begin));
-
-  // q (base-2 logits, divided by the code unit) for the lane's head, channels 16*la .. +15.
+  // q in base-2 logit units for the lane's head, channels 16*la .. +15 (0 for padded heads).
   float qv[NRS][16];
+  float qmax = 0.f;
 #pragma unroll
   for (int rs = 0; rs < NRS; ++rs) {
     const uint32_t h = rs * 4 + li;
     const float* qp = a.query + ((uint64_t)b * a.qh + kvh * gq + min(h, gq - 1)) * D + 16 * la;
-    const float s = h < gq ? a.scale2 * inv_unit : 0.f;
+    const float s = h < gq ? a.scale2 : 0.f;
 #pragma unroll
     for (int r = 0; r < 16; r += 4) {
       const float4 v = *reinterpret_cast<const float4*>(qp + r);
@@ -491,47 +741,92 @@ __global__ void __launch_bounds__(kThreads) k_attn_mfma(AttnArgs a) {
       qv[rs][r + 2] = v.z * s;
       qv[rs][r + 3] = v.w * s;
     }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) qmax = fmaxf(qmax, fabsf(qv[rs][r]));
   }
+  // Power-of-two operand ranges: every key A operand |q * scale| * 2^ek and every value A
+  // operand |w * scale| * 2^ev (w <= 1) stays below 2^15, from the unit's largest scales.
+  qmax = warp_max(qmax);
+  const float kmax = __uint_as_float(a.c.smax[2 * unit]);
+  const float vmax = __uint_as_float(a.c.smax[2 * unit + 1]);
+  const int ek = std::min(60, std::max(-100, 15 - __builtin_amdgcn_frexp_expf(qmax * kmax)));
+  const int ev = std::min(60, std::max(-100, 15 - __builtin_amdgcn_frexp_expf(vmax)));
+  constexpr int kExp = CodeUnit<BITS>::kExp;
+  const float kfac = ldexpf(1.f, ek), vfac = ldexpf(1.f, ev);
+  const float kout = ldexpf(1.f, -ek - kExp), vout = ldexpf(1.f, -ev - kExp);
+#pragma unroll
+  for (int rs = 0; rs < NRS; ++rs)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) qv[rs][r] *= kfac;
 
-  // ---------------- phase 1: logits of every owned chunk into LDS
+  // ---------------- phase 1: logits of every owned chunk into LDS (scaled by 2^(ek+kExp))
+  // A chunk's keys are packed for t < kq and fp32 after; packed arrays hold zero codes and
+  // zero (scale, zero) beyond kq (and vq), so each pass contributes nothing outside its range
+  // and the fp32 passes mask theirs. Tokens past `total` get logit -inf.
+  constexpr float kUnit = kExp == 0 ? 1.0f : kExp == -1 ? 0.5f : 0.001953125f;
+  const uint64_t kq = a.st.kq, vq = a.st.vq, total = a.total;
+  const int32_t lastk = static_cast<int32_t>((kq - 1) / 64);  // kq > 0 on this path
+  const int32_t lastv = vq > 0 ? static_cast<int32_t>((vq - 1) / 64) : 0;
   float mx[NRS][4];
 #pragma unroll
   for (int rs = 0; rs < NRS; ++rs)
 #pragma unroll
     for (int i = 0; i < 4; ++i) mx[rs][i] = -INFINITY;
-  auto logits_of = [&](int k, const KeyData<BITS>& kd) {
-    float lg[NRS][4];
-    chunk_logits<BITS, NRS>(kd, qv, unit_scale, lg);
-#pragma unroll
-    for (int rs = 0; rs < NRS; ++rs)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        wl[(rs * 4 + i) * ROW + k * 64 + lane] = lg[rs][i];
-        mx[rs][i] = fmaxf(mx[rs][i], lg[rs][i]);
-      }
-  };
   {
-    // two register buffers: chunk k+1 is in flight while chunk k is computed
-    KeyData<BITS> k0, k1;
-    if (nch > 0) load_key_data<BITS>(a, unit, c_begin, lane, la, lc, k0);
-    for (int k = 0; k < nch; k += 2) {
-      if (k + 1 < nch) load_key_data<BITS>(a, unit, c_begin + k + 1, lane, la, lc, k1);
-      logits_of(k, k0);
-      if (k + 1 < nch) {
-        if (k + 2 < nch) load_key_data<BITS>(a, unit, c_begin + k + 2, lane, la, lc, k0);
-        logits_of(k + 1, k1);
+    KeyParams kp;
+    KeyWords<BITS> kw0, kw1;
+    KeyA<NRS> A;
+    auto step = [&](int k, const KeyWords<BITS>& cur, KeyWords<BITS>& next) {
+      const uint64_t t0 = (uint64_t)chunk_of(k) * 64;
+      const bool packed = !MIXED || t0 < kq;
+      if (packed) key_operands<BITS, NRS>(kp, qv, A);
+      // unconditional (clamped to packed chunks; the last step re-reads an L2-resident chunk)
+      if constexpr (CPW > 1) {
+        const int32_t kn = std::min(chunk_of(std::min(k + 1, nch - 1)), lastk);
+        load_key_params(a, unit, kn, la, lc, kp);
+        load_key_words<BITS>(a, unit, kn, lane, next);
       }
+      float lg[NRS][4];
+#pragma unroll
+      for (int rs = 0; rs < NRS; ++rs)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) lg[rs][i] = 0.f;
+      if (packed) key_mfma<BITS, NRS>(cur, A, lg);
+      if (MIXED && t0 + 64 > kq && t0 < total) key_fp32<NRS>(a, unit, t0, lane, qv, kUnit, lg);
+      const bool live = !MIXED || (t0 + lane < total && lane / 16 == quarter);
+#pragma unroll
+      for (int rs = 0; rs < NRS; ++rs)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float v = live ? lg[rs][i] : -INFINITY;
+          wl[(rs * 4 + i) * ROW + k * 64 + lane] = v;
+          mx[rs][i] = fmaxf(mx[rs][i], v);
+        }
+    };
+    if (nch > 0) {
+      const int32_t k0 = std::min(chunk_of(0), lastk);
+      load_key_params(a, unit, k0, la, lc, kp);
+      load_key_words<BITS>(a, unit, k0, lane, kw0);
+    }
+    for (int k = 0; k < nch; k += 2) {
+      step(k, kw0, kw1);
+      if (k + 1 < nch) step(k + 1, kw1, kw0);
     }
   }
-  // wave max per head; each lane keeps the max of its own MFMA row
+  // wave max per head; each lane keeps the max of its own MFMA row (true base-2 units)
   float mrow[NRS];
-  float mall[NRS][4];
 #pragma unroll
   for (int rs = 0; rs < NRS; ++rs) {
+    float mall[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) mall[rs][i] = warp_max(mx[rs][i]);
-    mrow[rs] = li == 0 ? mall[rs][0] : li == 1 ? mall[rs][1] : li == 2 ? mall[rs][2] : mall[rs][3];
+    for (int i = 0; i < 4; ++i) mall[i] = warp_max(mx[rs][i]) * kout;
+    mrow[rs] = li == 0 ? mall[0] : li == 1 ? mall[1] : li == 2 ? mall[2] : mall[3];
   }
+  // exponent offset: the row max, or 0 when every logit of the row is -inf (a MIXED wave whose
+  // quarter lies past `total`), so the weights are 0 rather than NaN
+  float moff[NRS];
+#pragma unroll
+  for (int rs = 0; rs < NRS; ++rs) moff[rs] = mrow[rs] == -INFINITY ? 0.f : mrow[rs];
 
   // ---------------- phase 2: value mix
   v4f vacc[NRS][2];
@@ -544,31 +839,43 @@ __global__ void __launch_bounds__(kThreads) k_attn_mfma(AttnArgs a) {
     zacc[rs][0] = zacc[rs][1] = 0.f;
     lsum[rs] = 0.f;
   }
-  auto values_of = [&](int k, const ValueData<BITS>& vd) {
-    float w[NRS][8];
-#pragma unroll
-    for (int rs = 0; rs < NRS; ++rs) {
-      const float4* lp = reinterpret_cast<const float4*>(wl + (rs * 4 + li) * ROW + k * 64 + 8 * la);
-      const float4 x0 = lp[0], x1 = lp[1];
-      const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-#pragma unroll
-      for (int r = 0; r < 8; ++r) {
-        w[rs][r] = __builtin_amdgcn_exp2f(xs[r] - mrow[rs]);  // v_exp_f32; argument <= 0
-        lsum[rs] += w[rs][r];
-      }
-    }
-    chunk_values<BITS, NRS>(vd, w, inv_unit, vacc, zacc);
-  };
   {
-    ValueData<BITS> v0, v1;
-    if (nch > 0) load_value_data<BITS>(a, unit, c_begin, lane, la, lc, v0);
-    for (int k = 0; k < nch; k += 2) {
-      if (k + 1 < nch) load_value_data<BITS>(a, unit, c_begin + k + 1, lane, la, lc, v1);
-      values_of(k, v0);
-      if (k + 1 < nch) {
-        if (k + 2 < nch) load_value_data<BITS>(a, unit, c_begin + k + 2, lane, la, lc, v0);
-        values_of(k + 1, v1);
+    ValueParams vp;
+    ValueWords<BITS> vw0, vw1;
+    ValueA<NRS> A;
+    auto step = [&](int k, const ValueWords<BITS>& cur, ValueWords<BITS>& next) {
+      const uint64_t t0 = (uint64_t)chunk_of(k) * 64;
+      const bool packed = !MIXED || t0 < vq;
+      float w[NRS][8];
+#pragma unroll
+      for (int rs = 0; rs < NRS; ++rs) {
+        const float4* lp = reinterpret_cast<const float4*>(wl + (rs * 4 + li) * ROW + k * 64 + 8 * la);
+        const float4 x0 = lp[0], x1 = lp[1];
+        const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+          w[rs][r] = __builtin_amdgcn_exp2f(fmaf(xs[r], kout, -moff[rs]));  // argument <= 0
+          lsum[rs] += w[rs][r];
+        }
       }
+      if (packed) value_operands<NRS>(vp, w, vfac, A, zacc);
+      if constexpr (CPW > 1) {
+        const int32_t kn = std::min(chunk_of(std::min(k + 1, nch - 1)), lastv);
+        load_value_params(a, unit, kn, la, lc, vp);
+        load_value_words<BITS>(a, unit, kn, lane, next);
+      }
+      if (packed) value_mfma<BITS, NRS>(cur, A, vacc);
+      if (MIXED && t0 + 16 * quarter + 16 > vq && t0 + 16 * quarter < total)
+        value_fp32<NRS>(a, unit, t0, quarter, lane, la, wl + li * ROW, moff, kout, vfac * kUnit, vacc);
+    };
+    if (nch > 0) {
+      const int32_t k0 = std::min(chunk_of(0), lastv);
+      load_value_params(a, unit, k0, la, lc, vp);
+      load_value_words<BITS>(a, unit, k0, lane, vw0);
+    }
+    for (int k = 0; k < nch; k += 2) {
+      step(k, vw0, vw1);
+      if (k + 1 < nch) step(k + 1, vw1, vw0);
     }
   }
 
@@ -589,7 +896,7 @@ __global__ void __launch_bounds__(kThreads) k_attn_mfma(AttnArgs a) {
       for (int i = 0; i < 4; ++i) {
         // zero term of head i, channel group lc + 2*hv lives in lane 32*lc + i
         const float z = __shfl(zacc[rs][hv], 32 * lc + i);
-        cw[(rs * 4 + i) * (D + 2) + lane + 64 * hv] = vacc[rs][hv][i] + z;
+        cw[(rs * 4 + i) * (D + 2) + lane + 64 * hv] = fmaf(vacc[rs][hv][i], vout, z);
       }
     }
     if (lane < 4) {  // lanes 0..3 hold row li = lane after the reductions
@@ -598,7 +905,7 @@ __global__ void __launch_bounds__(kThreads) k_attn_mfma(AttnArgs a) {
     }
   }
   __syncthreads();
-  float* part = a.ws + ((uint64_t)unit * a.nsplit_total + a.split_base + split) * gq * (D + 2);
+  float* part = a.ws + ((uint64_t)unit * a.nsplit_total + split_base + split) * gq * (D + 2);
   for (uint32_t idx = threadIdx.x; idx < gq * (D + 2); idx += blockDim.x) {
     const uint32_t h = idx / (D + 2), d = idx % (D + 2);
     float M = -INFINITY;
@@ -616,6 +923,28 @@ __global__ void __launch_bounds__(kThreads) k_attn_mfma(AttnArgs a) {
       }
     }
     part[h * (D + 2) + d] = v;
+  }
+}
+
+// Chunk launch: workgroups [0, units*nsplit_win) take one window / suffix chunk each (MIXED
+// path, started first), the rest a split of 4*kFastCpw packed chunks; with counters, the
+// last split of each unit merges it.
+template <int BITS, int NRS>
+__global__ void __launch_bounds__(kThreads) k_attn_mfma(AttnArgs a) {
+  extern __shared__ float lds[];
+  const uint32_t nwin = a.units * a.nsplit_win;
+  uint32_t unit;
+  if (blockIdx.x < nwin) {
+    unit = blockIdx.x / a.nsplit_win;
+    mfma_split<BITS, NRS, 1, true>(a, unit, blockIdx.x % a.nsplit_win, lds);
+  } else {
+    const uint32_t blk = blockIdx.x - nwin;
+    unit = blk / a.nsplit_fast;
+    mfma_split<BITS, NRS, kFastCpw, false>(a, unit, blk % a.nsplit_fast, lds);
+  }
+  if (a.counters != nullptr) {
+    __syncthreads();
+    finish_split(a, unit, lds);
   }
 }
 
@@ -658,7 +987,8 @@ __global__ void __launch_bounds__(kThreads)
 
 // ------------------------------------------------------------------ planning
 
-constexpr int kFastCpw = 8;  // chunks (64 tokens) per wave in the MFMA kernel
+constexpr size_t kMaxMergeLds = 48 * 1024;  // in-kernel merge up to ~12K splits per unit
+constexpr bool kUseInKernelMerge = false;
 
 uint32_t split_tokens(uint32_t gq) {
   uint32_t s = 256;
@@ -690,55 +1020,60 @@ AttnArgs make_args(const AttnProblem& p, float* ws) {
   a.heads = p.heads;
   a.gq = p.qh / p.heads;
   a.scale2 = p.scale * kLog2e;
-  // the tail after the MFMA chunks is short: small splits give it enough workgroups
-  a.S = fast_eligible(p) ? 16 : split_tokens(a.gq);
+  // The MFMA path covers every 64-token chunk once some keys are packed: chunks
+  // [0, floor(vq/64)) (keys and values all packed) in one launch, the rest (the fp32 value
+  // window and key residual, the session suffix) in a second launch of the MIXED kernel.
+  // Without packed keys, or for other shapes, the generic splits cover everything.
+  const bool fast = fast_eligible(p) && p.st.kq > 0;
+  a.S = split_tokens(a.gq);
   a.chunk_begin = 0;
-  a.chunk_end = fast_eligible(p) ? static_cast<uint32_t>(p.st.vq / 64) : 0;
+  a.chunk_end = fast ? static_cast<uint32_t>(p.st.vq / 64) : 0;
+  a.win_begin = a.chunk_end;
+  a.win_end = fast ? static_cast<uint32_t>((a.total + 63) / 64) : 0;
   a.nsplit_fast = (a.chunk_end + 4 * kFastCpw - 1) / (4 * kFastCpw);
-  a.nsplit_launch = a.nsplit_fast;
-  a.split_base = 0;
-  a.t_begin = (uint64_t)a.chunk_end * 64;
+  a.nsplit_win = a.win_end - a.win_begin;  // one chunk per workgroup, a quarter per wave
+  a.t_begin = fast ? a.total : 0;
   a.nsplit_gen = static_cast<uint32_t>((a.total - a.t_begin + a.S - 1) / a.S);
-  a.nsplit_total = a.nsplit_fast + a.nsplit_gen;
+  a.nsplit_total = a.nsplit_fast + a.nsplit_win + a.nsplit_gen;
   a.ws = ws;
+  a.out = p.out;
+  a.units = p.cache.geo.units;
+  // The in-kernel merge (last split per unit) needs device-scope release/acquire fences, which
+  // on this multi-XCD part write back and invalidate L2 for every workgroup; the separate
+  // merge launch is faster, so the counters stay unused for now.
+  a.counters = kUseInKernelMerge && (a.nsplit_total + 8) * sizeof(float) <= kMaxMergeLds ? p.counters : nullptr;
   return a;
 }
 
 template <int BITS, int NRS>
-hipError_t launch_fast(const AttnArgs& a, hipStream_t stream) {
+hipError_t launch_fast(const AttnArgs& a, double bytes, hipStream_t stream) {
   constexpr int NH = 4 * NRS;
-  const size_t logits = (size_t)4 * NH * (kFastCpw * 64 + kRowPad);
+  const size_t logits = (size_t)4 * NH * ((a.nsplit_fast > 0 ? kFastCpw : 1) * 64 + kRowPad);
   const size_t combine = (size_t)4 * NH * (128 + 2);
-  const size_t lds = std::max(logits, combine) * sizeof(float);
-  k_attn_mfma<BITS, NRS, kFastCpw><<<a.c.geo.units * a.nsplit_fast, kThreads, lds, stream>>>(a);
+  const size_t merge = a.counters != nullptr ? (size_t)a.nsplit_total + 8 : 0;
+  const size_t lds = std::max(std::max(logits, combine), merge) * sizeof(float);
+  TimedLaunch timed(KIVI_KERNEL_ATTN_PACKED, stream, bytes);
+  k_attn_mfma<BITS, NRS><<<a.units * (a.nsplit_win + a.nsplit_fast), kThreads, lds, stream>>>(a);
   return hipGetLastError();
 }
 
-hipError_t dispatch_fast(const AttnArgs& a, hipStream_t stream) {
+hipError_t dispatch_fast(const AttnArgs& a, double bytes, hipStream_t stream) {
   const int nrs = a.gq <= 4 ? 1 : 2;
   switch (a.c.geo.bits * 10 + nrs) {
-    case 21: return launch_fast<2, 1>(a, stream);
-    case 22: return launch_fast<2, 2>(a, stream);
-    case 41: return launch_fast<4, 1>(a, stream);
-    case 42: return launch_fast<4, 2>(a, stream);
-    case 81: return launch_fast<8, 1>(a, stream);
-    case 82: return launch_fast<8, 2>(a, stream);
+    case 21: return launch_fast<2, 1>(a, bytes, stream);
+    case 22: return launch_fast<2, 2>(a, bytes, stream);
+    case 41: return launch_fast<4, 1>(a, bytes, stream);
+    case 42: return launch_fast<4, 2>(a, bytes, stream);
+    case 81: return launch_fast<8, 1>(a, bytes, stream);
+    case 82: return launch_fast<8, 2>(a, bytes, stream);
     default: return hipErrorInvalidValue;
   }
 }
 
-hipError_t dispatch_generic(const AttnArgs& a, bool fast_shape, hipStream_t stream) {
-  const size_t lds = ((size_t)a.gq * a.c.geo.D + (size_t)a.gq * a.S) * sizeof(float);
-  const dim3 grid(a.c.geo.units * a.nsplit_gen);
-  if (!fast_shape) {
-    k_attn_generic<0, 0, 0><<<grid, kThreads, lds, stream>>>(a);
-  } else if (a.c.geo.bits == 2) {
-    k_attn_generic<2, 128, 32><<<grid, kThreads, lds, stream>>>(a);
-  } else if (a.c.geo.bits == 4) {
-    k_attn_generic<4, 128, 32><<<grid, kThreads, lds, stream>>>(a);
-  } else {
-    k_attn_generic<8, 128, 32><<<grid, kThreads, lds, stream>>>(a);
-  }
+hipError_t dispatch_generic(const AttnArgs& a, hipStream_t stream) {
+  const size_t merge = a.counters != nullptr ? (size_t)a.nsplit_total + 8 : 0;
+  const size_t lds = std::max((size_t)a.gq * a.c.geo.D + (size_t)a.gq * a.S, merge) * sizeof(float);
+  k_attn_generic<0, 0, 0><<<a.units * a.nsplit_gen, kThreads, lds, stream>>>(a);
   return hipGetLastError();
 }
 
@@ -750,7 +1085,7 @@ size_t attention_workspace_floats(const AttnProblem& p) {
 }
 
 hipError_t launch_attention(const AttnProblem& p, float* workspace, hipStream_t stream) {
-  const AttnArgs a = make_args(p, workspace);
+  AttnArgs a = make_args(p, workspace);
   if (a.total == 0) return hipSuccess;
   const Geometry& g = p.cache.geo;
   const uint32_t units = g.units;
@@ -759,24 +1094,25 @@ hipError_t launch_attention(const AttnProblem& p, float* workspace, hipStream_t 
   const double val_tok = g.D * g.bits / 8.0 + g.ncg() * 8.0;
   const double row = g.D * 4.0;
   const double q_bytes = (double)units * a.gq * g.D * 4.0;
-  if (a.nsplit_fast > 0) {
-    const double tokens = (double)(a.chunk_end - a.chunk_begin) * 64;
-    TimedLaunch timed(KIVI_KERNEL_ATTN_PACKED, stream, units * tokens * (key_tok + val_tok) + q_bytes);
-    hipError_t e = dispatch_fast(a, stream);
+  const double out_bytes = a.counters != nullptr ? q_bytes : 0.0;  // the merge writes out
+  const uint64_t t0 = a.t_begin, kq = p.st.kq, vq = p.st.vq;
+  const double kp = kq > t0 ? (double)(kq - t0) : 0.0, vp = vq > t0 ? (double)(vq - t0) : 0.0;
+  const double kd = (double)(p.seq - std::max(kq, t0)), vd = (double)(p.seq - std::max(vq, t0));
+  const double tail_bytes = units * (kp * key_tok + vp * val_tok + (kd + vd + 2.0 * p.suffix_len) * row);
+  if (a.nsplit_fast > 0 || a.nsplit_win > 0) {
+    // one launch over every chunk: packed tokens at packed cost, the rest as fp32 rows
+    const double kpt = (double)std::min<uint64_t>(kq, p.seq), vpt = (double)vq;
+    const double fp32_rows = (double)(p.seq - kq) + (double)(p.seq - vq) + 2.0 * p.suffix_len;
+    hipError_t e = dispatch_fast(
+        a, units * (kpt * key_tok + vpt * val_tok + fp32_rows * row) + q_bytes + out_bytes, stream);
+    if (e != hipSuccess) return e;
+  } else {
+    TimedLaunch timed(KIVI_KERNEL_ATTN_TAIL, stream, tail_bytes + q_bytes + out_bytes);
+    hipError_t e = dispatch_generic(a, stream);
     if (e != hipSuccess) return e;
   }
-  if (a.nsplit_gen > 0) {
-    const uint64_t t0 = a.t_begin, kq = p.st.kq, vq = p.st.vq;
-    const double kp = kq > t0 ? (double)(kq - t0) : 0.0, vp = vq > t0 ? (double)(vq - t0) : 0.0;
-    const double kd = (double)(p.seq - std::max(kq, t0)), vd = (double)(p.seq - std::max(vq, t0));
-    const double bytes =
-        units * (kp * key_tok + vp * val_tok + (kd + vd + 2.0 * p.suffix_len) * row) + q_bytes;
-    TimedLaunch timed(KIVI_KERNEL_ATTN_TAIL, stream, bytes);
-    hipError_t e = dispatch_generic(a, fast_eligible(p), stream);
-    if (e != hipSuccess) return e;
-  }
-  const size_t merge_lds = ((size_t)a.nsplit_total + 8) * sizeof(float);
-  {
+  if (a.counters == nullptr) {
+    const size_t merge_lds = ((size_t)a.nsplit_total + 8) * sizeof(float);
     const double bytes = (double)units * a.gq * ((double)a.nsplit_total * (g.D + 2) + g.D) * 4.0;
     TimedLaunch timed(KIVI_KERNEL_ATTN_MERGE, stream, bytes);
     k_attn_merge<<<units * a.gq, kThreads, merge_lds, stream>>>(workspace, a.nsplit_total, a.gq,

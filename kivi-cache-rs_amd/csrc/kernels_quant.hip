@@ -36,6 +36,19 @@ __device__ __forceinline__ const float* source_row(const RowSource& s, uint32_t 
   return s.base + unit * s.stride_unit + tok * D;
 }
 
+// Raise *smax to the largest `v` of the workgroup (one atomic per workgroup).
+__device__ __forceinline__ void raise_max(uint32_t* smax, float v) {
+  __shared__ float red[kThreads / 64];
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  if (threadIdx.x % 64 == 0) red[threadIdx.x / 64] = v;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float m = red[0];
+    for (int w = 1; w < kThreads / 64; ++w) m = fmaxf(m, red[w]);
+    atomicMax(smax, __float_as_uint(m));
+  }
+}
+
 unsigned grid_for(uint64_t work, unsigned per_block = kThreads) {
   uint64_t b = (work + per_block - 1) / per_block;
   if (b > (1u << 20)) b = 1u << 20;  // grid-stride loops cover the rest
@@ -81,6 +94,7 @@ __global__ void __launch_bounds__(kThreads)
   const uint32_t g = blockIdx.x % ngroups;
   const float* rows = src.base + unit * src.stride_unit + (src.offset + (uint64_t)g * G) * D;
   float2* params = reinterpret_cast<float2*>(c.kparams + unit * geo.kparams_unit() + (g0 + g) * D * 2);
+  float smax = 0.f;
   for (uint32_t d = threadIdx.x; d < D; d += blockDim.x) {
     float mn = INFINITY, mx = -INFINITY;
     for (uint32_t t = 0; t < G; ++t) {
@@ -90,11 +104,12 @@ __global__ void __launch_bounds__(kThreads)
     }
     const float zero = mn;
     const float scale = scale_of(mx - zero, levels);
+    smax = fmaxf(smax, scale);
     params[d] = make_float2(scale, zero);
     for (uint32_t t = 0; t < G; ++t)
       codes_lds[t * D + d] = static_cast<uint8_t>(quant_code(rows[(uint64_t)t * D + d], zero, scale, levels));
   }
-  __syncthreads();
+  raise_max(c.smax + 2 * unit, smax);  // includes the barrier before the packing below
   const uint32_t ppw = geo.ppw();
   const uint32_t kw = geo.kwords_per_token();
   uint32_t* words = c.kcodes + unit * geo.kcodes_unit() + (g0 + g) * G * kw;
@@ -102,7 +117,7 @@ __global__ void __launch_bounds__(kThreads)
     const uint32_t t = w / kw, j = w % kw;
     const uint8_t* cc = codes_lds + t * D + j * ppw;
     uint32_t word = 0;
-    for (uint32_t i = 0; i < ppw; ++i) word |= static_cast<uint32_t>(cc[i]) << (bits * i);
+    for (uint32_t i = 0; i < ppw; ++i) word |= static_cast<uint32_t>(cc[i]) << code_shift(bits, i);
     words[w] = word;
   }
 }
@@ -126,6 +141,7 @@ __global__ void __launch_bounds__(kThreads)
   const uint64_t t_hi = t_end < (tb + 1) * kValueBlock ? t_end : (tb + 1) * kValueBlock;
   const uint32_t ntok = static_cast<uint32_t>(t_hi - t_lo);
   float2* params = reinterpret_cast<float2*>(c.vparams + unit * geo.vparams_unit());
+  float smax = 0.f;
   for (uint32_t p = threadIdx.x; p < ntok * ncg; p += blockDim.x) {
     const uint32_t k = p / ncg, cg = p % ncg;
     const uint64_t t = t_lo + k;
@@ -139,12 +155,13 @@ __global__ void __launch_bounds__(kThreads)
       mx = fmaxf(mx, grp[e]);
     }
     const float scale = scale_of(mx - mn, levels);
+    smax = fmaxf(smax, scale);
     const uint32_t tt = static_cast<uint32_t>(t % kValueBlock);
     params[(tb * ncg + cg) * kValueBlock + tt] = make_float2(scale, mn);
     uint8_t* dst = codes_lds + tt * D + cg * G;
     for (uint32_t e = 0; e < G; ++e) dst[e] = static_cast<uint8_t>(quant_code(grp[e], mn, scale, levels));
   }
-  __syncthreads();
+  raise_max(c.smax + 2 * unit + 1, smax);  // includes the barrier before the packing below
   const uint32_t ppw = geo.ppw();
   const uint32_t vw = geo.vwords_per_channel();
   const uint32_t w_lo = static_cast<uint32_t>(t_lo % kValueBlock) / ppw;
@@ -158,7 +175,7 @@ __global__ void __launch_bounds__(kThreads)
     for (uint32_t i = 0; i < ppw; ++i) {
       const uint64_t t = tb * kValueBlock + w * ppw + i;
       if (t >= t_lo && t < t_hi) {
-        word |= static_cast<uint32_t>(codes_lds[(t % kValueBlock) * D + d]) << (bits * i);
+        word |= static_cast<uint32_t>(codes_lds[(t % kValueBlock) * D + d]) << code_shift(bits, i);
       } else if (t < t_lo) {
         keep_old = true;
       }
@@ -191,7 +208,7 @@ __global__ void __launch_bounds__(kThreads)
     uint32_t word = 0;
     for (uint32_t i = 0; i < ppw; ++i) {
       const uint64_t t = g * G + w * ppw + i;
-      const uint32_t code = (src[t * kw + d / ppw] >> (bits * (d % ppw))) & mask;
+      const uint32_t code = (src[t * kw + d / ppw] >> code_shift(bits, d % ppw)) & mask;
       word |= code << (bits * i);
     }
     out[idx] = word;
@@ -221,7 +238,7 @@ __global__ void __launch_bounds__(kThreads)
     uint32_t word = 0;
     for (uint32_t i = 0; i < ppw; ++i) {
       const uint32_t d = j * ppw + i;
-      const uint32_t code = (src[(uint64_t)d * vw + tt / ppw] >> (bits * (tt % ppw))) & mask;
+      const uint32_t code = (src[(uint64_t)d * vw + tt / ppw] >> code_shift(bits, tt % ppw)) & mask;
       word |= code << (bits * i);
     }
     out_codes[idx] = word;
@@ -254,7 +271,7 @@ __global__ void __launch_bounds__(kThreads)
     float k, v;
     if (t < s.kq) {
       const uint32_t word = c.kcodes[unit * geo.kcodes_unit() + t * kw + d / ppw];
-      const float code = static_cast<float>((word >> (bits * (d % ppw))) & mask);
+      const float code = static_cast<float>((word >> code_shift(bits, d % ppw)) & mask);
       const float2 sz = reinterpret_cast<const float2*>(c.kparams + unit * geo.kparams_unit())[(t / G) * D + d];
       k = fmaf(code, sz.x, sz.y);
     } else {
@@ -264,7 +281,7 @@ __global__ void __launch_bounds__(kThreads)
       const uint64_t tb = t / kValueBlock;
       const uint32_t tt = t % kValueBlock;
       const uint32_t word = c.vcodes[unit * geo.vcodes_unit() + (tb * D + d) * vw + tt / ppw];
-      const float code = static_cast<float>((word >> (bits * (tt % ppw))) & mask);
+      const float code = static_cast<float>((word >> code_shift(bits, tt % ppw)) & mask);
       const float2 sz = reinterpret_cast<const float2*>(c.vparams + unit * geo.vparams_unit())
           [(tb * ncg + d / G) * kValueBlock + tt];
       v = fmaf(code, sz.x, sz.y);
