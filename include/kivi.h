@@ -22,6 +22,9 @@
  *  - Host-pointer entry points are synchronous: on return the caller's buffers may be
  *    reused and outputs are complete. `*_device` entry points take device pointers and
  *    a hipStream_t (as void*), enqueue work on that stream and return without waiting.
+ *    Attention calls on one cache (or one session) reuse its device workspace: a call on
+ *    a different stream than the previous one first waits for the previous stream's work,
+ *    so that stream must still exist then (or the cache / session must be freed first).
  *  - Threading follows the reference's borrow rules: at most one mutating call
  *    (append, reserve, prefill, decode) in flight per cache; read-only calls
  *    (attention, dequantize, export, getters) may share a cache but must not overlap

@@ -21,7 +21,7 @@
 #include <string>
 #include <vector>
 
-#include "../../include/kivi.h"
+#include "kivi.h"
 #include "common.hpp"
 
 namespace kivi {
@@ -515,14 +515,15 @@ size_t compressed_bytes(const kivi_memory_report& r) {
          r.key_residual_bytes + r.value_residual_bytes;
 }
 
-// Split counters of one attention target (a cache or a session): the last split workgroup
-// of a unit merges it and re-arms its counter, so two calls sharing the counters must not
-// overlap on the device. Calls on one stream are ordered by the stream; a call on another
-// stream waits for the event recorded after the previous call.
+// Split counters and workspace of one attention target (a cache or a session). Two calls
+// sharing them must not overlap on the device: calls on one stream are ordered by the stream;
+// when a call comes on another stream, an event recorded at that moment on the previous
+// call's stream is waited for first (no per-call event, which would stall the queue).
 struct AttnSync {
   DevBuf counters;
+  DevBuf workspace;  // split partials, grown on demand
   hipEvent_t done = nullptr;
-  bool pending = false;
+  bool used = false;
   hipStream_t last = nullptr;
   std::mutex mu;
   AttnSync() = default;
@@ -537,13 +538,29 @@ struct AttnSync {
     return Status{};
   }
   Status before(hipStream_t s) {
-    if (pending && s != last) HIP_TRY(hipStreamWaitEvent(s, done, 0), "attention ordering");
+    if (used && s != last) {
+      HIP_TRY(hipEventRecord(done, last), "attention ordering");
+      HIP_TRY(hipStreamWaitEvent(s, done, 0), "attention ordering");
+    }
     return Status{};
   }
   Status after(hipStream_t s) {
-    HIP_TRY(hipEventRecord(done, s), "attention ordering");
-    pending = true;
+    used = true;
     last = s;
+    return Status{};
+  }
+  // Waits until the last call's work is done (before freeing or regrowing).
+  Status drain() {
+    if (used) HIP_TRY(hipStreamSynchronize(last), "attention drain");
+    return Status{};
+  }
+  // Workspace of at least `bytes`; growing waits for the previous call to finish with it.
+  Status reserve(size_t bytes) {
+    if (bytes <= workspace.bytes) return Status{};
+    KIVI_TRY(drain());
+    workspace.release();
+    HIP_TRY(hipMalloc(&workspace.p, bytes), "attention workspace");
+    workspace.bytes = bytes;
     return Status{};
   }
 };
@@ -575,11 +592,10 @@ Status attend(const CacheCore& core, AttnSync& sync, const float* suffix_k, cons
   p.batch = static_cast<uint32_t>(core.batch);
   p.scale = scale;
   p.counters = sync.counters.as<uint32_t>();
-  Scratch ws;
-  KIVI_TRY(ws.get(attention_workspace_floats(p) * sizeof(float), s, "attention workspace"));
   std::lock_guard<std::mutex> lock(sync.mu);
+  KIVI_TRY(sync.reserve(attention_workspace_floats(p) * sizeof(float)));
   KIVI_TRY(sync.before(s));
-  HIP_TRY(launch_attention(p, ws.as<float>(), s), "attention");
+  HIP_TRY(launch_attention(p, sync.workspace.as<float>(), s), "attention");
   KIVI_TRY(sync.after(s));
   return Status{};
 }
@@ -978,7 +994,7 @@ void kivi_cache_free(kivi_cache* cache) {
   if (cache == nullptr) return;
   DeviceScope scope(cache->core.device);
   (void)hipStreamSynchronize(cache->core.stream);
-  if (cache->attn.pending) (void)hipEventSynchronize(cache->attn.done);
+  (void)cache->attn.drain();
   delete cache;
 }
 
@@ -1265,7 +1281,7 @@ void kivi_runtime_free(kivi_runtime* rt) {
   if (rt == nullptr) return;
   DeviceScope scope(rt->cache.core.device);
   (void)hipStreamSynchronize(rt->cache.core.stream);
-  if (rt->cache.attn.pending) (void)hipEventSynchronize(rt->cache.attn.done);
+  (void)rt->cache.attn.drain();
   delete rt;
 }
 
