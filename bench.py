@@ -163,6 +163,15 @@ def main():
     log(f"[bench] building inputs {desc}")
     k, v, q = gpu_inputs(torch, batch, heads, qh, dim, seq, 2001)
     out = torch.empty((batch, qh, dim), device="cuda", dtype=torch.float32)
+    # warm-up: a small cache of the same shape loads the kernels' code objects before timing
+    warm = kivi.KiviCache(amd, kivi.KiviConfig(bits, G, R), 1, heads, dim)
+    wk = torch.randn((1, heads, 4 * R, dim), device="cuda", dtype=torch.float32)
+    warm.append_device(wk.data_ptr(), wk.numel(), wk.data_ptr(), wk.numel(), 4 * R, sp)
+    wq = torch.randn((1, qh, dim), device="cuda", dtype=torch.float32)
+    wo = torch.empty_like(wq)
+    warm.attention_device(wq.data_ptr(), wq.numel(), qh, 0.1, wo.data_ptr(), wo.numel(), sp)
+    stream.synchronize()
+    del warm, wk, wq, wo
     cache = kivi.KiviCache(amd, kivi.KiviConfig(bits, G, R), batch, heads, dim)
     cache.reserve(seq)
     torch.cuda.synchronize()

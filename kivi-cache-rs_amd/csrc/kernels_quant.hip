@@ -9,6 +9,8 @@
 #include "common.hpp"
 #include "kivi.h"
 
+#include <algorithm>
+
 namespace kivi {
 namespace {
 
@@ -80,25 +82,55 @@ __global__ void __launch_bounds__(kThreads)
   }
 }
 
+// Rows are staged through LDS as floats [rows][D+1] (the odd stride spreads a column over the
+// banks) by coalesced reads, float4 when `vec4`; at most kStageFloats floats per pass.
+constexpr uint32_t kStageFloats = 8704;  // 34 KiB
+
+__device__ __forceinline__ void stage_row(const float* src, float* dst, uint32_t D, bool vec4,
+                                          uint32_t part, uint32_t parts) {
+  if (vec4) {
+    for (uint32_t c4 = part; c4 < D / 4; c4 += parts) {
+      const float4 v = reinterpret_cast<const float4*>(src)[c4];
+      dst[4 * c4] = v.x;
+      dst[4 * c4 + 1] = v.y;
+      dst[4 * c4 + 2] = v.z;
+      dst[4 * c4 + 3] = v.w;
+    }
+  } else {
+    for (uint32_t c = part; c < D; c += parts) dst[c] = src[c];
+  }
+}
+
 // ------------------------------------------------------------------ keys (native layout)
 // One workgroup per (unit, group): per-channel min/max over the group's G tokens
 // (src/quant.rs:296-306), (scale, zero) per channel (:307-311), codes for every token
-// (:312-323), then token-major words.
+// (:312-323), then token-major words. The G x D block is staged in LDS in one coalesced pass
+// when it fits (`staged`), else read from global memory directly.
 __global__ void __launch_bounds__(kThreads)
-    k_quant_keys(CacheView c, RowSource src, uint64_t g0, uint32_t ngroups) {
-  extern __shared__ uint8_t codes_lds[];  // [G][D]
+    k_quant_keys(CacheView c, RowSource src, uint64_t g0, uint32_t ngroups, uint32_t staged,
+                 uint32_t vec4) {
+  extern __shared__ uint8_t smem[];
   const Geometry& geo = c.geo;
   const uint32_t G = geo.G, D = geo.D, bits = geo.bits;
+  uint8_t* codes_lds = smem;                                                // [G][D]
+  float* xs = reinterpret_cast<float*>(smem + ((size_t)G * D + 15) / 16 * 16);  // [G][D+1]
   const float levels = static_cast<float>(geo.levels());
   const uint32_t unit = blockIdx.x / ngroups;
   const uint32_t g = blockIdx.x % ngroups;
   const float* rows = src.base + unit * src.stride_unit + (src.offset + (uint64_t)g * G) * D;
   float2* params = reinterpret_cast<float2*>(c.kparams + unit * geo.kparams_unit() + (g0 + g) * D * 2);
+  if (staged) {
+    // a wave per row at a time, all rows' loads in flight across the workgroup
+    const uint32_t lanes = 64, waves = blockDim.x / 64;
+    for (uint32_t t = threadIdx.x / lanes; t < G; t += waves)
+      stage_row(rows + (uint64_t)t * D, xs + t * (D + 1), D, vec4 != 0, threadIdx.x % lanes, lanes);
+    __syncthreads();
+  }
   float smax = 0.f;
   for (uint32_t d = threadIdx.x; d < D; d += blockDim.x) {
     float mn = INFINITY, mx = -INFINITY;
     for (uint32_t t = 0; t < G; ++t) {
-      const float x = rows[(uint64_t)t * D + d];
+      const float x = staged ? xs[t * (D + 1) + d] : rows[(uint64_t)t * D + d];
       mn = fminf(mn, x);
       mx = fmaxf(mx, x);
     }
@@ -106,8 +138,10 @@ __global__ void __launch_bounds__(kThreads)
     const float scale = scale_of(mx - zero, levels);
     smax = fmaxf(smax, scale);
     params[d] = make_float2(scale, zero);
-    for (uint32_t t = 0; t < G; ++t)
-      codes_lds[t * D + d] = static_cast<uint8_t>(quant_code(rows[(uint64_t)t * D + d], zero, scale, levels));
+    for (uint32_t t = 0; t < G; ++t) {
+      const float x = staged ? xs[t * (D + 1) + d] : rows[(uint64_t)t * D + d];
+      codes_lds[t * D + d] = static_cast<uint8_t>(quant_code(x, zero, scale, levels));
+    }
   }
   raise_max(c.smax + 2 * unit, smax);  // includes the barrier before the packing below
   const uint32_t ppw = geo.ppw();
@@ -123,16 +157,19 @@ __global__ void __launch_bounds__(kThreads)
 }
 
 // ------------------------------------------------------------------ values (native layout)
-// One workgroup per (unit, 64-token block touched). Phase 1: one thread per (token,
-// channel group) computes min/max, (scale, zero) and codes (src/quant.rs:349-375).
-// Phase 2: one thread per channel-major word; words that already hold earlier tokens
-// of the block are read, OR-ed and written back (blocks fill across appends).
+// One workgroup per (unit, 64-token block touched). Phase 1, per batch of TB tokens: the rows
+// are staged in LDS (coalesced), then one thread per (token, channel group) computes min/max,
+// (scale, zero) and codes (src/quant.rs:349-375). Phase 2: one thread per channel-major word;
+// words that already hold earlier tokens of the block are read, OR-ed and written back
+// (blocks fill across appends).
 __global__ void __launch_bounds__(kThreads)
     k_quant_values(CacheView c, RowSource ring, uint32_t n_ring, RowSource in, uint64_t vq0,
-                   uint64_t n, uint64_t blk0, uint32_t nblk) {
-  extern __shared__ uint8_t codes_lds[];  // [64][D]
+                   uint64_t n, uint64_t blk0, uint32_t nblk, uint32_t TB, uint32_t vec4) {
+  extern __shared__ uint8_t smem[];
   const Geometry& geo = c.geo;
   const uint32_t G = geo.G, D = geo.D, bits = geo.bits, R = geo.R, ncg = geo.ncg();
+  uint8_t* codes_lds = smem;                                                        // [64][D]
+  float* xs = reinterpret_cast<float*>(smem + ((size_t)kValueBlock * D + 15) / 16 * 16);  // [TB][D+1]
   const float levels = static_cast<float>(geo.levels());
   const uint32_t unit = blockIdx.x / nblk;
   const uint64_t tb = blk0 + blockIdx.x % nblk;
@@ -142,24 +179,33 @@ __global__ void __launch_bounds__(kThreads)
   const uint32_t ntok = static_cast<uint32_t>(t_hi - t_lo);
   float2* params = reinterpret_cast<float2*>(c.vparams + unit * geo.vparams_unit());
   float smax = 0.f;
-  for (uint32_t p = threadIdx.x; p < ntok * ncg; p += blockDim.x) {
-    const uint32_t k = p / ncg, cg = p % ncg;
-    const uint64_t t = t_lo + k;
-    const uint64_t i = t - vq0;
-    const float* row = i < n_ring ? source_row(ring, unit, i, R, D)
-                                  : source_row(in, unit, i - n_ring, R, D);
-    const float* grp = row + cg * G;
-    float mn = INFINITY, mx = -INFINITY;
-    for (uint32_t e = 0; e < G; ++e) {
-      mn = fminf(mn, grp[e]);
-      mx = fmaxf(mx, grp[e]);
+  const uint32_t lanes = 64, waves = blockDim.x / 64;
+  for (uint32_t k0 = 0; k0 < ntok; k0 += TB) {
+    const uint32_t nb = ntok - k0 < TB ? ntok - k0 : TB;
+    for (uint32_t r = threadIdx.x / lanes; r < nb; r += waves) {
+      const uint64_t i = t_lo + k0 + r - vq0;
+      const float* row = i < n_ring ? source_row(ring, unit, i, R, D) : source_row(in, unit, i - n_ring, R, D);
+      stage_row(row, xs + r * (D + 1), D, vec4 != 0, threadIdx.x % lanes, lanes);
     }
-    const float scale = scale_of(mx - mn, levels);
-    smax = fmaxf(smax, scale);
-    const uint32_t tt = static_cast<uint32_t>(t % kValueBlock);
-    params[(tb * ncg + cg) * kValueBlock + tt] = make_float2(scale, mn);
-    uint8_t* dst = codes_lds + tt * D + cg * G;
-    for (uint32_t e = 0; e < G; ++e) dst[e] = static_cast<uint8_t>(quant_code(grp[e], mn, scale, levels));
+    __syncthreads();
+    // token fastest, so neighbouring threads read neighbouring rows (distinct banks)
+    for (uint32_t p = threadIdx.x; p < nb * ncg; p += blockDim.x) {
+      const uint32_t r = p % nb, cg = p / nb;
+      const float* grp = xs + r * (D + 1) + cg * G;
+      float mn = INFINITY, mx = -INFINITY;
+      for (uint32_t e = 0; e < G; ++e) {
+        mn = fminf(mn, grp[e]);
+        mx = fmaxf(mx, grp[e]);
+      }
+      const float scale = scale_of(mx - mn, levels);
+      smax = fmaxf(smax, scale);
+      const uint64_t t = t_lo + k0 + r;
+      const uint32_t tt = static_cast<uint32_t>(t % kValueBlock);
+      params[(tb * ncg + cg) * kValueBlock + tt] = make_float2(scale, mn);
+      uint8_t* dst = codes_lds + tt * D + cg * G;
+      for (uint32_t e = 0; e < G; ++e) dst[e] = static_cast<uint8_t>(quant_code(grp[e], mn, scale, levels));
+    }
+    __syncthreads();  // the staging buffer is refilled by the next batch
   }
   raise_max(c.smax + 2 * unit + 1, smax);  // includes the barrier before the packing below
   const uint32_t ppw = geo.ppw();
@@ -176,6 +222,165 @@ __global__ void __launch_bounds__(kThreads)
       const uint64_t t = tb * kValueBlock + w * ppw + i;
       if (t >= t_lo && t < t_hi) {
         word |= static_cast<uint32_t>(codes_lds[(t % kValueBlock) * D + d]) << code_shift(bits, i);
+      } else if (t < t_lo) {
+        keep_old = true;
+      }
+    }
+    uint32_t* dst = base + (uint64_t)d * vw + w;
+    if (keep_old) word |= *dst;
+    *dst = word;
+  }
+}
+
+// ------------------------------------------------------------------ wave-per-item fast paths
+// For head_dim = 64*CPL (CPL = 1, 2, 4): lane l of a wave holds channels CPL*l .. +CPL-1 of a
+// row, so every row is one coalesced wave load and the quantization runs in registers; only
+// the codes go through LDS for the packing.
+
+template <int CPL>
+__device__ __forceinline__ void load_lane(const float* row, uint32_t lane, float (&x)[CPL]) {
+  if constexpr (CPL == 4) {
+    const float4 v = reinterpret_cast<const float4*>(row)[lane];
+    x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
+  } else if constexpr (CPL == 2) {
+    const float2 v = reinterpret_cast<const float2*>(row)[lane];
+    x[0] = v.x; x[1] = v.y;
+  } else {
+    x[0] = row[lane];
+  }
+}
+
+__device__ __forceinline__ void wave_raise_max(uint32_t* smax, float v) {
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  if (threadIdx.x % 64 == 0) atomicMax(smax, __float_as_uint(v));
+}
+
+// Keys: wave w of a workgroup takes item blockIdx.x*4 + w = (unit, group); the lane keeps its
+// channels of all GG rows in registers for the per-channel min/max (src/quant.rs:296-311).
+template <int CPL, int GG>
+__global__ void __launch_bounds__(kThreads)
+    k_quant_keys_wave(CacheView c, RowSource src, uint64_t g0, uint32_t ngroups, uint32_t items) {
+  constexpr uint32_t D = 64 * CPL;
+  __shared__ uint8_t codes_all[4][GG * D];  // per wave [G][D]
+  const Geometry& geo = c.geo;
+  const uint32_t bits = geo.bits;
+  const float levels = static_cast<float>(geo.levels());
+  const uint32_t lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+  const uint32_t item = blockIdx.x * 4 + wave;
+  const bool active = item < items;
+  const uint32_t unit = active ? item / ngroups : 0, g = active ? item % ngroups : 0;
+  uint8_t* codes = codes_all[wave];
+  if (active) {
+    const float* rows = src.base + unit * src.stride_unit + (src.offset + (uint64_t)g * GG) * D;
+    float x[GG][CPL];
+#pragma unroll
+    for (int t = 0; t < GG; ++t) load_lane<CPL>(rows + (uint64_t)t * D, lane, x[t]);
+    float smax = 0.f;
+    float2 sz[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      float mn = INFINITY, mx = -INFINITY;
+#pragma unroll
+      for (int t = 0; t < GG; ++t) {
+        mn = fminf(mn, x[t][j]);
+        mx = fmaxf(mx, x[t][j]);
+      }
+      sz[j] = make_float2(scale_of(mx - mn, levels), mn);
+      smax = fmaxf(smax, sz[j].x);
+#pragma unroll
+      for (int t = 0; t < GG; ++t)
+        codes[t * D + CPL * lane + j] = static_cast<uint8_t>(quant_code(x[t][j], sz[j].y, sz[j].x, levels));
+    }
+    float2* params = reinterpret_cast<float2*>(c.kparams + unit * geo.kparams_unit() + (g0 + g) * D * 2);
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) params[CPL * lane + j] = sz[j];
+    wave_raise_max(c.smax + 2 * unit, smax);
+  }
+  __syncthreads();
+  if (active) {
+    const uint32_t ppw = geo.ppw(), kw = D / ppw;
+    uint32_t* words = c.kcodes + unit * geo.kcodes_unit() + (g0 + g) * GG * kw;
+    for (uint32_t w = lane; w < GG * kw; w += 64) {
+      const uint32_t t = w / kw, jw = w % kw;
+      const uint8_t* cc = codes + t * D + jw * ppw;
+      uint32_t word = 0;
+      for (uint32_t i = 0; i < ppw; ++i) word |= static_cast<uint32_t>(cc[i]) << code_shift(bits, i);
+      words[w] = word;
+    }
+  }
+}
+
+// Values: one workgroup per (unit, 64-token block); wave w takes rows w, w+4, ...; the group
+// min/max (src/quant.rs:349-375) reduces over the G/CPL lanes of a channel group by shuffles.
+template <int CPL>
+__global__ void __launch_bounds__(kThreads)
+    k_quant_values_wave(CacheView c, RowSource ring, uint32_t n_ring, RowSource in, uint64_t vq0,
+                        uint64_t n, uint64_t blk0, uint32_t nblk) {
+  constexpr uint32_t D = 64 * CPL;
+  __shared__ uint8_t codes_lds[kValueBlock * D];
+  const Geometry& geo = c.geo;
+  const uint32_t G = geo.G, bits = geo.bits, R = geo.R, ncg = geo.ncg();
+  const uint32_t L = G / CPL;  // lanes per channel group (a power of two)
+  const float levels = static_cast<float>(geo.levels());
+  const uint32_t lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+  const uint32_t unit = blockIdx.x / nblk;
+  const uint64_t tb = blk0 + blockIdx.x % nblk;
+  const uint64_t t_lo = vq0 > tb * kValueBlock ? vq0 : tb * kValueBlock;
+  const uint64_t t_end = vq0 + n;
+  const uint64_t t_hi = t_end < (tb + 1) * kValueBlock ? t_end : (tb + 1) * kValueBlock;
+  const uint32_t ntok = static_cast<uint32_t>(t_hi - t_lo);
+  float2* params = reinterpret_cast<float2*>(c.vparams + unit * geo.vparams_unit());
+  const uint32_t cg = CPL * lane / G;
+  float smax = 0.f;
+  // rows wave, wave+4, ... in batches of kRows, every batch's loads issued before its math
+  constexpr uint32_t kRows = 4;
+  for (uint32_t r0 = wave; r0 < ntok; r0 += 4 * kRows) {
+    float x[kRows][CPL];
+#pragma unroll
+    for (uint32_t b = 0; b < kRows; ++b) {
+      const uint32_t r = std::min<uint32_t>(r0 + 4 * b, ntok - 1);  // clamped: always a valid row
+      const uint64_t i = t_lo + r - vq0;
+      const float* row = i < n_ring ? source_row(ring, unit, i, R, D) : source_row(in, unit, i - n_ring, R, D);
+      load_lane<CPL>(row, lane, x[b]);
+    }
+#pragma unroll
+    for (uint32_t b = 0; b < kRows; ++b) {
+      const uint32_t r = r0 + 4 * b;
+      if (r >= ntok) break;
+      float mn = x[b][0], mx = x[b][0];
+#pragma unroll
+      for (int j = 1; j < CPL; ++j) {
+        mn = fminf(mn, x[b][j]);
+        mx = fmaxf(mx, x[b][j]);
+      }
+      for (uint32_t o = 1; o < L; o <<= 1) {
+        mn = fminf(mn, __shfl_xor(mn, o));
+        mx = fmaxf(mx, __shfl_xor(mx, o));
+      }
+      const float scale = scale_of(mx - mn, levels);
+      smax = fmaxf(smax, scale);
+      const uint32_t tt = static_cast<uint32_t>((t_lo + r) % kValueBlock);
+      if (lane % L == 0) params[(tb * ncg + cg) * kValueBlock + tt] = make_float2(scale, mn);
+#pragma unroll
+      for (int j = 0; j < CPL; ++j)
+        codes_lds[tt * D + CPL * lane + j] = static_cast<uint8_t>(quant_code(x[b][j], mn, scale, levels));
+    }
+  }
+  raise_max(c.smax + 2 * unit + 1, smax);  // includes the barrier before the packing below
+  const uint32_t ppw = geo.ppw();
+  const uint32_t vw = geo.vwords_per_channel();
+  const uint32_t w_lo = static_cast<uint32_t>(t_lo % kValueBlock) / ppw;
+  const uint32_t w_hi = static_cast<uint32_t>((t_hi - 1) % kValueBlock) / ppw + 1;
+  const uint32_t nw = w_hi - w_lo;
+  uint32_t* base = c.vcodes + unit * geo.vcodes_unit() + tb * D * vw;
+  for (uint32_t idx = threadIdx.x; idx < D * nw; idx += blockDim.x) {
+    const uint32_t d = idx / nw, w = w_lo + idx % nw;
+    uint32_t word = 0;
+    bool keep_old = false;
+    for (uint32_t k = 0; k < ppw; ++k) {
+      const uint64_t t = tb * kValueBlock + w * ppw + k;
+      if (t >= t_lo && t < t_hi) {
+        word |= static_cast<uint32_t>(codes_lds[(t % kValueBlock) * D + d]) << code_shift(bits, k);
       } else if (t < t_lo) {
         keep_old = true;
       }
@@ -429,15 +634,40 @@ hipError_t launch_copy_rows(const Geometry& g, RowSource src, float* dst, uint32
   return hipGetLastError();
 }
 
+bool rows_vec4(const RowSource& r, uint32_t D) {
+  return reinterpret_cast<uintptr_t>(r.base) % 16 == 0 && D % 4 == 0 && r.stride_unit % 4 == 0;
+}
+
 hipError_t launch_quant_keys(const CacheView& c, RowSource src, uint64_t g0, uint32_t ngroups,
                              hipStream_t stream) {
   if (ngroups == 0) return hipSuccess;
   const uint64_t blocks = (uint64_t)c.geo.units * ngroups;
-  const size_t lds = (size_t)c.geo.G * c.geo.D;
+  const size_t codes = ((size_t)c.geo.G * c.geo.D + 15) / 16 * 16;
+  const bool staged = (size_t)c.geo.G * (c.geo.D + 1) <= kStageFloats;
+  const size_t lds = codes + (staged ? (size_t)c.geo.G * (c.geo.D + 1) * sizeof(float) : 0);
   const double rows = (double)blocks * c.geo.G;
   TimedLaunch timed(KIVI_KERNEL_QUANT_KEYS, stream,
                     rows * c.geo.D * (4.0 + c.geo.bits / 8.0) + (double)blocks * c.geo.D * 8.0);
-  k_quant_keys<<<static_cast<unsigned>(blocks), kThreads, lds, stream>>>(c, src, g0, ngroups);
+  const uint32_t cpl = c.geo.D / 64;
+  const bool lane_aligned = c.geo.D % 64 == 0 && reinterpret_cast<uintptr_t>(src.base) % (4 * cpl) == 0 &&
+                            src.stride_unit % (4 * cpl) == 0 && blocks <= (1ull << 31);
+  if (lane_aligned) {
+    const uint32_t items = static_cast<uint32_t>(blocks);
+    const unsigned grid = (items + 3) / 4;
+    switch (cpl * 1000 + c.geo.G) {
+      case 1016: k_quant_keys_wave<1, 16><<<grid, kThreads, 0, stream>>>(c, src, g0, ngroups, items); return hipGetLastError();
+      case 1032: k_quant_keys_wave<1, 32><<<grid, kThreads, 0, stream>>>(c, src, g0, ngroups, items); return hipGetLastError();
+      case 1064: k_quant_keys_wave<1, 64><<<grid, kThreads, 0, stream>>>(c, src, g0, ngroups, items); return hipGetLastError();
+      case 2016: k_quant_keys_wave<2, 16><<<grid, kThreads, 0, stream>>>(c, src, g0, ngroups, items); return hipGetLastError();
+      case 2032: k_quant_keys_wave<2, 32><<<grid, kThreads, 0, stream>>>(c, src, g0, ngroups, items); return hipGetLastError();
+      case 2064: k_quant_keys_wave<2, 64><<<grid, kThreads, 0, stream>>>(c, src, g0, ngroups, items); return hipGetLastError();
+      case 4016: k_quant_keys_wave<4, 16><<<grid, kThreads, 0, stream>>>(c, src, g0, ngroups, items); return hipGetLastError();
+      case 4032: k_quant_keys_wave<4, 32><<<grid, kThreads, 0, stream>>>(c, src, g0, ngroups, items); return hipGetLastError();
+      default: break;
+    }
+  }
+  k_quant_keys<<<static_cast<unsigned>(blocks), kThreads, lds, stream>>>(c, src, g0, ngroups, staged ? 1u : 0u,
+                                                                        rows_vec4(src, c.geo.D) ? 1u : 0u);
   return hipGetLastError();
 }
 
@@ -449,12 +679,35 @@ hipError_t launch_quant_values(const CacheView& c, RowSource ring, uint32_t n_ri
   const uint64_t blk1 = (vq0 + n - 1) / kValueBlock;
   const uint32_t nblk = static_cast<uint32_t>(blk1 - blk0 + 1);
   const uint64_t blocks = (uint64_t)c.geo.units * nblk;
-  const size_t lds = (size_t)kValueBlock * c.geo.D;
+  const uint32_t D = c.geo.D;
+  const uint32_t TB = std::max<uint32_t>(1, std::min<uint32_t>(kValueBlock, kStageFloats / (D + 1)));
+  const size_t lds = ((size_t)kValueBlock * D + 15) / 16 * 16 + (size_t)TB * (D + 1) * sizeof(float);
+  const bool vec4 = rows_vec4(ring, D) && (n_in == 0 || rows_vec4(in, D));
+  if (lds > 65536) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_quant_values),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    if (e != hipSuccess) return e;
+  }
   const double rows = (double)c.geo.units * n;
   TimedLaunch timed(KIVI_KERNEL_QUANT_VALUES, stream,
                     rows * (c.geo.D * (4.0 + c.geo.bits / 8.0) + c.geo.ncg() * 8.0));
+  const uint32_t cpl = D / 64;
+  const uint32_t lanes_per_group = cpl > 0 ? c.geo.G / cpl : 0;
+  auto aligned = [&](const RowSource& r) {
+    return reinterpret_cast<uintptr_t>(r.base) % (4 * cpl) == 0 && r.stride_unit % (4 * cpl) == 0;
+  };
+  if (D % 64 == 0 && (cpl == 1 || cpl == 2 || cpl == 4) && c.geo.G % cpl == 0 && lanes_per_group <= 64 &&
+      (lanes_per_group & (lanes_per_group - 1)) == 0 && aligned(ring) && (n_in == 0 || aligned(in))) {
+    if (cpl == 1)
+      k_quant_values_wave<1><<<static_cast<unsigned>(blocks), kThreads, 0, stream>>>(c, ring, n_ring, in, vq0, n, blk0, nblk);
+    else if (cpl == 2)
+      k_quant_values_wave<2><<<static_cast<unsigned>(blocks), kThreads, 0, stream>>>(c, ring, n_ring, in, vq0, n, blk0, nblk);
+    else
+      k_quant_values_wave<4><<<static_cast<unsigned>(blocks), kThreads, 0, stream>>>(c, ring, n_ring, in, vq0, n, blk0, nblk);
+    return hipGetLastError();
+  }
   k_quant_values<<<static_cast<unsigned>(blocks), kThreads, lds, stream>>>(c, ring, n_ring, in, vq0, n,
-                                                                         blk0, nblk);
+                                                                         blk0, nblk, TB, vec4 ? 1u : 0u);
   return hipGetLastError();
 }
 
