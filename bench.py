@@ -45,7 +45,12 @@ CONFIGS = {
            "config 2: batch 16, 32q/8kv heads, head_dim 128, 32768 cached tokens, 2-bit G=32 R=128"),
     "c3_4": (1, 8, 64, 128, 131072, 4, 32, 128, "config 3: batch 1, 64q/8kv heads, 131072 tokens, 4-bit"),
     "c3_8": (1, 8, 64, 128, 131072, 8, 32, 128, "config 3: batch 1, 64q/8kv heads, 131072 tokens, 8-bit"),
+    "c4": (1, 8, 32, 128, 65536, 2, 32, 128,
+           "config 4: one 65536-token 2-bit G=32 R=128 prefix (8 KV heads, head_dim 128) shared by "
+           "64 RagSessions with 96-token fp32 suffixes, 32 query heads, batched sessions attention"),
 }
+# batched-sessions workloads: name -> (sessions, suffix tokens per session)
+SESSIONS = {"c4": (64, 96)}
 
 
 def log(*a):
@@ -104,6 +109,47 @@ def cpu_baseline(kivi, cfg_tuple, target_s=12.0):
                   f"CPU path, single thread; prefill quantize {quant_bytes / t_quant / 1e9:.3f} GB/s",
         "quantize_gbps": quant_bytes / t_quant / 1e9,
         "ms_per_step": per_step * 1e3,
+        "cpu": _cpu_model(),
+    }
+
+
+def cpu_baseline_sessions(kivi, cfg_tuple, n_sessions, suffix, target_s=12.0):
+    """Oracle on the shared-prefix workload: the prefix once, then sessions one by one (the
+    reference's RagSession::attention, src/prefix.rs:223-289), timed per session."""
+    _, heads, qh, dim, seq, bits, G, R, _ = cfg_tuple
+    oracle = kivi.Backend.load(ROOT / "oracle" / "libkivi_oracle.so", "kivi_oracle_", device=False)
+    rng = np.random.default_rng(7)
+    k = rng.standard_normal((1, heads, seq, dim), dtype=np.float32)
+    for h, chans in enumerate(outlier_channels(heads, dim, 7)):
+        k[:, h, :, chans] *= 10.0
+    v = rng.standard_normal((1, heads, seq, dim), dtype=np.float32)
+    cache = kivi.KiviCache(oracle, kivi.KiviConfig(bits, G, R), 1, heads, dim)
+    cache.append(k, v, seq)
+    del k, v
+    prefix = cache.share_prefix()
+    del cache
+    scale = 1.0 / math.sqrt(dim)
+    reps, spent = 0, 0.0
+    while spent < target_s and reps < min(n_sessions, 5):
+        sess = prefix.session()
+        sk = rng.standard_normal((1, heads, suffix, dim), dtype=np.float32)
+        sv = rng.standard_normal((1, heads, suffix, dim), dtype=np.float32)
+        sess.append(sk, sv, suffix)
+        q = rng.standard_normal((1, qh, dim), dtype=np.float32)
+        t0 = time.perf_counter()
+        sess.attention(q, qh, scale)
+        spent += time.perf_counter() - t0
+        reps += 1
+    per_session = spent / reps
+    return {
+        "value": 1.0 / per_session,
+        "unit": "tokens/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"{reps} of the {n_sessions} sessions ({seq}-token prefix + {suffix}-token suffix, "
+                  f"{heads} KV / {qh} q heads): one RagSession decode attention each, C++ "
+                  f"restatement of the reference CPU path, single thread",
+        "ms_per_step": per_session * 1e3,
         "cpu": _cpu_model(),
     }
 
@@ -198,10 +244,39 @@ def main():
     torch.cuda.empty_cache()
 
     scale = 1.0 / math.sqrt(dim)
-    qp, op, n_q = q.data_ptr(), out.data_ptr(), q.numel()
+    sessions_cfg = SESSIONS.get(args.config)
+    if sessions_cfg:
+        # shared prefix + RagSessions with private fp32 suffixes; a step is one batched
+        # attention over all sessions (the prefix streamed once per step)
+        n_sess, suffix = sessions_cfg
+        prefix = cache.share_prefix()
+        del cache
+        torch.cuda.empty_cache()
+        sessions = [prefix.session() for _ in range(n_sess)]
+        gs = torch.Generator(device="cuda")
+        gs.manual_seed(2002)
+        for se in sessions:
+            sk = torch.randn((batch, heads, suffix, dim), generator=gs, device="cuda")
+            sv = torch.randn((batch, heads, suffix, dim), generator=gs, device="cuda")
+            se.append_device(sk.data_ptr(), sk.numel(), sv.data_ptr(), sv.numel(), suffix, sp)
+        stream.synchronize()
+        q = torch.randn((n_sess, batch, qh, dim), generator=gs, device="cuda")
+        out = torch.empty_like(q)
+        handles = kivi.session_handles(sessions)
+        qp, op, n_q = q.data_ptr(), out.data_ptr(), q.numel()
+        tokens_per_step = n_sess * batch
+        kv_bytes = prefix.prefix_bytes() + n_sess * batch * heads * suffix * dim * 4 * 2
 
-    def step():
-        cache.attention_device(qp, n_q, qh, scale, op, n_q, sp)
+        def step():
+            kivi.sessions_attention_device(amd, sessions, qp, n_q, qh, scale, op, n_q, sp,
+                                           handles=handles)
+    else:
+        qp, op, n_q = q.data_ptr(), out.data_ptr(), q.numel()
+        tokens_per_step = batch
+        kv_bytes = mem.compressed_bytes()
+
+        def step():
+            cache.attention_device(qp, n_q, qh, scale, op, n_q, sp)
 
     with torch.cuda.stream(stream):
         for _ in range(args.warmup):
@@ -247,13 +322,14 @@ def main():
         torch.cuda.synchronize()
         log(f"[bench] copy calibration: 3 x {args.copy_calibration} MiB device copies")
         del src, dst
-    algo_bytes = mem.compressed_bytes() + 2 * out.numel() * 4  # KV bytes + query + output
+    algo_bytes = kv_bytes + 2 * out.numel() * 4  # KV bytes + query + output
     eff_gbps = algo_bytes / per_step / 1e9
-    tokens_per_s = batch / per_step
+    tokens_per_s = tokens_per_step / per_step
     log(f"[bench] attention {per_step * 1e6:.1f} us/step, {eff_gbps:.0f} GB/s effective")
 
     dom = kernels.get("attn_packed") or kernels.get("attn_tail")
-    dom_name = "k_attn_mfma" if "attn_packed" in kernels else "k_attn_generic"
+    dom_name = ("k_attn_sessions" if sessions_cfg else "k_attn_mfma") if "attn_packed" in kernels \
+        else "k_attn_generic"
     achieved = dom["gbps"] if dom else eff_gbps
     rec = recorded_traffic(dom_name, args.config, dom["bytes_per_launch"]) if dom else None
     roofline = {
@@ -285,7 +361,9 @@ def main():
         "data": "synthetic",
         "config": {"workload": desc, "batch": batch, "kv_heads": heads, "q_heads": qh,
                    "head_dim": dim, "cached_tokens": seq, "bits": bits, "group_size": G,
-                   "residual_length": R},
+                   "residual_length": R,
+                   **({"sessions": sessions_cfg[0], "suffix_tokens": sessions_cfg[1]}
+                      if sessions_cfg else {})},
         "effective_hbm_gbps": eff_gbps,
         "hbm_fraction": eff_gbps / HBM_PEAK_GBPS,
         "quantize_gbps": quant_bytes / t_quant / 1e9,
@@ -295,7 +373,8 @@ def main():
     }
     if not args.no_cpu:
         log("[bench] CPU baseline (oracle, 1 thread) ...")
-        result["cpu_baseline"] = cpu_baseline(kivi, CONFIGS[args.config])
+        result["cpu_baseline"] = (cpu_baseline_sessions(kivi, CONFIGS[args.config], *sessions_cfg)
+                                  if sessions_cfg else cpu_baseline(kivi, CONFIGS[args.config]))
         log(f"[bench] CPU {result['cpu_baseline']['value']:.3f} tokens/s")
     print(json.dumps(result), flush=True)
 

@@ -188,19 +188,34 @@ struct AttnProblem {
 size_t attention_workspace_floats(const AttnProblem& p);
 hipError_t launch_attention(const AttnProblem& p, float* workspace, hipStream_t stream);
 
-// n sessions sharing one prefix: the prefix part of every session is computed in one pass
-// over the prefix; suffixes[i] (device, [units][L_i][D]) are per session.
+// One session of a batched call: its fp32 suffix ([units][*][D], `stride` floats between
+// units; k / v may be null when len is 0).
+struct SessionDesc {
+  const float* k;
+  const float* v;
+  uint64_t len;
+  uint64_t stride;
+};
+
+// Sessions of one batched launch; larger batches run in groups of this many (each group
+// streams the prefix once). Their descriptors travel in the kernel arguments (2 KB).
+constexpr uint32_t kMaxLaunchSessions = 64;
+struct SessionTable {
+  SessionDesc d[kMaxLaunchSessions];
+};
+
+// n sessions sharing one prefix: each workgroup of the prefix's packed chunks serves every
+// session in turn (the chunk data stays in L2 between sessions, so HBM sees the prefix once);
+// the prefix window and each session's suffix run per session. Returns hipErrorNotSupported
+// for shapes without the packed-chunk path (the caller then runs the sessions one by one).
 struct SessionsProblem {
   CacheView cache;
   SeqState st;
   uint64_t seq;
   uint32_t n;
-  const float* const* suffix_k;  // device array of n pointers
-  const float* const* suffix_v;
-  const uint64_t* suffix_len;    // device array of n lengths
-  uint64_t max_suffix;
-  const float* queries;  // [n][batch][QH][D]
-  float* out;            // [n][batch][QH][D]
+  const SessionDesc* sessions;  // host array of n (device suffix pointers)
+  const float* queries;         // [n][batch][QH][D]
+  float* out;                   // [n][batch][QH][D]
   uint32_t qh, heads, batch;
   float scale;
 };

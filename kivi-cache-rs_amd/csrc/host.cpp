@@ -634,6 +634,7 @@ struct kivi_cache {
 struct kivi_prefix_state {
   CacheCore core;
   size_t prefix_bytes = 0;
+  mutable AttnSync batch;  // workspace of batched session calls over this prefix
 };
 
 struct kivi_prefix {
@@ -834,10 +835,39 @@ Status batched_sessions(const kivi_session* const* sessions, size_t n, const flo
     dq = sq.as<float>();
     dout = so.as<float>();
   }
+  // One launch over the shared prefix per group of sessions when the packed-chunk path applies.
+  std::vector<SessionDesc> descs(n);
   for (size_t i = 0; i < n; ++i) {
-    kivi_session* se = const_cast<kivi_session*>(sessions[i]);  // counters only
-    KIVI_TRY(attend(core, se->attn, se->keys.as<float>(), se->values.as<float>(), se->len,
-                    se->cap * core.head_dim, dq + i * per, num_q_heads, scale, dout + i * per, s));
+    const kivi_session* se = sessions[i];
+    descs[i] = SessionDesc{se->keys.as<float>(), se->values.as<float>(), se->len, se->cap * core.head_dim};
+  }
+  SessionsProblem sp{};
+  sp.cache = core.view();
+  sp.st = core.state();
+  sp.seq = core.seq;
+  sp.n = static_cast<uint32_t>(n);
+  sp.sessions = descs.data();
+  sp.queries = dq;
+  sp.out = dout;
+  sp.qh = static_cast<uint32_t>(num_q_heads);
+  sp.heads = static_cast<uint32_t>(core.heads);
+  sp.batch = static_cast<uint32_t>(core.batch);
+  sp.scale = scale;
+  const size_t gq = num_q_heads / core.heads;
+  const size_t ws_floats = n <= UINT32_MAX ? sessions_workspace_floats(sp) : 0;
+  if (ws_floats > 0 && gq * core.head_dim <= kMaxGqD) {
+    AttnSync& sync_ = st->batch;
+    std::lock_guard<std::mutex> lock(sync_.mu);
+    KIVI_TRY(sync_.reserve(ws_floats * sizeof(float)));
+    KIVI_TRY(sync_.before(s));
+    HIP_TRY(launch_sessions_attention(sp, sync_.workspace.as<float>(), s), "sessions attention");
+    KIVI_TRY(sync_.after(s));
+  } else {
+    for (size_t i = 0; i < n; ++i) {
+      kivi_session* se = const_cast<kivi_session*>(sessions[i]);  // counters only
+      KIVI_TRY(attend(core, se->attn, se->keys.as<float>(), se->values.as<float>(), se->len,
+                      se->cap * core.head_dim, dq + i * per, num_q_heads, scale, dout + i * per, s));
+    }
   }
   if (!device) {
     HIP_TRY(hipMemcpyAsync(out, dout, all * 4, hipMemcpyDeviceToHost, s), "sessions D2H");
@@ -1137,6 +1167,7 @@ kivi_status kivi_cache_share_prefix(const kivi_cache* cache, kivi_prefix** out, 
     DeviceScope scope(cache->core.device);
     auto st = std::make_shared<kivi_prefix_state>();
     KIVI_TRY(cache->core.copy_into(st->core, cache->core.stream));
+    KIVI_TRY(st->batch.init(st->core.units(), cache->core.stream));
     KIVI_TRY(sync(cache->core.stream, "share_prefix"));
     st->prefix_bytes = compressed_bytes(st->core.memory());
     auto p = std::make_unique<kivi_prefix>();

@@ -63,6 +63,10 @@ struct AttnArgs {
   uint32_t nsplit_win;
   uint32_t nsplit_total;   // splits per unit in the workspace
   float* ws;               // [units][nsplit_total][gq][D+2]
+  // batched sessions (0 otherwise): session count and the strides between consecutive
+  // sessions' queries, partials and outputs
+  uint32_t nsess;
+  uint64_t q_sess_stride, ws_sess_stride;
   uint32_t* counters;      // [units] finished splits (0 between calls), or null: separate merge
   float* out;              // [batch][QH][D]
   uint32_t units;
@@ -948,14 +952,63 @@ __global__ void __launch_bounds__(kThreads) k_attn_mfma(AttnArgs a) {
   }
 }
 
+// Arguments of session s of a batched call: its queries, partials and suffix.
+__device__ __forceinline__ AttnArgs session_args(const AttnArgs& a, const SessionTable& t,
+                                                 uint32_t s) {
+  AttnArgs as = a;
+  const SessionDesc d = t.d[s];
+  as.query = a.query + s * a.q_sess_stride;
+  as.ws = a.ws + s * a.ws_sess_stride;
+  as.suffix_k = d.k;
+  as.suffix_v = d.v;
+  as.L = d.len;
+  as.suffix_stride = d.stride;
+  as.total = a.seq + d.len;
+  as.win_end = static_cast<uint32_t>((as.total + 63) / 64);
+  return as;
+}
+
+// Packed chunks per wave in a batched-sessions launch: a workgroup's chunks (4*kSessCpw*8 KB at
+// 2-bit) are re-read for every session, so they are kept few enough to stay cache resident.
+constexpr int kSessCpw = 4;
+
+// Batched sessions over one prefix: workgroups [0, nsess*units*nsplit_win) take one window /
+// suffix chunk of one session; the rest one packed-chunk split of a unit, for every session
+// in turn (the split's chunks are re-read from L2, not HBM, after the first session).
+template <int BITS, int NRS>
+__global__ void __launch_bounds__(kThreads) k_attn_sessions(AttnArgs a, SessionTable t) {
+  extern __shared__ float lds[];
+  const uint32_t per_sess = a.units * a.nsplit_win;
+  const uint32_t nwin = a.nsess * per_sess;
+  if (blockIdx.x < nwin) {
+    const uint32_t s = blockIdx.x / per_sess, r = blockIdx.x % per_sess;
+    const AttnArgs as = session_args(a, t, s);
+    mfma_split<BITS, NRS, 1, true>(as, r / a.nsplit_win, r % a.nsplit_win, lds);
+  } else {
+    const uint32_t blk = blockIdx.x - nwin;
+    const uint32_t unit = blk / a.nsplit_fast, split = blk % a.nsplit_fast;
+    for (uint32_t s = 0; s < a.nsess; ++s) {
+      AttnArgs as = a;
+      as.query = a.query + s * a.q_sess_stride;
+      as.ws = a.ws + s * a.ws_sess_stride;
+      mfma_split<BITS, NRS, kSessCpw, false>(as, unit, split, lds);
+      __syncthreads();  // the next session reuses the LDS
+    }
+  }
+}
+
 // Log-sum-exp merge of the split partials: one workgroup per (unit, head). LDS holds the
 // per-split factors 2^(m_s - M).
 __global__ void __launch_bounds__(kThreads)
     k_attn_merge(const float* ws, uint32_t nsplit, uint32_t gq, uint32_t D, uint32_t heads,
-                 uint32_t qh, float* out) {
+                 uint32_t qh, float* out, uint32_t units, uint64_t ws_sess_stride,
+                 uint64_t out_sess_stride) {
   extern __shared__ float f_lds[];  // [nsplit] factors, then 8 reduction slots
   float* red = f_lds + nsplit;
-  const uint32_t unit = blockIdx.x / gq, h = blockIdx.x % gq;
+  const uint32_t sess = blockIdx.x / (units * gq);
+  ws += sess * ws_sess_stride;
+  out += sess * out_sess_stride;
+  const uint32_t unit = (blockIdx.x / gq) % units, h = blockIdx.x % gq;
   const uint32_t b = unit / heads, kvh = unit % heads;
   const float* base = ws + (uint64_t)unit * nsplit * gq * (D + 2) + h * (D + 2);
   const uint64_t stride = (uint64_t)gq * (D + 2);
@@ -1038,6 +1091,8 @@ AttnArgs make_args(const AttnProblem& p, float* ws) {
   a.ws = ws;
   a.out = p.out;
   a.units = p.cache.geo.units;
+  a.nsess = 0;
+  a.q_sess_stride = a.ws_sess_stride = 0;
   // The in-kernel merge (last split per unit) needs device-scope release/acquire fences, which
   // on this multi-XCD part write back and invalidate L2 for every workgroup; the separate
   // merge launch is faster, so the counters stay unused for now.
@@ -1116,22 +1171,123 @@ hipError_t launch_attention(const AttnProblem& p, float* workspace, hipStream_t 
     const double bytes = (double)units * a.gq * ((double)a.nsplit_total * (g.D + 2) + g.D) * 4.0;
     TimedLaunch timed(KIVI_KERNEL_ATTN_MERGE, stream, bytes);
     k_attn_merge<<<units * a.gq, kThreads, merge_lds, stream>>>(workspace, a.nsplit_total, a.gq,
-                                                                g.D, p.heads, p.qh, p.out);
+                                                                g.D, p.heads, p.qh, p.out, units, 0, 0);
   }
   return hipGetLastError();
 }
 
+namespace {
+
+// Arguments of one launch group as one problem over the prefix (the window range is sized
+// for the group's longest suffix; each session clips it to its own).
+AttnArgs make_session_args(const SessionsProblem& sp, uint32_t nsess, uint64_t max_suffix, float* ws) {
+  AttnProblem p{};
+  p.cache = sp.cache;
+  p.st = sp.st;
+  p.seq = sp.seq;
+  p.suffix_len = max_suffix;
+  p.query = sp.queries;
+  p.out = sp.out;
+  p.qh = sp.qh;
+  p.heads = sp.heads;
+  p.batch = sp.batch;
+  p.scale = sp.scale;
+  AttnArgs a = make_args(p, ws);
+  a.counters = nullptr;
+  a.nsplit_fast = (a.chunk_end + 4 * kSessCpw - 1) / (4 * kSessCpw);
+  a.nsplit_total = a.nsplit_fast + a.nsplit_win + a.nsplit_gen;
+  a.nsess = nsess;
+  a.q_sess_stride = (uint64_t)sp.batch * sp.qh * sp.cache.geo.D;
+  a.ws_sess_stride = (uint64_t)sp.cache.geo.units * a.nsplit_total * a.gq * (sp.cache.geo.D + 2);
+  return a;
+}
+
+bool sessions_supported(const SessionsProblem& sp) {
+  AttnProblem p{};
+  p.cache = sp.cache;
+  p.st = sp.st;
+  p.qh = sp.qh;
+  p.heads = sp.heads;
+  return sp.n > 0 && fast_eligible(p) && sp.st.kq > 0;
+}
+
+uint64_t longest_suffix(const SessionsProblem& sp, uint32_t first, uint32_t count) {
+  uint64_t m = 0;
+  for (uint32_t i = first; i < first + count; ++i) m = std::max<uint64_t>(m, sp.sessions[i].len);
+  return m;
+}
+
+template <int BITS, int NRS>
+hipError_t launch_sessions(const AttnArgs& a, const SessionTable& t, hipStream_t stream) {
+  constexpr int NH = 4 * NRS;
+  const size_t logits = (size_t)4 * NH * ((a.nsplit_fast > 0 ? kSessCpw : 1) * 64 + kRowPad);
+  const size_t combine = (size_t)4 * NH * (128 + 2);
+  const size_t lds = std::max(logits, combine) * sizeof(float);
+  const uint32_t grid = a.nsess * a.units * a.nsplit_win + a.units * a.nsplit_fast;
+  k_attn_sessions<BITS, NRS><<<grid, kThreads, lds, stream>>>(a, t);
+  return hipGetLastError();
+}
+
+}  // namespace
+
 size_t sessions_workspace_floats(const SessionsProblem& p) {
-  (void)p;
-  return 0;
+  if (!sessions_supported(p)) return 0;
+  // the largest launch group: up to kMaxLaunchSessions sessions, window sized for the longest
+  // suffix of all
+  const uint32_t group = std::min(p.n, kMaxLaunchSessions);
+  const AttnArgs a = make_session_args(p, group, longest_suffix(p, 0, p.n), nullptr);
+  return (size_t)group * a.ws_sess_stride;
 }
 
 hipError_t launch_sessions_attention(const SessionsProblem& p, float* workspace,
                                      hipStream_t stream) {
-  (void)p;
-  (void)workspace;
-  (void)stream;
-  return hipErrorNotSupported;
+  if (!sessions_supported(p)) return hipErrorNotSupported;
+  const Geometry& g = p.cache.geo;
+  for (uint32_t first = 0; first < p.n; first += kMaxLaunchSessions) {
+    const uint32_t count = std::min(kMaxLaunchSessions, p.n - first);
+    SessionTable t{};
+    double suffix_rows = 0.0;
+    for (uint32_t i = 0; i < count; ++i) {
+      t.d[i] = p.sessions[first + i];
+      suffix_rows += 2.0 * (double)t.d[i].len;
+    }
+    SessionsProblem gp = p;
+    gp.queries = p.queries + (uint64_t)first * p.batch * p.qh * g.D;
+    gp.out = p.out + (uint64_t)first * p.batch * p.qh * g.D;
+    const AttnArgs a = make_session_args(gp, count, longest_suffix(p, first, count), workspace);
+    hipError_t e = hipSuccess;
+    {
+      // algorithmic bytes: the prefix once, every session's suffix, queries and outputs
+      const double key_tok = g.D * g.bits / 8.0 + g.D * 8.0 / g.G;
+      const double val_tok = g.D * g.bits / 8.0 + g.ncg() * 8.0;
+      const double row = g.D * 4.0;
+      const double fp32_rows = (double)(p.seq - p.st.kq) + (double)(p.seq - p.st.vq);
+      const double bytes =
+          g.units * ((double)p.st.kq * key_tok + (double)p.st.vq * val_tok + (fp32_rows + suffix_rows) * row) +
+          2.0 * count * (double)a.q_sess_stride * 4.0;
+      TimedLaunch timed(KIVI_KERNEL_ATTN_PACKED, stream, bytes);
+      const int nrs = a.gq <= 4 ? 1 : 2;
+      switch (g.bits * 10 + nrs) {
+        case 21: e = launch_sessions<2, 1>(a, t, stream); break;
+        case 22: e = launch_sessions<2, 2>(a, t, stream); break;
+        case 41: e = launch_sessions<4, 1>(a, t, stream); break;
+        case 42: e = launch_sessions<4, 2>(a, t, stream); break;
+        case 81: e = launch_sessions<8, 1>(a, t, stream); break;
+        case 82: e = launch_sessions<8, 2>(a, t, stream); break;
+        default: e = hipErrorInvalidValue; break;
+      }
+    }
+    if (e != hipSuccess) return e;
+    const size_t merge_lds = ((size_t)a.nsplit_total + 8) * sizeof(float);
+    const double bytes = (double)count * g.units * a.gq * ((double)a.nsplit_total * (g.D + 2) + g.D) * 4.0;
+    TimedLaunch timed(KIVI_KERNEL_ATTN_MERGE, stream, bytes);
+    k_attn_merge<<<count * g.units * a.gq, kThreads, merge_lds, stream>>>(
+        workspace, a.nsplit_total, a.gq, g.D, p.heads, p.qh, gp.out, g.units, a.ws_sess_stride,
+        a.q_sess_stride);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 }  // namespace kivi

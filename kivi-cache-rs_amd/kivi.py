@@ -590,6 +590,10 @@ class RagSession:
                      C.c_float(scale), _fptr(out), out.size)
         return out
 
+    def append_device(self, k_ptr, k_len, v_ptr, v_len, seq_len, stream=0):
+        self._b.call("session_append_device", self._h, C.c_void_p(k_ptr), k_len,
+                     C.c_void_p(v_ptr), v_len, seq_len, C.c_void_p(stream))
+
 
 # kivi_kernel_family (include/kivi.h)
 KERNEL_FAMILIES = {"attn_packed": 0, "attn_tail": 1, "attn_merge": 2, "quant_keys": 3,
@@ -613,8 +617,7 @@ def sessions_attention(backend, sessions, queries, num_q_heads, scale):
     """Batched ``RagSession::attention`` over sessions of one prefix (C-ABI extension)."""
     q = _f32(queries)
     n = len(sessions)
-    arr = (C.c_void_p * max(n, 1))(*[s._h.value if isinstance(s._h, C.c_void_p) else s._h
-                                      for s in sessions])
+    arr = session_handles(sessions)
     if n:
         p = sessions[0]._parent
         per = p.batch_size() * num_q_heads * p.head_dim()
@@ -624,6 +627,23 @@ def sessions_attention(backend, sessions, queries, num_q_heads, scale):
     backend.call("sessions_attention", C.cast(arr, C.POINTER(C.c_void_p)), n, _fptr(q), q.size,
                  num_q_heads, C.c_float(scale), _fptr(out), out.size)
     return out
+
+
+def session_handles(sessions):
+    """ctypes array of the sessions' handles (the ``const kivi_session* const*`` argument)."""
+    return (C.c_void_p * max(len(sessions), 1))(
+        *[s._h.value if isinstance(s._h, C.c_void_p) else s._h for s in sessions])
+
+
+def sessions_attention_device(backend, sessions, q_ptr, q_len, num_q_heads, scale, out_ptr,
+                              out_len, stream=0, handles=None):
+    """Device-pointer form of :func:`sessions_attention`, enqueued on ``stream``. ``handles``
+    (from :func:`session_handles`) skips rebuilding the handle array on every call."""
+    arr = session_handles(sessions) if handles is None else handles
+    backend.call("sessions_attention_device", C.cast(arr, C.POINTER(C.c_void_p)), len(sessions),
+                 C.c_void_p(q_ptr), q_len, num_q_heads, C.c_float(scale), C.c_void_p(out_ptr),
+                 out_len, C.c_void_p(stream))
+    return arr
 
 
 class RuntimeKv:

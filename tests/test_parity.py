@@ -166,6 +166,45 @@ def test_session_parity(amd, oracle):
     assert_close(batched, per)
 
 
+@pytest.mark.parametrize("bits,qh,n_sess,doc", [(2, 32, 6, 1000), (2, 64, 4, 1024), (4, 32, 4, 777),
+                                               (8, 64, 3, 1000), (2, 32, 70, 640)])
+def test_batched_sessions_kernel_parity(amd, oracle, bits, qh, n_sess, doc):
+    """Batched RagSession attention on the packed-chunk path (head_dim 128, G=32): one launch
+    per 64 sessions over the shared prefix (70 sessions = two launch groups), suffixes of 0 to
+    130 tokens, every session against the oracle's RagSession::attention (src/prefix.rs:223-289)."""
+    batch, heads, dim = 1, 8, 128
+    rng = np.random.default_rng(bits * 1000 + n_sess)
+    k = rng.standard_normal(batch * heads * doc * dim).astype(np.float32)
+    k.reshape(batch, heads, doc, dim)[:, :, :, 3] *= np.float32(10.0)
+    v = rng.standard_normal(batch * heads * doc * dim).astype(np.float32)
+    cfg = KiviConfig(bits, 32, 128)
+    ca, co = KiviCache(amd, cfg, batch, heads, dim), KiviCache(oracle, cfg, batch, heads, dim)
+    ca.append(k, v, doc)
+    co.append(k, v, doc)
+    pa, po = ca.share_prefix(), co.share_prefix()
+    sa = [pa.session() for _ in range(n_sess)]
+    so = [po.session() for _ in range(n_sess)]
+    lens = [(0, 1, 63, 64, 97, 130)[i % 6] for i in range(n_sess)]
+    for a, o, n in zip(sa, so, lens):
+        if n:
+            sk = rng.standard_normal(batch * heads * n * dim).astype(np.float32)
+            sv = rng.standard_normal(batch * heads * n * dim).astype(np.float32)
+            a.append(sk, sv, n)
+            o.append(sk, sv, n)
+    per = batch * qh * dim
+    qs = rng.standard_normal(n_sess * per).astype(np.float32)
+    scale = np.float32(1 / np.sqrt(128))
+    got = kivi.sessions_attention(amd, sa, qs, qh, scale)
+    for i, o in enumerate(so):
+        assert_close(got[i * per:(i + 1) * per], o.attention(qs[i * per:(i + 1) * per], qh, scale),
+                     f"session {i} (suffix {lens[i]})")
+    # the same call again (persistent workspace reused), then a smaller batch
+    again = kivi.sessions_attention(amd, sa, qs, qh, scale)
+    assert np.array_equal(again.view(np.uint32), got.view(np.uint32))
+    few = kivi.sessions_attention(amd, sa[1:3], qs[per:3 * per], qh, scale)
+    assert_close(few, got[per:3 * per], "sessions 1..2 alone")
+
+
 def test_runtime_decode_parity(amd, oracle):
     """512-step streaming decode shape of config 1, scaled down: prefill, then decode steps
     crossing key flushes and window evictions, compared with the oracle each step."""
