@@ -20,7 +20,8 @@
 // offset 2*(i/8) of that nibble). One shift-and-mask then leaves four (4-bit) or eight
 // (2-bit) consecutive elements one per byte or nibble, which the attention kernels convert
 // into MFMA operands with the packed fp8 / fp4 converters and no further shuffling.
-// Per unit, smax[2] holds the largest key and value scale quantized so far (see CacheView).
+// Per unit, smax[4] holds the largest key and value scale and the largest key and value
+// magnitude quantized so far (see CacheView).
 //
 // fp32 state per unit: key residual [R][D] (linear, token kq+i in slot i) and the value
 // window [R][D] as a ring (token vq+i in slot (vhead+i) % R), so a decode step evicts one
@@ -71,9 +72,10 @@ struct CacheView {
   float* vparams;
   float* kres;   // [units][R][D]
   float* vring;  // [units][R][D]
-  // [units][2]: running maxima of the key and of the value scales ever quantized into each
-  // unit (f32 bit patterns; scales are >= 0, so unsigned order is float order). The
-  // attention kernels derive power-of-two operand ranges from them.
+  // [units][4]: running maxima of the key scales, the value scales, the key |x| and the
+  // value |x| ever quantized into each unit (f32 bit patterns of values >= 0, so unsigned
+  // order is float order). The attention kernels derive power-of-two operand ranges from
+  // them; |x| bounds every dequantized element (up to rounding).
   uint32_t* smax;
 };
 

@@ -751,8 +751,8 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
   // Power-of-two operand ranges: every key A operand |q * scale| * 2^ek and every value A
   // operand |w * scale| * 2^ev (w <= 1) stays below 2^15, from the unit's largest scales.
   qmax = warp_max(qmax);
-  const float kmax = __uint_as_float(a.c.smax[2 * unit]);
-  const float vmax = __uint_as_float(a.c.smax[2 * unit + 1]);
+  const float kmax = __uint_as_float(a.c.smax[4 * unit]);
+  const float vmax = __uint_as_float(a.c.smax[4 * unit + 1]);
   const int ek = std::min(60, std::max(-100, 15 - __builtin_amdgcn_frexp_expf(qmax * kmax)));
   const int ev = std::min(60, std::max(-100, 15 - __builtin_amdgcn_frexp_expf(vmax)));
   constexpr int kExp = CodeUnit<BITS>::kExp;
@@ -1038,6 +1038,311 @@ __global__ void __launch_bounds__(kThreads)
   }
 }
 
+// ------------------------------------------------------------------ shared-prefix GEMM splits
+// Batched sessions over one prefix: a unit's rows are all its (session, GQA head) pairs (64
+// sessions x 4 heads = 256 rows), so each packed chunk is the shared operand of a real GEMM.
+// A workgroup (4 waves x 32 rows) dequantizes one 64-token chunk of keys and values into LDS
+// once (f32 dequant, scaled by a power of two, split into hi + lo f16), and every wave runs
+//   S^T[64 t][32 r]   = K[t][d]   . Q^T[d][r]     (v_mfma_f32_32x32x16_f16)
+//   O^T[128 d][32 r] += V^T[d][t] . P^T[t][r]
+// with hi/lo operands on both sides (a*b ~ ah*bh + ah*bl + al*bh: ~22-bit products, f32
+// sums). A row is the MFMA N index (lane % 32) in both products, so one lane pair (lanes r
+// and r + 32) owns a row's logits, softmax state and outputs.
+
+typedef _Float16 hx8 __attribute__((ext_vector_type(8)));
+typedef float fx16 __attribute__((ext_vector_type(16)));
+
+constexpr uint32_t kShRows = 128;      // rows per workgroup (32 per wave)
+constexpr uint32_t kShKRow = 128 + 8;  // K LDS row (one token) stride in halves, padded
+constexpr uint32_t kShVRow = 64 + 8;   // V^T LDS row (one channel) stride in halves, padded
+constexpr size_t kShLdsBytes = (2 * 64 * kShKRow + 2 * 128 * kShVRow) * sizeof(_Float16);
+constexpr float kShPScale = 16384.f;   // P operands are p * 2^14 (p <= 1)
+
+__device__ __forceinline__ void split_hl(float x, _Float16& hi, _Float16& lo) {
+  hi = static_cast<_Float16>(x);
+  lo = static_cast<_Float16>(x - static_cast<float>(hi));
+}
+
+__device__ __forceinline__ fx16 mfma32(const hx8& a, const hx8& b, const fx16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// Power-of-two factor 2^e with |x| * 2^e < 2^14 for |x| <= amax.
+__device__ __forceinline__ int range_exp(float amax) {
+  return std::min(60, std::max(-100, 14 - __builtin_amdgcn_frexp_expf(amax)));
+}
+
+// Keys of chunk `chunk` into khi/klo [64 tokens][kShKRow]: thread = (channel octet o, token
+// quad tq); one (scale, zero) load per channel serves its four tokens.
+template <int BITS>
+__device__ __forceinline__ void shared_stage_keys(const AttnArgs& a, uint32_t unit, uint32_t chunk,
+                                                  float kf, _Float16* khi, _Float16* klo) {
+  constexpr uint32_t D = 128, PPW = 32 / BITS, KW = D / PPW, MASK = (1u << BITS) - 1u;
+  const Geometry& g = a.c.geo;
+  const uint32_t o = threadIdx.x % 16, tq = threadIdx.x / 16;
+  const uint64_t t0 = (uint64_t)chunk * 64 + 4 * tq;
+  const float4* pp = reinterpret_cast<const float4*>(a.c.kparams + unit * g.kparams_unit() +
+                                                     (t0 / 32) * D * 2 + 16 * o);
+  float4 p[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) p[j] = pp[j];
+  const uint32_t* wp = a.c.kcodes + unit * g.kcodes_unit() + t0 * KW;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    uint32_t w0, w1 = 0;
+    if constexpr (BITS == 8) {
+      const uint2 w = *reinterpret_cast<const uint2*>(wp + j * KW + 2 * o);
+      w0 = w.x;
+      w1 = w.y;
+    } else if constexpr (BITS == 4) {
+      w0 = wp[j * KW + o];
+    } else {
+      w0 = wp[j * KW + o / 2] >> (2 * (o % 2));  // channels 8o.. are elements 8(o%2).. of the word
+    }
+    hx8 hi, lo;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      uint32_t code;
+      if constexpr (BITS == 8) code = ((e < 4 ? w0 : w1) >> (8 * (e % 4))) & MASK;
+      else if constexpr (BITS == 4) code = (w0 >> code_shift(4, e)) & MASK;
+      else code = (w0 >> (4 * e)) & MASK;
+      const float s = e % 2 ? p[e / 2].z : p[e / 2].x;
+      const float z = e % 2 ? p[e / 2].w : p[e / 2].y;
+      _Float16 h, l;
+      split_hl(fmaf(static_cast<float>(code), s, z) * kf, h, l);
+      hi[e] = h;
+      lo[e] = l;
+    }
+    *reinterpret_cast<hx8*>(khi + (4 * tq + j) * kShKRow + 8 * o) = hi;
+    *reinterpret_cast<hx8*>(klo + (4 * tq + j) * kShKRow + 8 * o) = lo;
+  }
+}
+
+// Values of chunk `chunk` into vhi/vlo [128 channels][kShVRow], tokens permuted so that a
+// lane's 8 MFMA K-slots are 8 consecutive halves: position 16j + 8h + i holds token
+// 16j + 8(i/4) + 4h + i%4 (bits 2 and 3 swapped), the order in which the S^T output leaves
+// the probabilities in a lane. Thread = (token octet (j, h), channel quad).
+template <int BITS>
+__device__ __forceinline__ void shared_stage_values(const AttnArgs& a, uint32_t unit, uint32_t chunk,
+                                                    float vf, _Float16* vhi, _Float16* vlo) {
+  constexpr uint32_t D = 128, PPW = 32 / BITS, VW = 64 / PPW, MASK = (1u << BITS) - 1u;
+  const Geometry& g = a.c.geo;
+  const uint32_t oc = threadIdx.x % 8, cq = threadIdx.x / 8;
+  const uint32_t j = oc / 2, h = oc % 2, cg = cq / 8;
+  const float4* pp = reinterpret_cast<const float4*>(
+      a.c.vparams + unit * g.vparams_unit() + (((uint64_t)chunk * g.ncg() + cg) * 64 + 16 * j + 4 * h) * 2);
+  const float4 p[4] = {pp[0], pp[1], pp[4], pp[5]};  // tokens +0,1 | +2,3 | +8,9 | +10,11
+  const uint32_t* wbase = a.c.vcodes + unit * g.vcodes_unit() + (uint64_t)chunk * D * VW;
+#pragma unroll
+  for (int x = 0; x < 4; ++x) {
+    const uint32_t c = 4 * cq + x;
+    const uint32_t* wc = wbase + c * VW;
+    uint32_t w0, w1;
+    if constexpr (BITS == 8) {
+      w0 = wc[4 * j + h];
+      w1 = wc[4 * j + 2 + h];
+    } else if constexpr (BITS == 4) {
+      const uint2 w = *reinterpret_cast<const uint2*>(wc + 2 * j);
+      w0 = w.x >> (4 * h);
+      w1 = w.y >> (4 * h);
+    } else {
+      w0 = wc[j] >> (16 * h);
+      w1 = w0 >> 2;
+    }
+    hx8 hi, lo;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t w = e < 4 ? w0 : w1;
+      const uint32_t i = e % 4;
+      uint32_t code;
+      if constexpr (BITS == 8) code = (w >> (8 * i)) & MASK;
+      else if constexpr (BITS == 4) code = (w >> (8 * i)) & MASK;
+      else code = (w >> (4 * i)) & MASK;
+      const float4 q = p[e / 2];
+      const float s = e % 2 ? q.z : q.x;
+      const float z = e % 2 ? q.w : q.y;
+      _Float16 hh, ll;
+      split_hl(fmaf(static_cast<float>(code), s, z) * vf, hh, ll);
+      hi[e] = hh;
+      lo[e] = ll;
+    }
+    *reinterpret_cast<hx8*>(vhi + c * kShVRow + 16 * j + 8 * h) = hi;
+    *reinterpret_cast<hx8*>(vlo + c * kShVRow + 16 * j + 8 * h) = lo;
+  }
+}
+
+// One workgroup: rows [rblk*128, +128) of `unit` over packed chunks of split `split` (a
+// contiguous range), partials into split index `split` of each row's session.
+template <int BITS>
+__device__ __forceinline__ void shared_split(const AttnArgs& a, uint32_t unit, uint32_t rblk,
+                                             uint32_t split, _Float16* lds) {
+  constexpr uint32_t D = 128;
+  _Float16* khi = lds;
+  _Float16* klo = khi + 64 * kShKRow;
+  _Float16* vhi = klo + 64 * kShKRow;
+  _Float16* vlo = vhi + 128 * kShVRow;
+  const uint32_t lane = threadIdx.x % 64, wave = threadIdx.x / 64, h = lane / 32, r = lane % 32;
+  const uint32_t gq = a.gq;
+  const uint32_t row = rblk * kShRows + wave * 32 + r;
+  const uint32_t sess = row / gq, head = row % gq;
+  const bool live = sess < a.nsess;
+  const uint32_t b = unit / a.heads, kvh = unit % a.heads;
+
+  // q of the lane's row, channels 16s + 8h + i, in base-2 logit units, split hi/lo at a
+  // per-row power-of-two range
+  const float* qp = a.query + (uint64_t)(live ? sess : 0) * a.q_sess_stride +
+                    ((uint64_t)b * a.qh + kvh * gq + head) * D + 8 * h;
+  const float qs = live ? a.scale2 : 0.f;
+  float qf[8][8];
+  float qmax = 0.f;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    const float4 v0 = *reinterpret_cast<const float4*>(qp + 16 * s);
+    const float4 v1 = *reinterpret_cast<const float4*>(qp + 16 * s + 4);
+    qf[s][0] = v0.x * qs; qf[s][1] = v0.y * qs; qf[s][2] = v0.z * qs; qf[s][3] = v0.w * qs;
+    qf[s][4] = v1.x * qs; qf[s][5] = v1.y * qs; qf[s][6] = v1.z * qs; qf[s][7] = v1.w * qs;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) qmax = fmaxf(qmax, fabsf(qf[s][i]));
+  }
+  qmax = fmaxf(qmax, __shfl_xor(qmax, 32));
+  const int eq = range_exp(qmax);
+  const float qfac = ldexpf(1.f, eq);
+  hx8 qhi[8], qlo[8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      _Float16 hh, ll;
+      split_hl(qf[s][i] * qfac, hh, ll);
+      qhi[s][i] = hh;
+      qlo[s][i] = ll;
+    }
+  const int ek = range_exp(__uint_as_float(a.c.smax[4 * unit + 2]));
+  const int ev = range_exp(__uint_as_float(a.c.smax[4 * unit + 3]));
+  const float kf = ldexpf(1.f, ek), vf = ldexpf(1.f, ev);
+  const float s_unscale = ldexpf(1.f, -ek - eq);
+  const float o_unscale = ldexpf(1.f, -ev) / kShPScale;
+
+  const uint32_t cps = (a.chunk_end + a.nsplit_fast - 1) / a.nsplit_fast;
+  const uint32_t c0 = std::min(a.chunk_end, split * cps);
+  const uint32_t c1 = std::min(a.chunk_end, c0 + cps);
+  float m = -INFINITY, l = 0.f;
+  fx16 o[4];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) o[mt][v] = 0.f;
+
+  for (uint32_t c = c0; c < c1; ++c) {
+    __syncthreads();  // the previous chunk's operands are consumed
+    shared_stage_keys<BITS>(a, unit, c, kf, khi, klo);
+    shared_stage_values<BITS>(a, unit, c, vf, vhi, vlo);
+    __syncthreads();
+    // S^T: tokens r (tile 0) and 32 + r (tile 1) against the lane's row
+    fx16 s0, s1;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      s0[v] = 0.f;
+      s1[v] = 0.f;
+    }
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const hx8 kh0 = *reinterpret_cast<const hx8*>(khi + r * kShKRow + 16 * s + 8 * h);
+      const hx8 kl0 = *reinterpret_cast<const hx8*>(klo + r * kShKRow + 16 * s + 8 * h);
+      const hx8 kh1 = *reinterpret_cast<const hx8*>(khi + (32 + r) * kShKRow + 16 * s + 8 * h);
+      const hx8 kl1 = *reinterpret_cast<const hx8*>(klo + (32 + r) * kShKRow + 16 * s + 8 * h);
+      s0 = mfma32(kh0, qhi[s], s0);
+      s1 = mfma32(kh1, qhi[s], s1);
+      s0 = mfma32(kh0, qlo[s], s0);
+      s1 = mfma32(kh1, qlo[s], s1);
+      s0 = mfma32(kl0, qhi[s], s0);
+      s1 = mfma32(kl1, qhi[s], s1);
+    }
+    // online softmax over the chunk (the lane pair r, r + 32 holds the row's 64 logits)
+    float mx = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      s0[v] *= s_unscale;
+      s1[v] *= s_unscale;
+      mx = fmaxf(mx, fmaxf(s0[v], s1[v]));
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float mnew = fmaxf(m, mx);
+    const float alpha = m == -INFINITY ? 0.f : exp2f(m - mnew);
+    m = mnew;
+    float psum = 0.f;
+    hx8 ph[4], pl[4];  // P^T K-steps: tokens 16j .. 16j + 15 (tile j/2, values 8(j%2) ..)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const float p0 = exp2f(s0[v] - mnew), p1 = exp2f(s1[v] - mnew);
+      psum += p0 + p1;
+      _Float16 hh, ll;
+      split_hl(p0 * kShPScale, hh, ll);
+      ph[v / 8][v % 8] = hh;
+      pl[v / 8][v % 8] = ll;
+      split_hl(p1 * kShPScale, hh, ll);
+      ph[2 + v / 8][v % 8] = hh;
+      pl[2 + v / 8][v % 8] = ll;
+    }
+    l = fmaf(l, alpha, psum);
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) o[mt][v] *= alpha;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+        const hx8 vh = *reinterpret_cast<const hx8*>(vhi + (32 * mt + r) * kShVRow + 16 * j + 8 * h);
+        const hx8 vl = *reinterpret_cast<const hx8*>(vlo + (32 * mt + r) * kShVRow + 16 * j + 8 * h);
+        o[mt] = mfma32(vh, ph[j], o[mt]);
+        o[mt] = mfma32(vh, pl[j], o[mt]);
+        o[mt] = mfma32(vl, ph[j], o[mt]);
+      }
+  }
+  l += __shfl_xor(l, 32);
+  if (!live) return;
+  float* part = a.ws + (uint64_t)sess * a.ws_sess_stride +
+                (((uint64_t)unit * a.nsplit_total + split) * gq + head) * (D + 2);
+  // O^T value v of tile mt is channel 32mt + 8(v/4) + 4h + v%4
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const float4 v = make_float4(o[mt][4 * q4] * o_unscale, o[mt][4 * q4 + 1] * o_unscale,
+                                   o[mt][4 * q4 + 2] * o_unscale, o[mt][4 * q4 + 3] * o_unscale);
+      *reinterpret_cast<float4*>(part + 32 * mt + 8 * q4 + 4 * h) = v;
+    }
+  if (h == 0) {
+    part[D] = c1 > c0 ? m : -INFINITY;
+    part[D + 1] = c1 > c0 ? l : 0.f;
+  }
+}
+
+// Batched sessions, GEMM form: workgroups [0, nsess*units*nsplit_win) take one window /
+// suffix chunk of one session (as k_attn_sessions); the rest one (unit, row block, split) of
+// the packed prefix chunks for all sessions' rows at once.
+template <int BITS, int NRS>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
+    k_attn_shared(AttnArgs a, SessionTable t) {
+  extern __shared__ float lds[];
+  const uint32_t per_sess = a.units * a.nsplit_win;
+  const uint32_t nwin = a.nsess * per_sess;
+  if (blockIdx.x < nwin) {
+    const uint32_t s = blockIdx.x / per_sess, r = blockIdx.x % per_sess;
+    const AttnArgs as = session_args(a, t, s);
+    mfma_split<BITS, NRS, 1, true>(as, r / a.nsplit_win, r % a.nsplit_win, lds);
+  } else {
+    // (unit, row block) outer, split inner: the row blocks of one split are nsplit_fast apart
+    // in the grid, a multiple of the XCD count when nsplit_fast is, so they share an L2
+    const uint32_t blk = blockIdx.x - nwin;
+    const uint32_t rblocks = (a.nsess * a.gq + kShRows - 1) / kShRows;
+    const uint32_t unit = blk / (rblocks * a.nsplit_fast);
+    const uint32_t rem = blk % (rblocks * a.nsplit_fast);
+    shared_split<BITS>(a, unit, rem / a.nsplit_fast, rem % a.nsplit_fast, reinterpret_cast<_Float16*>(lds));
+  }
+}
+
 // ------------------------------------------------------------------ planning
 
 constexpr size_t kMaxMergeLds = 48 * 1024;  // in-kernel merge up to ~12K splits per unit
@@ -1217,6 +1522,31 @@ uint64_t longest_suffix(const SessionsProblem& sp, uint32_t first, uint32_t coun
   return m;
 }
 
+// Rows (sessions x GQA heads) from which one launch group takes the GEMM form: below it a
+// 32-row MFMA tile would be mostly padding and the per-session form does less work.
+constexpr uint32_t kSharedMinRows = 16;
+// Workgroups the GEMM form aims for (two per CU: 70 KB of LDS each).
+constexpr uint32_t kSharedTargetGroups = 512;
+
+bool use_shared(const SessionsProblem& sp, uint32_t nsess) {
+  return nsess * (sp.qh / sp.heads) >= kSharedMinRows;
+}
+
+// The GEMM form's splits: the packed chunks of a unit in nsplit contiguous ranges, nsplit a
+// multiple of 8 (the XCD count) where the chunks allow, so about kSharedTargetGroups
+// workgroups cover units x row blocks x splits.
+AttnArgs make_shared_args(const SessionsProblem& sp, uint32_t nsess, uint64_t max_suffix, float* ws) {
+  AttnArgs a = make_session_args(sp, nsess, max_suffix, ws);
+  const uint32_t rblocks = (nsess * a.gq + kShRows - 1) / kShRows;
+  const uint32_t per = a.units * rblocks;
+  uint32_t ns = (kSharedTargetGroups + per - 1) / per;
+  ns = (ns + 7) / 8 * 8;
+  a.nsplit_fast = a.chunk_end == 0 ? 0 : std::max(1u, std::min(ns, a.chunk_end));
+  a.nsplit_total = a.nsplit_fast + a.nsplit_win + a.nsplit_gen;
+  a.ws_sess_stride = (uint64_t)sp.cache.geo.units * a.nsplit_total * a.gq * (sp.cache.geo.D + 2);
+  return a;
+}
+
 template <int BITS, int NRS>
 hipError_t launch_sessions(const AttnArgs& a, const SessionTable& t, hipStream_t stream) {
   constexpr int NH = 4 * NRS;
@@ -1228,15 +1558,53 @@ hipError_t launch_sessions(const AttnArgs& a, const SessionTable& t, hipStream_t
   return hipGetLastError();
 }
 
+template <int BITS, int NRS>
+hipError_t launch_shared(const AttnArgs& a, const SessionTable& t, hipStream_t stream) {
+  constexpr int NH = 4 * NRS;
+  static_assert((size_t)4 * NH * (128 + 2) * sizeof(float) <= kShLdsBytes, "window path LDS");
+  static_assert((size_t)4 * NH * (64 + kRowPad) * sizeof(float) <= kShLdsBytes, "window path LDS");
+  static bool configured = false;  // the attribute is per kernel and per process
+  if (!configured) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_shared<BITS, NRS>),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             static_cast<int>(kShLdsBytes));
+    if (e != hipSuccess) return e;
+    configured = true;
+  }
+  const uint32_t rblocks = (a.nsess * a.gq + kShRows - 1) / kShRows;
+  const uint32_t grid = a.nsess * a.units * a.nsplit_win + a.units * rblocks * a.nsplit_fast;
+  k_attn_shared<BITS, NRS><<<grid, kThreads, kShLdsBytes, stream>>>(a, t);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+namespace {
+
+// Launch group [first, first + count): its form and arguments (queries, outputs and the
+// window range of that group).
+AttnArgs group_args(const SessionsProblem& p, uint32_t first, uint32_t count, float* ws, bool* shared) {
+  SessionsProblem gp = p;
+  gp.queries = p.queries + (uint64_t)first * p.batch * p.qh * p.cache.geo.D;
+  gp.out = p.out + (uint64_t)first * p.batch * p.qh * p.cache.geo.D;
+  *shared = use_shared(p, count);
+  const uint64_t longest = longest_suffix(p, first, count);
+  return *shared ? make_shared_args(gp, count, longest, ws) : make_session_args(gp, count, longest, ws);
+}
+
 }  // namespace
 
 size_t sessions_workspace_floats(const SessionsProblem& p) {
   if (!sessions_supported(p)) return 0;
-  // the largest launch group: up to kMaxLaunchSessions sessions, window sized for the longest
-  // suffix of all
-  const uint32_t group = std::min(p.n, kMaxLaunchSessions);
-  const AttnArgs a = make_session_args(p, group, longest_suffix(p, 0, p.n), nullptr);
-  return (size_t)group * a.ws_sess_stride;
+  // every launch group reuses the workspace from its start
+  size_t most = 0;
+  for (uint32_t first = 0; first < p.n; first += kMaxLaunchSessions) {
+    const uint32_t count = std::min(kMaxLaunchSessions, p.n - first);
+    bool shared;
+    const AttnArgs a = group_args(p, first, count, nullptr, &shared);
+    most = std::max(most, (size_t)count * a.ws_sess_stride);
+  }
+  return most;
 }
 
 hipError_t launch_sessions_attention(const SessionsProblem& p, float* workspace,
@@ -1251,10 +1619,8 @@ hipError_t launch_sessions_attention(const SessionsProblem& p, float* workspace,
       t.d[i] = p.sessions[first + i];
       suffix_rows += 2.0 * (double)t.d[i].len;
     }
-    SessionsProblem gp = p;
-    gp.queries = p.queries + (uint64_t)first * p.batch * p.qh * g.D;
-    gp.out = p.out + (uint64_t)first * p.batch * p.qh * g.D;
-    const AttnArgs a = make_session_args(gp, count, longest_suffix(p, first, count), workspace);
+    bool shared;
+    const AttnArgs a = group_args(p, first, count, workspace, &shared);
     hipError_t e = hipSuccess;
     {
       // algorithmic bytes: the prefix once, every session's suffix, queries and outputs
@@ -1268,12 +1634,12 @@ hipError_t launch_sessions_attention(const SessionsProblem& p, float* workspace,
       TimedLaunch timed(KIVI_KERNEL_ATTN_PACKED, stream, bytes);
       const int nrs = a.gq <= 4 ? 1 : 2;
       switch (g.bits * 10 + nrs) {
-        case 21: e = launch_sessions<2, 1>(a, t, stream); break;
-        case 22: e = launch_sessions<2, 2>(a, t, stream); break;
-        case 41: e = launch_sessions<4, 1>(a, t, stream); break;
-        case 42: e = launch_sessions<4, 2>(a, t, stream); break;
-        case 81: e = launch_sessions<8, 1>(a, t, stream); break;
-        case 82: e = launch_sessions<8, 2>(a, t, stream); break;
+        case 21: e = shared ? launch_shared<2, 1>(a, t, stream) : launch_sessions<2, 1>(a, t, stream); break;
+        case 22: e = shared ? launch_shared<2, 2>(a, t, stream) : launch_sessions<2, 2>(a, t, stream); break;
+        case 41: e = shared ? launch_shared<4, 1>(a, t, stream) : launch_sessions<4, 1>(a, t, stream); break;
+        case 42: e = shared ? launch_shared<4, 2>(a, t, stream) : launch_sessions<4, 2>(a, t, stream); break;
+        case 81: e = shared ? launch_shared<8, 1>(a, t, stream) : launch_sessions<8, 1>(a, t, stream); break;
+        case 82: e = shared ? launch_shared<8, 2>(a, t, stream) : launch_sessions<8, 2>(a, t, stream); break;
         default: e = hipErrorInvalidValue; break;
       }
     }
@@ -1282,7 +1648,7 @@ hipError_t launch_sessions_attention(const SessionsProblem& p, float* workspace,
     const double bytes = (double)count * g.units * a.gq * ((double)a.nsplit_total * (g.D + 2) + g.D) * 4.0;
     TimedLaunch timed(KIVI_KERNEL_ATTN_MERGE, stream, bytes);
     k_attn_merge<<<count * g.units * a.gq, kThreads, merge_lds, stream>>>(
-        workspace, a.nsplit_total, a.gq, g.D, p.heads, p.qh, gp.out, g.units, a.ws_sess_stride,
+        workspace, a.nsplit_total, a.gq, g.D, p.heads, p.qh, a.out, g.units, a.ws_sess_stride,
         a.q_sess_stride);
     e = hipGetLastError();
     if (e != hipSuccess) return e;

@@ -38,16 +38,27 @@ __device__ __forceinline__ const float* source_row(const RowSource& s, uint32_t 
   return s.base + unit * s.stride_unit + tok * D;
 }
 
-// Raise *smax to the largest `v` of the workgroup (one atomic per workgroup).
-__device__ __forceinline__ void raise_max(uint32_t* smax, float v) {
-  __shared__ float red[kThreads / 64];
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-  if (threadIdx.x % 64 == 0) red[threadIdx.x / 64] = v;
+// Raise the unit's running maxima m[0] (largest scale) and m[2] (largest |x|) to the largest
+// `scale` / `amax` of the workgroup (one atomic each per workgroup).
+__device__ __forceinline__ void raise_max(uint32_t* m, float scale, float amax) {
+  __shared__ float red[2][kThreads / 64];
+  for (int o = 32; o > 0; o >>= 1) {
+    scale = fmaxf(scale, __shfl_xor(scale, o));
+    amax = fmaxf(amax, __shfl_xor(amax, o));
+  }
+  if (threadIdx.x % 64 == 0) {
+    red[0][threadIdx.x / 64] = scale;
+    red[1][threadIdx.x / 64] = amax;
+  }
   __syncthreads();
   if (threadIdx.x == 0) {
-    float m = red[0];
-    for (int w = 1; w < kThreads / 64; ++w) m = fmaxf(m, red[w]);
-    atomicMax(smax, __float_as_uint(m));
+    float a = red[0][0], b = red[1][0];
+    for (int w = 1; w < kThreads / 64; ++w) {
+      a = fmaxf(a, red[0][w]);
+      b = fmaxf(b, red[1][w]);
+    }
+    atomicMax(m, __float_as_uint(a));
+    atomicMax(m + 2, __float_as_uint(b));
   }
 }
 
@@ -126,7 +137,7 @@ __global__ void __launch_bounds__(kThreads)
       stage_row(rows + (uint64_t)t * D, xs + t * (D + 1), D, vec4 != 0, threadIdx.x % lanes, lanes);
     __syncthreads();
   }
-  float smax = 0.f;
+  float smax = 0.f, amax = 0.f;
   for (uint32_t d = threadIdx.x; d < D; d += blockDim.x) {
     float mn = INFINITY, mx = -INFINITY;
     for (uint32_t t = 0; t < G; ++t) {
@@ -137,13 +148,14 @@ __global__ void __launch_bounds__(kThreads)
     const float zero = mn;
     const float scale = scale_of(mx - zero, levels);
     smax = fmaxf(smax, scale);
+    amax = fmaxf(amax, fmaxf(fabsf(mn), fabsf(mx)));
     params[d] = make_float2(scale, zero);
     for (uint32_t t = 0; t < G; ++t) {
       const float x = staged ? xs[t * (D + 1) + d] : rows[(uint64_t)t * D + d];
       codes_lds[t * D + d] = static_cast<uint8_t>(quant_code(x, zero, scale, levels));
     }
   }
-  raise_max(c.smax + 2 * unit, smax);  // includes the barrier before the packing below
+  raise_max(c.smax + 4 * unit, smax, amax);  // includes the barrier before the packing below
   const uint32_t ppw = geo.ppw();
   const uint32_t kw = geo.kwords_per_token();
   uint32_t* words = c.kcodes + unit * geo.kcodes_unit() + (g0 + g) * G * kw;
@@ -178,7 +190,7 @@ __global__ void __launch_bounds__(kThreads)
   const uint64_t t_hi = t_end < (tb + 1) * kValueBlock ? t_end : (tb + 1) * kValueBlock;
   const uint32_t ntok = static_cast<uint32_t>(t_hi - t_lo);
   float2* params = reinterpret_cast<float2*>(c.vparams + unit * geo.vparams_unit());
-  float smax = 0.f;
+  float smax = 0.f, amax = 0.f;
   const uint32_t lanes = 64, waves = blockDim.x / 64;
   for (uint32_t k0 = 0; k0 < ntok; k0 += TB) {
     const uint32_t nb = ntok - k0 < TB ? ntok - k0 : TB;
@@ -199,6 +211,7 @@ __global__ void __launch_bounds__(kThreads)
       }
       const float scale = scale_of(mx - mn, levels);
       smax = fmaxf(smax, scale);
+      amax = fmaxf(amax, fmaxf(fabsf(mn), fabsf(mx)));
       const uint64_t t = t_lo + k0 + r;
       const uint32_t tt = static_cast<uint32_t>(t % kValueBlock);
       params[(tb * ncg + cg) * kValueBlock + tt] = make_float2(scale, mn);
@@ -207,7 +220,7 @@ __global__ void __launch_bounds__(kThreads)
     }
     __syncthreads();  // the staging buffer is refilled by the next batch
   }
-  raise_max(c.smax + 2 * unit + 1, smax);  // includes the barrier before the packing below
+  raise_max(c.smax + 4 * unit + 1, smax, amax);  // includes the barrier before the packing below
   const uint32_t ppw = geo.ppw();
   const uint32_t vw = geo.vwords_per_channel();
   const uint32_t w_lo = static_cast<uint32_t>(t_lo % kValueBlock) / ppw;
@@ -250,9 +263,15 @@ __device__ __forceinline__ void load_lane(const float* row, uint32_t lane, float
   }
 }
 
-__device__ __forceinline__ void wave_raise_max(uint32_t* smax, float v) {
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-  if (threadIdx.x % 64 == 0) atomicMax(smax, __float_as_uint(v));
+__device__ __forceinline__ void wave_raise_max(uint32_t* m, float scale, float amax) {
+  for (int o = 32; o > 0; o >>= 1) {
+    scale = fmaxf(scale, __shfl_xor(scale, o));
+    amax = fmaxf(amax, __shfl_xor(amax, o));
+  }
+  if (threadIdx.x % 64 == 0) {
+    atomicMax(m, __float_as_uint(scale));
+    atomicMax(m + 2, __float_as_uint(amax));
+  }
 }
 
 // Keys: wave w of a workgroup takes item blockIdx.x*4 + w = (unit, group); the lane keeps its
@@ -275,7 +294,7 @@ __global__ void __launch_bounds__(kThreads)
     float x[GG][CPL];
 #pragma unroll
     for (int t = 0; t < GG; ++t) load_lane<CPL>(rows + (uint64_t)t * D, lane, x[t]);
-    float smax = 0.f;
+    float smax = 0.f, amax = 0.f;
     float2 sz[CPL];
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
@@ -287,6 +306,7 @@ __global__ void __launch_bounds__(kThreads)
       }
       sz[j] = make_float2(scale_of(mx - mn, levels), mn);
       smax = fmaxf(smax, sz[j].x);
+      amax = fmaxf(amax, fmaxf(fabsf(mn), fabsf(mx)));
 #pragma unroll
       for (int t = 0; t < GG; ++t)
         codes[t * D + CPL * lane + j] = static_cast<uint8_t>(quant_code(x[t][j], sz[j].y, sz[j].x, levels));
@@ -294,7 +314,7 @@ __global__ void __launch_bounds__(kThreads)
     float2* params = reinterpret_cast<float2*>(c.kparams + unit * geo.kparams_unit() + (g0 + g) * D * 2);
 #pragma unroll
     for (int j = 0; j < CPL; ++j) params[CPL * lane + j] = sz[j];
-    wave_raise_max(c.smax + 2 * unit, smax);
+    wave_raise_max(c.smax + 4 * unit, smax, amax);
   }
   __syncthreads();
   if (active) {
@@ -331,7 +351,7 @@ __global__ void __launch_bounds__(kThreads)
   const uint32_t ntok = static_cast<uint32_t>(t_hi - t_lo);
   float2* params = reinterpret_cast<float2*>(c.vparams + unit * geo.vparams_unit());
   const uint32_t cg = CPL * lane / G;
-  float smax = 0.f;
+  float smax = 0.f, amax = 0.f;
   // rows wave, wave+4, ... in batches of kRows, every batch's loads issued before its math
   constexpr uint32_t kRows = 4;
   for (uint32_t r0 = wave; r0 < ntok; r0 += 4 * kRows) {
@@ -359,6 +379,7 @@ __global__ void __launch_bounds__(kThreads)
       }
       const float scale = scale_of(mx - mn, levels);
       smax = fmaxf(smax, scale);
+      amax = fmaxf(amax, fmaxf(fabsf(mn), fabsf(mx)));
       const uint32_t tt = static_cast<uint32_t>((t_lo + r) % kValueBlock);
       if (lane % L == 0) params[(tb * ncg + cg) * kValueBlock + tt] = make_float2(scale, mn);
 #pragma unroll
@@ -366,7 +387,7 @@ __global__ void __launch_bounds__(kThreads)
         codes_lds[tt * D + CPL * lane + j] = static_cast<uint8_t>(quant_code(x[b][j], mn, scale, levels));
     }
   }
-  raise_max(c.smax + 2 * unit + 1, smax);  // includes the barrier before the packing below
+  raise_max(c.smax + 4 * unit + 1, smax, amax);  // includes the barrier before the packing below
   const uint32_t ppw = geo.ppw();
   const uint32_t vw = geo.vwords_per_channel();
   const uint32_t w_lo = static_cast<uint32_t>(t_lo % kValueBlock) / ppw;

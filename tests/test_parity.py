@@ -166,13 +166,15 @@ def test_session_parity(amd, oracle):
     assert_close(batched, per)
 
 
-@pytest.mark.parametrize("bits,qh,n_sess,doc", [(2, 32, 6, 1000), (2, 64, 4, 1024), (4, 32, 4, 777),
-                                               (8, 64, 3, 1000), (2, 32, 70, 640)])
-def test_batched_sessions_kernel_parity(amd, oracle, bits, qh, n_sess, doc):
+@pytest.mark.parametrize("bits,batch,qh,n_sess,doc", [
+    (2, 1, 32, 6, 1000), (2, 1, 64, 4, 1024), (4, 1, 32, 4, 777), (8, 1, 64, 3, 1000),
+    (2, 1, 32, 70, 640), (4, 2, 32, 40, 300), (8, 1, 32, 2, 500)])
+def test_batched_sessions_kernel_parity(amd, oracle, bits, batch, qh, n_sess, doc):
     """Batched RagSession attention on the packed-chunk path (head_dim 128, G=32): one launch
-    per 64 sessions over the shared prefix (70 sessions = two launch groups), suffixes of 0 to
-    130 tokens, every session against the oracle's RagSession::attention (src/prefix.rs:223-289)."""
-    batch, heads, dim = 1, 8, 128
+    per 64 sessions over the shared prefix (70 sessions = two launch groups), in the GEMM form
+    (sessions x heads >= 16 rows) and the per-session form, suffixes of 0 to 130 tokens, every
+    session against the oracle's RagSession::attention (src/prefix.rs:223-289)."""
+    heads, dim = 8, 128
     rng = np.random.default_rng(bits * 1000 + n_sess)
     k = rng.standard_normal(batch * heads * doc * dim).astype(np.float32)
     k.reshape(batch, heads, doc, dim)[:, :, :, 3] *= np.float32(10.0)
