@@ -37,6 +37,7 @@ sys.path.insert(0, str(PKG))
 
 METRIC = "decode-attn tokens/s + effective HBM GB/s (% of 8 TB/s); quantize GB/s"
 HBM_PEAK_GBPS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0  # dense f16 matrix-core peak
 
 CONFIGS = {
     # name: (batch, kv_heads, q_heads, head_dim, seq, bits, G, R, description)
@@ -328,7 +329,8 @@ def main():
     log(f"[bench] attention {per_step * 1e6:.1f} us/step, {eff_gbps:.0f} GB/s effective")
 
     dom = kernels.get("attn_packed") or kernels.get("attn_tail")
-    dom_name = ("k_attn_sessions" if sessions_cfg else "k_attn_mfma") if "attn_packed" in kernels \
+    # the sessions workload (64 sessions x 4 heads = 256 rows per unit) runs the GEMM form
+    dom_name = ("k_attn_shared" if sessions_cfg else "k_attn_mfma") if "attn_packed" in kernels \
         else "k_attn_generic"
     achieved = dom["gbps"] if dom else eff_gbps
     rec = recorded_traffic(dom_name, args.config, dom["bytes_per_launch"]) if dom else None
@@ -346,6 +348,21 @@ def main():
                   "region of the same steps",
         "traffic_source": rec["source"] if rec else None,
     }
+    if sessions_cfg and dom:
+        # The batched-sessions GEMM form is bound by the matrix cores: algorithmic flops of the
+        # launch (q.k and p.v over every session row and token, 4*D flops per row-token) over
+        # its mean duration, against the dense f16 MFMA peak it runs on. Each product executes
+        # as three f16 MFMA products (hi/lo operand splits), reported beside it.
+        n_sess, suffix = sessions_cfg
+        rows = n_sess * (qh // heads)
+        flops = 4.0 * dim * rows * (seq + suffix) * batch * heads
+        tflops = flops / (dom["mean_us"] * 1e-6) / 1e12
+        roofline.update({
+            "bound": "mfma", "achieved": tflops, "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": tflops / MFMA_F16_PEAK_TFLOPS, "algorithmic_flops_per_launch": flops,
+            "executed_f16_tflops": 3.0 * tflops,
+            "hbm_gbps": dom["gbps"],
+        })
     result = {
         "metric": METRIC,
         "value": tokens_per_s,

@@ -245,10 +245,13 @@ kivi_status kivi_session_attention(const kivi_session* session, const float* que
                                    size_t out_len, kivi_error* err);
 
 /* Extension, no reference counterpart: n sessions of ONE prefix scored in one pass
- * that streams each prefix tile from HBM once for all of them. Semantically
- * sessions[i].attention(queries[i]) for every i (src/prefix.rs:228-289).
- * queries/out are [n][batch][num_q_heads][head_dim]. Device pointers for
- * queries/out, enqueued on `stream`. */
+ * that streams each prefix tile from HBM once for all of them (one launch per 64
+ * sessions). Semantically sessions[i].attention(queries[i]) for every i
+ * (src/prefix.rs:228-289). queries/out are [n][batch][num_q_heads][head_dim]. Device
+ * pointers for queries/out, enqueued on `stream`. The split workspace belongs to the
+ * prefix: batched calls on one prefix are ordered after each other (a call on another
+ * stream waits for the previous call's stream, which must still exist). The sessions'
+ * suffixes must not be appended to while a call that reads them is in flight. */
 kivi_status kivi_sessions_attention_device(const kivi_session* const* sessions, size_t n,
                                            const float* queries, size_t queries_len,
                                            size_t num_q_heads, float scale, float* out,
