@@ -1041,26 +1041,42 @@ __global__ void __launch_bounds__(kThreads)
 // ------------------------------------------------------------------ shared-prefix GEMM splits
 // Batched sessions over one prefix: a unit's rows are all its (session, GQA head) pairs (64
 // sessions x 4 heads = 256 rows), so each packed chunk is the shared operand of a real GEMM.
-// A workgroup (4 waves x 32 rows) dequantizes one 64-token chunk of keys and values into LDS
-// once (f32 dequant, scaled by a power of two, split into hi + lo f16), and every wave runs
+// A workgroup of 8 waves owns 256 rows (32 per wave). It dequantizes each 64-token chunk of
+// keys and values into LDS once (f32 dequant at a power-of-two range, split into hi + lo f16),
+// and every wave runs
 //   S^T[64 t][32 r]   = K[t][d]   . Q^T[d][r]     (v_mfma_f32_32x32x16_f16)
 //   O^T[128 d][32 r] += V^T[d][t] . P^T[t][r]
 // with hi/lo operands on both sides (a*b ~ ah*bh + ah*bl + al*bh: ~22-bit products, f32
 // sums). A row is the MFMA N index (lane % 32) in both products, so one lane pair (lanes r
 // and r + 32) owns a row's logits, softmax state and outputs.
+//
+// Pipeline (one barrier per chunk): while the waves run the MFMAs of chunk c from LDS buffer
+// c%2, they dequantize chunk c+1 into buffer (c+1)%2 from code words already in registers and
+// (scale, zero) already in LDS, and the loads of chunk c+2 are in flight.
 
 typedef _Float16 hx8 __attribute__((ext_vector_type(8)));
 typedef float fx16 __attribute__((ext_vector_type(16)));
 
-constexpr uint32_t kShRows = 128;      // rows per workgroup (32 per wave)
+constexpr uint32_t kShThreads = 512;   // 8 waves
+constexpr uint32_t kShRows = 256;      // rows per workgroup (32 per wave)
 constexpr uint32_t kShKRow = 128 + 8;  // K LDS row (one token) stride in halves, padded
 constexpr uint32_t kShVRow = 64 + 8;   // V^T LDS row (one channel) stride in halves, padded
-constexpr size_t kShLdsBytes = (2 * 64 * kShKRow + 2 * 128 * kShVRow) * sizeof(_Float16);
+constexpr uint32_t kShBufHalves = 2 * 64 * kShKRow + 2 * 128 * kShVRow;  // khi, klo, vhi, vlo
+constexpr uint32_t kShParamFloats = 1024;  // keys [2 groups][128][2], values [4 groups][64][2]
+constexpr size_t kShLdsBytes = 2 * (size_t)kShBufHalves * sizeof(_Float16) + 2 * kShParamFloats * sizeof(float);
 constexpr float kShPScale = 16384.f;   // P operands are p * 2^14 (p <= 1)
 
-__device__ __forceinline__ void split_hl(float x, _Float16& hi, _Float16& lo) {
-  hi = static_cast<_Float16>(x);
-  lo = static_cast<_Float16>(x - static_cast<float>(hi));
+typedef uint32_t ux4 __attribute__((ext_vector_type(4)));
+
+// hi + lo f16 pairs of two floats (hi rounded toward zero: lo = x - hi is exact in f32, and
+// hi + lo keeps ~22 significant bits whatever the rounding of hi).
+// Returns (hi pair, lo pair).
+__device__ __forceinline__ uint2 split2(float x, float y) {
+  typedef _Float16 hh2 __attribute__((ext_vector_type(2)));
+  const hh2 h = __builtin_bit_cast(hh2, __builtin_amdgcn_cvt_pkrtz(x, y));
+  return make_uint2(__builtin_bit_cast(uint32_t, h),
+                    __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(x - static_cast<float>(h[0]),
+                                                                            y - static_cast<float>(h[1]))));
 }
 
 __device__ __forceinline__ fx16 mfma32(const hx8& a, const hx8& b, const fx16& c) {
@@ -1072,115 +1088,249 @@ __device__ __forceinline__ int range_exp(float amax) {
   return std::min(60, std::max(-100, 14 - __builtin_amdgcn_frexp_expf(amax)));
 }
 
-// Keys of chunk `chunk` into khi/klo [64 tokens][kShKRow]: thread = (channel octet o, token
-// quad tq); one (scale, zero) load per channel serves its four tokens.
+// One chunk's global data as a thread holds it between its load and its dequant: the key
+// words of tokens 2tp, 2tp+1 for channels 8o..8o+7; the value words of channel c, tokens
+// 16j..16j+15; threads 0..255 also carry one float4 of the chunk's (scale, zero) block.
 template <int BITS>
-__device__ __forceinline__ void shared_stage_keys(const AttnArgs& a, uint32_t unit, uint32_t chunk,
-                                                  float kf, _Float16* khi, _Float16* klo) {
-  constexpr uint32_t D = 128, PPW = 32 / BITS, KW = D / PPW, MASK = (1u << BITS) - 1u;
+struct ShRaw {
+  static constexpr int KW = BITS == 8 ? 2 : 1;  // words per token per channel octet
+  static constexpr int VW = BITS / 2;           // words per channel per 16 tokens
+  uint32_t k[2][KW];
+  uint32_t v[VW];
+  float4 prm;
+};
+
+// Per-thread base pointers of a unit's chunk data (chunk 0); chunk c adds c times the
+// per-chunk strides, which are the same for every thread.
+template <int BITS>
+struct ShSrc {
+  const uint32_t* k;  // key words of tokens 2tp, 2tp+1, channel octet o
+  const uint32_t* v;  // value words of channel c, tokens 16j..
+  const float4* p;    // one float4 of the chunk's (scale, zero) block
+  static constexpr uint32_t kStride = 64 * (128 * BITS / 32);  // words per chunk, keys
+  static constexpr uint32_t vStride = 128 * (64 * BITS / 32);  // words per chunk, values
+  static constexpr uint32_t pStride = 128;                      // float4 per chunk, either kind
+};
+
+template <int BITS>
+__device__ __forceinline__ ShSrc<BITS> shared_src(const AttnArgs& a, uint32_t unit) {
+  constexpr uint32_t D = 128, PPW = 32 / BITS, KWT = D / PPW, VWC = 64 / PPW;
   const Geometry& g = a.c.geo;
-  const uint32_t o = threadIdx.x % 16, tq = threadIdx.x / 16;
-  const uint64_t t0 = (uint64_t)chunk * 64 + 4 * tq;
-  const float4* pp = reinterpret_cast<const float4*>(a.c.kparams + unit * g.kparams_unit() +
-                                                     (t0 / 32) * D * 2 + 16 * o);
-  float4 p[4];
+  const uint32_t tid = threadIdx.x;
+  const uint32_t o = tid % 16, tp = tid / 16, c = tid % 128, j = tid / 128;
+  ShSrc<BITS> src;
+  src.k = a.c.kcodes + unit * g.kcodes_unit() + (uint64_t)(2 * tp) * KWT + (BITS == 8 ? 2 * o : BITS == 4 ? o : o / 2);
+  src.v = a.c.vcodes + unit * g.vcodes_unit() + c * VWC + j * (BITS / 2);
+  // (scale, zero): keys [2 groups][128][2] and values [4 groups][64][2] are each 512
+  // contiguous floats per chunk; threads 128..255 take values, the others keys (threads
+  // 256.. load a key float4 again and drop it, so there is no branch around the load)
+  src.p = (tid >= 128 && tid < 256)
+              ? reinterpret_cast<const float4*>(a.c.vparams + unit * g.vparams_unit()) + (tid - 128)
+              : reinterpret_cast<const float4*>(a.c.kparams + unit * g.kparams_unit()) + tid % 128;
+  return src;
+}
+
+template <int BITS>
+__device__ __forceinline__ void shared_load(const ShSrc<BITS>& src, uint32_t chunk, ShRaw<BITS>& raw) {
+  constexpr uint32_t KWT = 128 * BITS / 32;
+  const uint32_t* kw = src.k + (uint64_t)chunk * ShSrc<BITS>::kStride;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) p[j] = pp[j];
-  const uint32_t* wp = a.c.kcodes + unit * g.kcodes_unit() + t0 * KW;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    uint32_t w0, w1 = 0;
+  for (int x = 0; x < 2; ++x) {
     if constexpr (BITS == 8) {
-      const uint2 w = *reinterpret_cast<const uint2*>(wp + j * KW + 2 * o);
-      w0 = w.x;
-      w1 = w.y;
-    } else if constexpr (BITS == 4) {
-      w0 = wp[j * KW + o];
+      const uint2 w = *reinterpret_cast<const uint2*>(kw + x * KWT);
+      raw.k[x][0] = w.x;
+      raw.k[x][1] = w.y;
     } else {
-      w0 = wp[j * KW + o / 2] >> (2 * (o % 2));  // channels 8o.. are elements 8(o%2).. of the word
+      raw.k[x][0] = kw[x * KWT];
     }
-    hx8 hi, lo;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      uint32_t code;
-      if constexpr (BITS == 8) code = ((e < 4 ? w0 : w1) >> (8 * (e % 4))) & MASK;
-      else if constexpr (BITS == 4) code = (w0 >> code_shift(4, e)) & MASK;
-      else code = (w0 >> (4 * e)) & MASK;
-      const float s = e % 2 ? p[e / 2].z : p[e / 2].x;
-      const float z = e % 2 ? p[e / 2].w : p[e / 2].y;
-      _Float16 h, l;
-      split_hl(fmaf(static_cast<float>(code), s, z) * kf, h, l);
-      hi[e] = h;
-      lo[e] = l;
-    }
-    *reinterpret_cast<hx8*>(khi + (4 * tq + j) * kShKRow + 8 * o) = hi;
-    *reinterpret_cast<hx8*>(klo + (4 * tq + j) * kShKRow + 8 * o) = lo;
+  }
+  const uint32_t* vw = src.v + (uint64_t)chunk * ShSrc<BITS>::vStride;
+  if constexpr (BITS == 8) {
+    const uint4 w = *reinterpret_cast<const uint4*>(vw);
+    raw.v[0] = w.x; raw.v[1] = w.y; raw.v[2] = w.z; raw.v[3] = w.w;
+  } else if constexpr (BITS == 4) {
+    const uint2 w = *reinterpret_cast<const uint2*>(vw);
+    raw.v[0] = w.x; raw.v[1] = w.y;
+  } else {
+    raw.v[0] = vw[0];
+  }
+  raw.prm = src.p[(uint64_t)chunk * ShSrc<BITS>::pStride];
+}
+
+// (scale, zero) into LDS, pre-multiplied by the range factor of keys (kf) or values (vf)
+// (exact: powers of two), so the dequant is one fma per element.
+template <int BITS>
+__device__ __forceinline__ void shared_store_params(const ShRaw<BITS>& raw, float kf, float vf, float* prm) {
+  if (threadIdx.x < 256) {
+    const float f = threadIdx.x < 128 ? kf : vf;
+    reinterpret_cast<float4*>(prm)[threadIdx.x] =
+        make_float4(raw.prm.x * f, raw.prm.y * f, raw.prm.z * f, raw.prm.w * f);
   }
 }
 
-// Values of chunk `chunk` into vhi/vlo [128 channels][kShVRow], tokens permuted so that a
-// lane's 8 MFMA K-slots are 8 consecutive halves: position 16j + 8h + i holds token
-// 16j + 8(i/4) + 4h + i%4 (bits 2 and 3 swapped), the order in which the S^T output leaves
-// the probabilities in a lane. Thread = (token octet (j, h), channel quad).
+// Dequantize one chunk into a buffer: keys as [64 tokens][kShKRow] hi and lo, values as
+// [128 channels][kShVRow] hi and lo with the tokens permuted so that a lane's 8 MFMA K-slots
+// are 8 consecutive halves: position 16j + 8h + i holds token 16j + 8(i/4) + 4h + i%4 (bits 2
+// and 3 swapped), the order in which the S^T output leaves the probabilities in a lane.
 template <int BITS>
-__device__ __forceinline__ void shared_stage_values(const AttnArgs& a, uint32_t unit, uint32_t chunk,
-                                                    float vf, _Float16* vhi, _Float16* vlo) {
-  constexpr uint32_t D = 128, PPW = 32 / BITS, VW = 64 / PPW, MASK = (1u << BITS) - 1u;
-  const Geometry& g = a.c.geo;
-  const uint32_t oc = threadIdx.x % 8, cq = threadIdx.x / 8;
-  const uint32_t j = oc / 2, h = oc % 2, cg = cq / 8;
-  const float4* pp = reinterpret_cast<const float4*>(
-      a.c.vparams + unit * g.vparams_unit() + (((uint64_t)chunk * g.ncg() + cg) * 64 + 16 * j + 4 * h) * 2);
-  const float4 p[4] = {pp[0], pp[1], pp[4], pp[5]};  // tokens +0,1 | +2,3 | +8,9 | +10,11
-  const uint32_t* wbase = a.c.vcodes + unit * g.vcodes_unit() + (uint64_t)chunk * D * VW;
-#pragma unroll
-  for (int x = 0; x < 4; ++x) {
-    const uint32_t c = 4 * cq + x;
-    const uint32_t* wc = wbase + c * VW;
-    uint32_t w0, w1;
-    if constexpr (BITS == 8) {
-      w0 = wc[4 * j + h];
-      w1 = wc[4 * j + 2 + h];
-    } else if constexpr (BITS == 4) {
-      const uint2 w = *reinterpret_cast<const uint2*>(wc + 2 * j);
-      w0 = w.x >> (4 * h);
-      w1 = w.y >> (4 * h);
-    } else {
-      w0 = wc[j] >> (16 * h);
-      w1 = w0 >> 2;
-    }
-    hx8 hi, lo;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const uint32_t w = e < 4 ? w0 : w1;
-      const uint32_t i = e % 4;
-      uint32_t code;
-      if constexpr (BITS == 8) code = (w >> (8 * i)) & MASK;
-      else if constexpr (BITS == 4) code = (w >> (8 * i)) & MASK;
-      else code = (w >> (4 * i)) & MASK;
-      const float4 q = p[e / 2];
-      const float s = e % 2 ? q.z : q.x;
-      const float z = e % 2 ? q.w : q.y;
-      _Float16 hh, ll;
-      split_hl(fmaf(static_cast<float>(code), s, z) * vf, hh, ll);
-      hi[e] = hh;
-      lo[e] = ll;
-    }
-    *reinterpret_cast<hx8*>(vhi + c * kShVRow + 16 * j + 8 * h) = hi;
-    *reinterpret_cast<hx8*>(vlo + c * kShVRow + 16 * j + 8 * h) = lo;
-  }
-}
-
-// One workgroup: rows [rblk*128, +128) of `unit` over packed chunks of split `split` (a
-// contiguous range), partials into split index `split` of each row's session.
-template <int BITS>
-__device__ __forceinline__ void shared_split(const AttnArgs& a, uint32_t unit, uint32_t rblk,
-                                             uint32_t split, _Float16* lds) {
-  constexpr uint32_t D = 128;
-  _Float16* khi = lds;
+__device__ __forceinline__ void shared_dequant(const ShRaw<BITS>& raw, const float* prm, _Float16* buf) {
+  constexpr uint32_t MASK = (1u << BITS) - 1u;
+  _Float16* khi = buf;
   _Float16* klo = khi + 64 * kShKRow;
   _Float16* vhi = klo + 64 * kShKRow;
   _Float16* vlo = vhi + 128 * kShVRow;
+  const uint32_t tid = threadIdx.x;
+  {
+    const uint32_t o = tid % 16, tp = tid / 16;
+    const float4* pk = reinterpret_cast<const float4*>(prm + ((tp / 16) * 128 + 8 * o) * 2);
+    float sc[8], zr[8];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float4 v = pk[q];
+      sc[2 * q] = v.x; zr[2 * q] = v.y;
+      sc[2 * q + 1] = v.z; zr[2 * q + 1] = v.w;
+    }
+#pragma unroll
+    for (int x = 0; x < 2; ++x) {
+      float d[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        uint32_t code;
+        if constexpr (BITS == 8) code = (raw.k[x][e / 4] >> (8 * (e % 4))) & MASK;
+        else if constexpr (BITS == 4) code = (raw.k[x][0] >> code_shift(4, e)) & MASK;
+        else code = (raw.k[x][0] >> (2 * (o % 2) + 4 * e)) & MASK;  // elements 8(o%2) + e
+        d[e] = fmaf(static_cast<float>(code), sc[e], zr[e]);
+      }
+      ux4 hi, lo;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+      const uint2 t2 = split2(d[2 * q], d[2 * q + 1]);
+      hi[q] = t2.x;
+      lo[q] = t2.y;
+    }
+      *reinterpret_cast<ux4*>(khi + (2 * tp + x) * kShKRow + 8 * o) = hi;
+      *reinterpret_cast<ux4*>(klo + (2 * tp + x) * kShKRow + 8 * o) = lo;
+    }
+  }
+  {
+    const uint32_t c = tid % 128, j = tid / 128;
+    const float4* pv = reinterpret_cast<const float4*>(prm + 512 + ((c / 32) * 64 + 16 * j) * 2);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      float d[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int k = 8 * (i / 4) + 4 * h + i % 4;  // token within the 16-token run
+        uint32_t code;
+        if constexpr (BITS == 8) code = (raw.v[k / 4] >> (8 * (k % 4))) & MASK;
+        else if constexpr (BITS == 4) code = (raw.v[k / 8] >> code_shift(4, k % 8)) & MASK;
+        else code = (raw.v[0] >> code_shift(2, k)) & MASK;
+        const float4 p = pv[k / 2];
+        d[i] = fmaf(static_cast<float>(code), k % 2 ? p.z : p.x, k % 2 ? p.w : p.y);
+      }
+      ux4 hi, lo;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+      const uint2 t2 = split2(d[2 * q], d[2 * q + 1]);
+      hi[q] = t2.x;
+      lo[q] = t2.y;
+    }
+      *reinterpret_cast<ux4*>(vhi + c * kShVRow + 16 * j + 8 * h) = hi;
+      *reinterpret_cast<ux4*>(vlo + c * kShVRow + 16 * j + 8 * h) = lo;
+    }
+  }
+}
+
+// Logits of one chunk for a wave's 32 rows: S^T tiles of tokens r and 32 + r.
+__device__ __forceinline__ void shared_logits(const _Float16* buf, const hx8 (&qhi)[8], const hx8 (&qlo)[8],
+                                              fx16& s0, fx16& s1) {
+  const uint32_t lane = threadIdx.x % 64, h = lane / 32, r = lane % 32;
+  const _Float16* khi = buf;
+  const _Float16* klo = khi + 64 * kShKRow;
+#pragma unroll
+  for (int v = 0; v < 16; ++v) {
+    s0[v] = 0.f;
+    s1[v] = 0.f;
+  }
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    const hx8 kh0 = *reinterpret_cast<const hx8*>(khi + r * kShKRow + 16 * s + 8 * h);
+    const hx8 kl0 = *reinterpret_cast<const hx8*>(klo + r * kShKRow + 16 * s + 8 * h);
+    const hx8 kh1 = *reinterpret_cast<const hx8*>(khi + (32 + r) * kShKRow + 16 * s + 8 * h);
+    const hx8 kl1 = *reinterpret_cast<const hx8*>(klo + (32 + r) * kShKRow + 16 * s + 8 * h);
+    s0 = mfma32(kh0, qhi[s], s0);
+    s1 = mfma32(kh1, qhi[s], s1);
+    s0 = mfma32(kh0, qlo[s], s0);
+    s1 = mfma32(kh1, qlo[s], s1);
+    s0 = mfma32(kl0, qhi[s], s0);
+    s1 = mfma32(kl1, qhi[s], s1);
+  }
+}
+
+// Online softmax of one chunk's logits and the value mix for a wave's 32 rows.
+__device__ __forceinline__ void shared_mix(const _Float16* buf, const fx16& s0, const fx16& s1,
+                                           float s_unscale, float& m, float& l, fx16 (&o)[4]) {
+  const uint32_t lane = threadIdx.x % 64, h = lane / 32, r = lane % 32;
+  const _Float16* vhi = buf + 2 * 64 * kShKRow;
+  const _Float16* vlo = vhi + 128 * kShVRow;
+  // online softmax over the chunk (the lane pair r, r + 32 holds the row's 64 logits); the
+  // probabilities come out as p * 2^14 (the P operand range), and so does l
+  float mx = -INFINITY;
+#pragma unroll
+  for (int v = 0; v < 16; ++v) mx = fmaxf(mx, fmaxf(s0[v], s1[v]));
+  mx = fmaxf(mx, __shfl_xor(mx, 32));
+  const float mnew = fmaxf(m, mx * s_unscale);
+  const float alpha = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mnew);
+  m = mnew;
+  const float off = 14.f - mnew;
+  if (__ballot(alpha != 1.f)) {
+    l *= alpha;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) o[mt][v] *= alpha;
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    // P^T K-step j: tokens 16j .. 16j + 15 = tile j/2, values 8(j%2) .. 8(j%2) + 7
+    float p[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float sv = j < 2 ? s0[8 * (j % 2) + i] : s1[8 * (j % 2) + i];
+      p[i] = __builtin_amdgcn_exp2f(fmaf(sv, s_unscale, off));
+      l += p[i];
+    }
+    ux4 ph, pl;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint2 t2 = split2(p[2 * q], p[2 * q + 1]);
+      ph[q] = t2.x;
+      pl[q] = t2.y;
+    }
+    const hx8 phh = __builtin_bit_cast(hx8, ph), pll = __builtin_bit_cast(hx8, pl);
+    hx8 vh[4], vl[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      vh[mt] = *reinterpret_cast<const hx8*>(vhi + (32 * mt + r) * kShVRow + 16 * j + 8 * h);
+      vl[mt] = *reinterpret_cast<const hx8*>(vlo + (32 * mt + r) * kShVRow + 16 * j + 8 * h);
+    }
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) o[mt] = mfma32(vh[mt], phh, o[mt]);
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) o[mt] = mfma32(vh[mt], pll, o[mt]);
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) o[mt] = mfma32(vl[mt], phh, o[mt]);
+  }
+}
+
+// One workgroup: rows [rblk*256, +256) of `unit` over the packed chunks of split `split` (a
+// contiguous range), partials into split index `split` of each row's session.
+template <int BITS>
+__device__ __forceinline__ void shared_split(const AttnArgs& a, uint32_t unit, uint32_t rblk,
+                                             uint32_t split, uint8_t* lds) {
+  constexpr uint32_t D = 128;
+  _Float16* bufs = reinterpret_cast<_Float16*>(lds);  // [2][kShBufHalves]
+  float* prms = reinterpret_cast<float*>(lds + 2 * (size_t)kShBufHalves * sizeof(_Float16));  // [2][1024]
   const uint32_t lane = threadIdx.x % 64, wave = threadIdx.x / 64, h = lane / 32, r = lane % 32;
   const uint32_t gq = a.gq;
   const uint32_t row = rblk * kShRows + wave * 32 + r;
@@ -1209,19 +1359,22 @@ __device__ __forceinline__ void shared_split(const AttnArgs& a, uint32_t unit, u
   const float qfac = ldexpf(1.f, eq);
   hx8 qhi[8], qlo[8];
 #pragma unroll
-  for (int s = 0; s < 8; ++s)
+  for (int s = 0; s < 8; ++s) {
+    ux4 hi, lo;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      _Float16 hh, ll;
-      split_hl(qf[s][i] * qfac, hh, ll);
-      qhi[s][i] = hh;
-      qlo[s][i] = ll;
+    for (int q = 0; q < 4; ++q) {
+      const uint2 t2 = split2(qf[s][2 * q] * qfac, qf[s][2 * q + 1] * qfac);
+      hi[q] = t2.x;
+      lo[q] = t2.y;
     }
+    qhi[s] = __builtin_bit_cast(hx8, hi);
+    qlo[s] = __builtin_bit_cast(hx8, lo);
+  }
   const int ek = range_exp(__uint_as_float(a.c.smax[4 * unit + 2]));
   const int ev = range_exp(__uint_as_float(a.c.smax[4 * unit + 3]));
   const float kf = ldexpf(1.f, ek), vf = ldexpf(1.f, ev);
   const float s_unscale = ldexpf(1.f, -ek - eq);
-  const float o_unscale = ldexpf(1.f, -ev) / kShPScale;
+  const float o_unscale = ldexpf(1.f, -ev) / kShPScale;  // O and l carry the 2^14 of P
 
   const uint32_t cps = (a.chunk_end + a.nsplit_fast - 1) / a.nsplit_fast;
   const uint32_t c0 = std::min(a.chunk_end, split * cps);
@@ -1233,72 +1386,32 @@ __device__ __forceinline__ void shared_split(const AttnArgs& a, uint32_t unit, u
 #pragma unroll
     for (int v = 0; v < 16; ++v) o[mt][v] = 0.f;
 
-  for (uint32_t c = c0; c < c1; ++c) {
-    __syncthreads();  // the previous chunk's operands are consumed
-    shared_stage_keys<BITS>(a, unit, c, kf, khi, klo);
-    shared_stage_values<BITS>(a, unit, c, vf, vhi, vlo);
+  if (c0 < c1) {
+    // Chunks past the split's end are clamped to its last chunk: their loads stay in bounds and
+    // their dequant goes to the buffer no later iteration reads.
+    const ShSrc<BITS> src = shared_src<BITS>(a, unit);
+    ShRaw<BITS> cur, nxt;
+    shared_load<BITS>(src, c0, cur);
+    shared_store_params<BITS>(cur, kf, vf, prms + (c0 % 2) * kShParamFloats);
     __syncthreads();
-    // S^T: tokens r (tile 0) and 32 + r (tile 1) against the lane's row
-    fx16 s0, s1;
-#pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      s0[v] = 0.f;
-      s1[v] = 0.f;
+    shared_dequant<BITS>(cur, prms + (c0 % 2) * kShParamFloats, bufs + (c0 % 2) * kShBufHalves);
+    shared_load<BITS>(src, std::min(c0 + 1, c1 - 1), cur);
+    shared_store_params<BITS>(cur, kf, vf, prms + ((c0 + 1) % 2) * kShParamFloats);
+    __syncthreads();
+    // Top of iteration c: buffer c%2 holds chunk c; params (c+1)%2 and `cur` hold chunk c+1.
+    // The dequant of chunk c+1 comes first, so `cur` is dead before the logit registers are
+    // live (no spills at 256 VGPRs).
+    for (uint32_t c = c0; c < c1; ++c) {
+      shared_load<BITS>(src, std::min(c + 2, c1 - 1), nxt);
+      const _Float16* buf = bufs + (c % 2) * kShBufHalves;
+      shared_dequant<BITS>(cur, prms + ((c + 1) % 2) * kShParamFloats, bufs + ((c + 1) % 2) * kShBufHalves);
+      fx16 s0, s1;
+      shared_logits(buf, qhi, qlo, s0, s1);
+      shared_mix(buf, s0, s1, s_unscale, m, l, o);
+      shared_store_params<BITS>(nxt, kf, vf, prms + (c % 2) * kShParamFloats);
+      cur = nxt;
+      __syncthreads();
     }
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      const hx8 kh0 = *reinterpret_cast<const hx8*>(khi + r * kShKRow + 16 * s + 8 * h);
-      const hx8 kl0 = *reinterpret_cast<const hx8*>(klo + r * kShKRow + 16 * s + 8 * h);
-      const hx8 kh1 = *reinterpret_cast<const hx8*>(khi + (32 + r) * kShKRow + 16 * s + 8 * h);
-      const hx8 kl1 = *reinterpret_cast<const hx8*>(klo + (32 + r) * kShKRow + 16 * s + 8 * h);
-      s0 = mfma32(kh0, qhi[s], s0);
-      s1 = mfma32(kh1, qhi[s], s1);
-      s0 = mfma32(kh0, qlo[s], s0);
-      s1 = mfma32(kh1, qlo[s], s1);
-      s0 = mfma32(kl0, qhi[s], s0);
-      s1 = mfma32(kl1, qhi[s], s1);
-    }
-    // online softmax over the chunk (the lane pair r, r + 32 holds the row's 64 logits)
-    float mx = -INFINITY;
-#pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      s0[v] *= s_unscale;
-      s1[v] *= s_unscale;
-      mx = fmaxf(mx, fmaxf(s0[v], s1[v]));
-    }
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float mnew = fmaxf(m, mx);
-    const float alpha = m == -INFINITY ? 0.f : exp2f(m - mnew);
-    m = mnew;
-    float psum = 0.f;
-    hx8 ph[4], pl[4];  // P^T K-steps: tokens 16j .. 16j + 15 (tile j/2, values 8(j%2) ..)
-#pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const float p0 = exp2f(s0[v] - mnew), p1 = exp2f(s1[v] - mnew);
-      psum += p0 + p1;
-      _Float16 hh, ll;
-      split_hl(p0 * kShPScale, hh, ll);
-      ph[v / 8][v % 8] = hh;
-      pl[v / 8][v % 8] = ll;
-      split_hl(p1 * kShPScale, hh, ll);
-      ph[2 + v / 8][v % 8] = hh;
-      pl[2 + v / 8][v % 8] = ll;
-    }
-    l = fmaf(l, alpha, psum);
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) o[mt][v] *= alpha;
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
-        const hx8 vh = *reinterpret_cast<const hx8*>(vhi + (32 * mt + r) * kShVRow + 16 * j + 8 * h);
-        const hx8 vl = *reinterpret_cast<const hx8*>(vlo + (32 * mt + r) * kShVRow + 16 * j + 8 * h);
-        o[mt] = mfma32(vh, ph[j], o[mt]);
-        o[mt] = mfma32(vh, pl[j], o[mt]);
-        o[mt] = mfma32(vl, ph[j], o[mt]);
-      }
   }
   l += __shfl_xor(l, 32);
   if (!live) return;
@@ -1315,32 +1428,21 @@ __device__ __forceinline__ void shared_split(const AttnArgs& a, uint32_t unit, u
     }
   if (h == 0) {
     part[D] = c1 > c0 ? m : -INFINITY;
-    part[D + 1] = c1 > c0 ? l : 0.f;
+    part[D + 1] = c1 > c0 ? l / kShPScale : 0.f;
   }
 }
 
-// Batched sessions, GEMM form: workgroups [0, nsess*units*nsplit_win) take one window /
-// suffix chunk of one session (as k_attn_sessions); the rest one (unit, row block, split) of
-// the packed prefix chunks for all sessions' rows at once.
-template <int BITS, int NRS>
-__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
-    k_attn_shared(AttnArgs a, SessionTable t) {
+// Batched sessions, GEMM form: one workgroup per (unit, 256-row block, split) of the packed
+// prefix chunks, for all sessions' rows at once. The split ranges are contiguous; the row
+// blocks of one split are nsplit_fast apart in the grid (a multiple of the XCD count when
+// nsplit_fast is), so they share an L2.
+template <int BITS>
+__global__ void __launch_bounds__(kShThreads) k_attn_shared(AttnArgs a) {
   extern __shared__ float lds[];
-  const uint32_t per_sess = a.units * a.nsplit_win;
-  const uint32_t nwin = a.nsess * per_sess;
-  if (blockIdx.x < nwin) {
-    const uint32_t s = blockIdx.x / per_sess, r = blockIdx.x % per_sess;
-    const AttnArgs as = session_args(a, t, s);
-    mfma_split<BITS, NRS, 1, true>(as, r / a.nsplit_win, r % a.nsplit_win, lds);
-  } else {
-    // (unit, row block) outer, split inner: the row blocks of one split are nsplit_fast apart
-    // in the grid, a multiple of the XCD count when nsplit_fast is, so they share an L2
-    const uint32_t blk = blockIdx.x - nwin;
-    const uint32_t rblocks = (a.nsess * a.gq + kShRows - 1) / kShRows;
-    const uint32_t unit = blk / (rblocks * a.nsplit_fast);
-    const uint32_t rem = blk % (rblocks * a.nsplit_fast);
-    shared_split<BITS>(a, unit, rem / a.nsplit_fast, rem % a.nsplit_fast, reinterpret_cast<_Float16*>(lds));
-  }
+  const uint32_t rblocks = (a.nsess * a.gq + kShRows - 1) / kShRows;
+  const uint32_t unit = blockIdx.x / (rblocks * a.nsplit_fast);
+  const uint32_t rem = blockIdx.x % (rblocks * a.nsplit_fast);
+  shared_split<BITS>(a, unit, rem / a.nsplit_fast, rem % a.nsplit_fast, reinterpret_cast<uint8_t*>(lds));
 }
 
 // ------------------------------------------------------------------ planning
@@ -1525,8 +1627,8 @@ uint64_t longest_suffix(const SessionsProblem& sp, uint32_t first, uint32_t coun
 // Rows (sessions x GQA heads) from which one launch group takes the GEMM form: below it a
 // 32-row MFMA tile would be mostly padding and the per-session form does less work.
 constexpr uint32_t kSharedMinRows = 16;
-// Workgroups the GEMM form aims for (two per CU: 70 KB of LDS each).
-constexpr uint32_t kSharedTargetGroups = 512;
+// Workgroups the GEMM form aims for (one per CU: 148 KB of LDS each).
+constexpr uint32_t kSharedTargetGroups = 256;
 
 bool use_shared(const SessionsProblem& sp, uint32_t nsess) {
   return nsess * (sp.qh / sp.heads) >= kSharedMinRows;
@@ -1560,20 +1662,26 @@ hipError_t launch_sessions(const AttnArgs& a, const SessionTable& t, hipStream_t
 
 template <int BITS, int NRS>
 hipError_t launch_shared(const AttnArgs& a, const SessionTable& t, hipStream_t stream) {
-  constexpr int NH = 4 * NRS;
-  static_assert((size_t)4 * NH * (128 + 2) * sizeof(float) <= kShLdsBytes, "window path LDS");
-  static_assert((size_t)4 * NH * (64 + kRowPad) * sizeof(float) <= kShLdsBytes, "window path LDS");
+  // window / suffix chunks per session: the window workgroups of the per-session kernel
+  const uint32_t nwin = a.nsess * a.units * a.nsplit_win;
+  if (nwin > 0) {
+    constexpr int NH = 4 * NRS;
+    const size_t lds = (size_t)4 * NH * (128 + 2) * sizeof(float);
+    k_attn_sessions<BITS, NRS><<<nwin, kThreads, lds, stream>>>(a, t);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  if (a.nsplit_fast == 0) return hipSuccess;
   static bool configured = false;  // the attribute is per kernel and per process
   if (!configured) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_shared<BITS, NRS>),
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_shared<BITS>),
                                              hipFuncAttributeMaxDynamicSharedMemorySize,
                                              static_cast<int>(kShLdsBytes));
     if (e != hipSuccess) return e;
     configured = true;
   }
   const uint32_t rblocks = (a.nsess * a.gq + kShRows - 1) / kShRows;
-  const uint32_t grid = a.nsess * a.units * a.nsplit_win + a.units * rblocks * a.nsplit_fast;
-  k_attn_shared<BITS, NRS><<<grid, kThreads, kShLdsBytes, stream>>>(a, t);
+  k_attn_shared<BITS><<<a.units * rblocks * a.nsplit_fast, kShThreads, kShLdsBytes, stream>>>(a);
   return hipGetLastError();
 }
 
