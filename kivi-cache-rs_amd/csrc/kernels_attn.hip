@@ -141,6 +141,16 @@ __device__ __forceinline__ float warp_sum(float v) {
   return v;
 }
 
+// Split partials are exchanged between workgroups that may sit on different XCDs (separate
+// L2s): they are written and read with device-coherent (agent-scope) accesses, so the merge
+// needs no L2 write-back or invalidation.
+__device__ __forceinline__ void store_partial(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_partial(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // ------------------------------------------------------------------ generic splits
 // One workgroup per (unit, split) over tokens [t_begin, total). LDS: q [gq][D], logits/weights
 // [gq][S]. Instantiated for every shape (BITS = DD = GG = 0) and, with the shape fixed, for the
@@ -212,8 +222,8 @@ __device__ __forceinline__ void generic_split(const AttnArgs& a, uint32_t unit, 
     }
     l = warp_sum(l);
     if (lane == 0) {
-      part[h * (D + 2) + D] = m;
-      part[h * (D + 2) + D + 1] = l;
+      store_partial(part + h * (D + 2) + D, m);
+      store_partial(part + h * (D + 2) + D + 1, l);
     }
   }
   __syncthreads();
@@ -238,59 +248,62 @@ __device__ __forceinline__ void generic_split(const AttnArgs& a, uint32_t unit, 
     }
 #pragma unroll
     for (int h = 0; h < kHeadsPerPass; ++h)
-      if (h < (int)nh) part[(h0 + h) * (D + 2) + d] = acc[h];
+      if (h < (int)nh) store_partial(part + (h0 + h) * (D + 2) + d, acc[h]);
   }
 }
 
-// Log-sum-exp merge of one unit's split partials into out, one head at a time (LDS: nsplit
-// factors + 8 reduction slots).
+// Log-sum-exp merge of one unit's split partials into out: wave w merges heads w, w+4, ...
+// with wave-local reductions (LDS: nsplit factors per wave). Each split's (m, l) pair is read
+// once, then its D accumulators, so a head costs two rounds of loads.
 __device__ void merge_unit(const float* ws, uint32_t unit, uint32_t nsplit, uint32_t gq, uint32_t D,
                            uint32_t heads, uint32_t qh, float* out, float* f_lds) {
-  float* red = f_lds + nsplit;
   const uint32_t b = unit / heads, kvh = unit % heads;
-  const uint32_t lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+  const uint32_t lane = threadIdx.x % 64, wave = threadIdx.x / 64, nwave = blockDim.x / 64;
   const uint64_t stride = (uint64_t)gq * (D + 2);
-  for (uint32_t h = 0; h < gq; ++h) {
+  float* fw = f_lds + wave * nsplit;
+  for (uint32_t h = wave; h < gq; h += nwave) {
     const float* base = ws + (uint64_t)unit * nsplit * stride + h * (D + 2);
     float m = -INFINITY;
-    for (uint32_t s = threadIdx.x; s < nsplit; s += blockDim.x) m = fmaxf(m, base[s * stride + D]);
-    m = warp_max(m);
-    if (lane == 0) red[wave] = m;
-    __syncthreads();
-    const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    float l = 0.f;
-    for (uint32_t s = threadIdx.x; s < nsplit; s += blockDim.x) {
-      const float ms = base[s * stride + D];
-      const float f = ms == -INFINITY ? 0.f : exp2f(ms - M);
-      f_lds[s] = f;
-      l += base[s * stride + D + 1] * f;
+    for (uint32_t s = lane; s < nsplit; s += 64) {
+      const float ms = load_partial(base + s * stride + D);
+      fw[s] = ms;
+      m = fmaxf(m, ms);
     }
-    l = warp_sum(l);
-    if (lane == 0) red[4 + wave] = l;
-    __syncthreads();
-    const float inv = 1.0f / (red[4] + red[5] + red[6] + red[7]);
+    const float M = warp_max(m);
+    float l = 0.f;
+    for (uint32_t s = lane; s < nsplit; s += 64) {
+      const float ms = fw[s];
+      const float f = ms == -INFINITY ? 0.f : exp2f(ms - M);
+      fw[s] = f;
+      l += load_partial(base + s * stride + D + 1) * f;
+    }
+    const float inv = 1.0f / warp_sum(l);
     float* o = out + ((uint64_t)b * qh + kvh * gq + h) * D;
-    for (uint32_t d = threadIdx.x; d < D; d += blockDim.x) {
+    for (uint32_t d = lane; d < D; d += 64) {
       float acc = 0.f;
-      for (uint32_t s = 0; s < nsplit; ++s) acc = fmaf(base[s * stride + d], f_lds[s], acc);
+      for (uint32_t s = 0; s < nsplit; ++s) acc = fmaf(load_partial(base + s * stride + d), fw[s], acc);
       o[d] = acc * inv;
     }
-    __syncthreads();  // f_lds and red are reused by the next head
   }
 }
 
-// Called by every split workgroup after its partial is written: the last of the unit's
-// splits to finish (device-scope counter) merges the unit and re-arms the counter.
+// Called by every split workgroup after its partial is written (agent-scope stores): each
+// thread waits until its stores are acknowledged, then one thread counts the split in with an
+// agent-scope atomic. The last of the unit's splits to arrive merges the unit (agent-scope
+// loads) and re-arms the counter.
 __device__ void finish_split(const AttnArgs& a, uint32_t unit, float* lds) {
   __shared__ uint32_t is_last;
-  __threadfence();  // release this workgroup's partial
+  __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed
   __syncthreads();
-  if (threadIdx.x == 0) is_last = atomicAdd(&a.counters[unit], 1u) == a.nsplit_total - 1 ? 1u : 0u;
+  if (threadIdx.x == 0)
+    is_last = __hip_atomic_fetch_add(&a.counters[unit], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                      a.nsplit_total - 1
+                  ? 1u
+                  : 0u;
   __syncthreads();
   if (is_last == 0u) return;
-  __threadfence();  // acquire every split's partial
   merge_unit(a.ws, unit, a.nsplit_total, a.gq, a.c.geo.D, a.heads, a.qh, a.out, lds);
-  if (threadIdx.x == 0) atomicExch(&a.counters[unit], 0u);
+  if (threadIdx.x == 0) __hip_atomic_store(&a.counters[unit], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int BITS, int DD, int GG>
@@ -926,7 +939,7 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
         v += (d == D + 1 ? c[D + 1] : c[d]) * f;
       }
     }
-    part[h * (D + 2) + d] = v;
+    store_partial(part + h * (D + 2) + d, v);
   }
 }
 
@@ -1448,6 +1461,9 @@ __global__ void __launch_bounds__(kShThreads) k_attn_shared(AttnArgs a) {
 // ------------------------------------------------------------------ planning
 
 constexpr size_t kMaxMergeLds = 48 * 1024;  // in-kernel merge up to ~12K splits per unit
+// The in-kernel merge is correct but measured slower at C2 (137 us kernel vs 122 + 8.5 us for
+// the two launches): every split then waits for its stores and a device-scope atomic before
+// it retires, and the last split of a unit merges on the critical path.
 constexpr bool kUseInKernelMerge = false;
 
 uint32_t split_tokens(uint32_t gq) {
@@ -1500,10 +1516,9 @@ AttnArgs make_args(const AttnProblem& p, float* ws) {
   a.units = p.cache.geo.units;
   a.nsess = 0;
   a.q_sess_stride = a.ws_sess_stride = 0;
-  // The in-kernel merge (last split per unit) needs device-scope release/acquire fences, which
-  // on this multi-XCD part write back and invalidate L2 for every workgroup; the separate
-  // merge launch is faster, so the counters stay unused for now.
-  a.counters = kUseInKernelMerge && (a.nsplit_total + 8) * sizeof(float) <= kMaxMergeLds ? p.counters : nullptr;
+  // With kUseInKernelMerge the last split of each unit merges it in the same launch (partials
+  // exchanged through agent-scope accesses, no L2 write-back or invalidation).
+  a.counters = kUseInKernelMerge && (size_t)4 * a.nsplit_total * sizeof(float) <= kMaxMergeLds ? p.counters : nullptr;
   return a;
 }
 
@@ -1512,7 +1527,7 @@ hipError_t launch_fast(const AttnArgs& a, double bytes, hipStream_t stream) {
   constexpr int NH = 4 * NRS;
   const size_t logits = (size_t)4 * NH * ((a.nsplit_fast > 0 ? kFastCpw : 1) * 64 + kRowPad);
   const size_t combine = (size_t)4 * NH * (128 + 2);
-  const size_t merge = a.counters != nullptr ? (size_t)a.nsplit_total + 8 : 0;
+  const size_t merge = a.counters != nullptr ? (size_t)4 * a.nsplit_total : 0;
   const size_t lds = std::max(std::max(logits, combine), merge) * sizeof(float);
   TimedLaunch timed(KIVI_KERNEL_ATTN_PACKED, stream, bytes);
   k_attn_mfma<BITS, NRS><<<a.units * (a.nsplit_win + a.nsplit_fast), kThreads, lds, stream>>>(a);
@@ -1533,7 +1548,7 @@ hipError_t dispatch_fast(const AttnArgs& a, double bytes, hipStream_t stream) {
 }
 
 hipError_t dispatch_generic(const AttnArgs& a, hipStream_t stream) {
-  const size_t merge = a.counters != nullptr ? (size_t)a.nsplit_total + 8 : 0;
+  const size_t merge = a.counters != nullptr ? (size_t)4 * a.nsplit_total : 0;
   const size_t lds = std::max((size_t)a.gq * a.c.geo.D + (size_t)a.gq * a.S, merge) * sizeof(float);
   k_attn_generic<0, 0, 0><<<a.units * a.nsplit_gen, kThreads, lds, stream>>>(a);
   return hipGetLastError();
