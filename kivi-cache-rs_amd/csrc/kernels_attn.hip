@@ -1010,43 +1010,42 @@ __global__ void __launch_bounds__(kThreads) k_attn_sessions(AttnArgs a, SessionT
   }
 }
 
-// Log-sum-exp merge of the split partials: one workgroup per (unit, head). LDS holds the
-// per-split factors 2^(m_s - M).
-__global__ void __launch_bounds__(kThreads)
+// Log-sum-exp merge of the split partials: one workgroup of D threads per (session, unit,
+// head). Every wave reduces the splits' (m, l) pairs itself (no barrier), then thread d sums
+// channel d over the splits with the factors 2^(m_s - M); no LDS, so any split count fits.
+__global__ void __launch_bounds__(256)
     k_attn_merge(const float* ws, uint32_t nsplit, uint32_t gq, uint32_t D, uint32_t heads,
                  uint32_t qh, float* out, uint32_t units, uint64_t ws_sess_stride,
                  uint64_t out_sess_stride) {
-  extern __shared__ float f_lds[];  // [nsplit] factors, then 8 reduction slots
-  float* red = f_lds + nsplit;
+  const uint32_t lane = threadIdx.x % 64;
   const uint32_t sess = blockIdx.x / (units * gq);
-  ws += sess * ws_sess_stride;
-  out += sess * out_sess_stride;
   const uint32_t unit = (blockIdx.x / gq) % units, h = blockIdx.x % gq;
   const uint32_t b = unit / heads, kvh = unit % heads;
-  const float* base = ws + (uint64_t)unit * nsplit * gq * (D + 2) + h * (D + 2);
   const uint64_t stride = (uint64_t)gq * (D + 2);
-  const uint32_t lane = threadIdx.x % 64, wave = threadIdx.x / 64;
-  float m = -INFINITY;
-  for (uint32_t s = threadIdx.x; s < nsplit; s += blockDim.x) m = fmaxf(m, base[s * stride + D]);
-  m = warp_max(m);
-  if (lane == 0) red[wave] = m;
-  __syncthreads();
-  const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  float l = 0.f;
-  for (uint32_t s = threadIdx.x; s < nsplit; s += blockDim.x) {
-    const float ms = base[s * stride + D];
-    const float f = ms == -INFINITY ? 0.f : exp2f(ms - M);
-    f_lds[s] = f;
-    l += base[s * stride + D + 1] * f;
+  const float* base = ws + sess * ws_sess_stride + (uint64_t)unit * nsplit * stride + h * (D + 2);
+  float m = -INFINITY, l = 0.f;
+  for (uint32_t s = lane; s < nsplit; s += 64) {
+    const float ms = base[s * stride + D], ls = base[s * stride + D + 1];
+    // running (max, sum) of this lane's splits
+    if (ms > m) {
+      l = l * __builtin_amdgcn_exp2f(m - ms) + ls;  // m = -inf first: the factor is 0
+      m = ms;
+    } else if (ms != -INFINITY) {
+      l += ls * __builtin_amdgcn_exp2f(ms - m);
+    }
   }
-  l = warp_sum(l);
-  if (lane == 0) red[4 + wave] = l;
-  __syncthreads();
-  const float inv = 1.0f / (red[4] + red[5] + red[6] + red[7]);
-  float* o = out + ((uint64_t)b * qh + kvh * gq + h) * D;
+  const float M = warp_max(m);
+  l = m == -INFINITY ? 0.f : l * __builtin_amdgcn_exp2f(m - M);
+  const float inv = 1.0f / warp_sum(l);
+  float* o = out + sess * out_sess_stride + ((uint64_t)b * qh + kvh * gq + h) * D;
   for (uint32_t d = threadIdx.x; d < D; d += blockDim.x) {
     float acc = 0.f;
-    for (uint32_t s = 0; s < nsplit; ++s) acc = fmaf(base[s * stride + d], f_lds[s], acc);
+#pragma unroll 4
+    for (uint32_t s = 0; s < nsplit; ++s) {
+      const float ms = base[s * stride + D];
+      const float f = ms == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms - M);
+      acc = fmaf(base[s * stride + d], f, acc);
+    }
     o[d] = acc * inv;
   }
 }
@@ -1589,11 +1588,10 @@ hipError_t launch_attention(const AttnProblem& p, float* workspace, hipStream_t 
     if (e != hipSuccess) return e;
   }
   if (a.counters == nullptr) {
-    const size_t merge_lds = ((size_t)a.nsplit_total + 8) * sizeof(float);
     const double bytes = (double)units * a.gq * ((double)a.nsplit_total * (g.D + 2) + g.D) * 4.0;
     TimedLaunch timed(KIVI_KERNEL_ATTN_MERGE, stream, bytes);
-    k_attn_merge<<<units * a.gq, kThreads, merge_lds, stream>>>(workspace, a.nsplit_total, a.gq,
-                                                                g.D, p.heads, p.qh, p.out, units, 0, 0);
+    k_attn_merge<<<units * a.gq, std::min(256u, (g.D + 63) / 64 * 64), 0, stream>>>(
+        workspace, a.nsplit_total, a.gq, g.D, p.heads, p.qh, p.out, units, 0, 0);
   }
   return hipGetLastError();
 }
@@ -1767,10 +1765,9 @@ hipError_t launch_sessions_attention(const SessionsProblem& p, float* workspace,
       }
     }
     if (e != hipSuccess) return e;
-    const size_t merge_lds = ((size_t)a.nsplit_total + 8) * sizeof(float);
     const double bytes = (double)count * g.units * a.gq * ((double)a.nsplit_total * (g.D + 2) + g.D) * 4.0;
     TimedLaunch timed(KIVI_KERNEL_ATTN_MERGE, stream, bytes);
-    k_attn_merge<<<count * g.units * a.gq, kThreads, merge_lds, stream>>>(
+    k_attn_merge<<<count * g.units * a.gq, 128, 0, stream>>>(
         workspace, a.nsplit_total, a.gq, g.D, p.heads, p.qh, a.out, g.units, a.ws_sess_stride,
         a.q_sess_stride);
     e = hipGetLastError();
