@@ -17,6 +17,11 @@ bytes per launch of that kernel from rocprofv3 FETCH_SIZE + WRITE_SIZE runs, cal
 plain copy kernel (--copy-calibration), as recorded in profiles/traffic.json; null when no
 record matches this kernel, workload and byte count.
 
+Other workloads (a line each, same contract): --config c0 (the reference's CPU-runnable case),
+c1 (streaming decode: a step is RuntimeKv::decode = append one token + attention, after an
+8192-token prefill; warmup + 2*steps <= 512), c3_4 / c3_8 (4-/8-bit at 131072 tokens, GQA 8),
+c4 (64 RagSessions over one 65536-token prefix, one batched call per step).
+
 Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--config c2] [--no-cpu]
                        [--copy-calibration MIB]
 """
@@ -42,6 +47,9 @@ MFMA_F16_PEAK_TFLOPS = 2500.0  # dense f16 matrix-core peak
 CONFIGS = {
     # name: (batch, kv_heads, q_heads, head_dim, seq, bits, G, R, description)
     "c0": (1, 8, 8, 128, 4097, 2, 32, 128, "config 0: batch 1, 8q/8kv heads, seq 4097 (4096 prefill + 1), 2-bit"),
+    "c1": (1, 8, 32, 128, 8192, 2, 32, 128,
+           "config 1: streaming decode, batch 1, 32q/8kv heads, head_dim 128, 2-bit G=32 R=128, "
+           "8192-token prefill then RuntimeKv::decode steps (append 1 token + attention)"),
     "c2": (16, 8, 32, 128, 32768, 2, 32, 128,
            "config 2: batch 16, 32q/8kv heads, head_dim 128, 32768 cached tokens, 2-bit G=32 R=128"),
     "c3_4": (1, 8, 64, 128, 131072, 4, 32, 128, "config 3: batch 1, 64q/8kv heads, 131072 tokens, 4-bit"),
@@ -52,6 +60,8 @@ CONFIGS = {
 }
 # batched-sessions workloads: name -> (sessions, suffix tokens per session)
 SESSIONS = {"c4": (64, 96)}
+# streaming-decode workloads: name -> decode steps the workload allows after the prefill
+DECODE = {"c1": 512}
 
 
 def log(*a):
@@ -155,6 +165,43 @@ def cpu_baseline_sessions(kivi, cfg_tuple, n_sessions, suffix, target_s=12.0):
     }
 
 
+def cpu_baseline_decode(kivi, cfg_tuple, target_s=10.0):
+    """Oracle RuntimeKv (src/runtime.rs:12-57): the prefill, then decode steps (append one token
+    and attend) timed one by one on one thread."""
+    _, heads, qh, dim, seq, bits, G, R, _ = cfg_tuple
+    oracle = kivi.Backend.load(ROOT / "oracle" / "libkivi_oracle.so", "kivi_oracle_", device=False)
+    rng = np.random.default_rng(7)
+    k = rng.standard_normal((1, heads, seq, dim), dtype=np.float32)
+    for h, chans in enumerate(outlier_channels(heads, dim, 7)):
+        k[:, h, :, chans] *= 10.0
+    v = rng.standard_normal((1, heads, seq, dim), dtype=np.float32)
+    rt = kivi.RuntimeKv(oracle, kivi.KiviConfig(bits, G, R), 1, heads, dim)
+    rt.prefill(k, v, seq)
+    del k, v
+    scale = 1.0 / math.sqrt(dim)
+    reps, spent = 0, 0.0
+    while spent < target_s and reps < 200:
+        kk = rng.standard_normal(heads * dim, dtype=np.float32)
+        vv = rng.standard_normal(heads * dim, dtype=np.float32)
+        q = rng.standard_normal(qh * dim, dtype=np.float32)
+        t0 = time.perf_counter()
+        rt.decode(kk, vv, q, qh, scale)
+        spent += time.perf_counter() - t0
+        reps += 1
+    per_step = spent / reps
+    return {
+        "value": 1.0 / per_step,
+        "unit": "tokens/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"{reps} RuntimeKv::decode steps (append 1 token + attention, {heads} KV / {qh} q "
+                  f"heads) after a {seq}-token prefill, C++ restatement of the reference CPU path, "
+                  f"single thread",
+        "ms_per_step": per_step * 1e3,
+        "cpu": _cpu_model(),
+    }
+
+
 def _cpu_model():
     try:
         for line in open("/proc/cpuinfo"):
@@ -219,8 +266,15 @@ def main():
     warm.attention_device(wq.data_ptr(), wq.numel(), qh, 0.1, wo.data_ptr(), wo.numel(), sp)
     stream.synchronize()
     del warm, wk, wq, wo
-    cache = kivi.KiviCache(amd, kivi.KiviConfig(bits, G, R), batch, heads, dim)
-    cache.reserve(seq)
+    decode_steps = DECODE.get(args.config)
+    if decode_steps:
+        # RuntimeKv (src/runtime.rs:12-57): prefill through its cache, then decode steps
+        runtime = kivi.RuntimeKv(amd, kivi.KiviConfig(bits, G, R), batch, heads, dim)
+        cache = runtime.cache()
+        cache.reserve(seq + decode_steps)
+    else:
+        cache = kivi.KiviCache(amd, kivi.KiviConfig(bits, G, R), batch, heads, dim)
+        cache.reserve(seq)
     torch.cuda.synchronize()
     # Prefill quantization, timed once on the library's stream (whole append, and per
     # quantize kernel with the library's launch timing).
@@ -271,6 +325,30 @@ def main():
         def step():
             kivi.sessions_attention_device(amd, sessions, qp, n_q, qh, scale, op, n_q, sp,
                                            handles=handles)
+    elif decode_steps:
+        # one decode step = append one token (key residual, value window, flush every R) and
+        # attend; the plain and the evented timed regions each run `steps` of them
+        total = args.warmup + 2 * args.steps
+        if total > decode_steps:
+            sys.exit(f"c1 allows {decode_steps} decode steps after the prefill: warmup + 2 * steps = {total}")
+        gd = torch.Generator(device="cuda")
+        gd.manual_seed(2003)
+        kd = torch.randn((total, batch, heads, 1, dim), generator=gd, device="cuda")
+        for h, chans in enumerate(outlier_channels(heads, dim, 2001)):
+            kd[:, :, h, :, chans] *= 10.0
+        vd = torch.randn((total, batch, heads, 1, dim), generator=gd, device="cuda")
+        qd = torch.randn((total, batch, qh, dim), generator=gd, device="cuda")
+        n_kv, n_q = batch * heads * dim, batch * qh * dim
+        op = out.data_ptr()
+        counter = [0]
+        tokens_per_step = batch
+        kv_bytes = mem.compressed_bytes()
+
+        def step():
+            i = counter[0]
+            counter[0] += 1
+            runtime.decode_device(kd[i].data_ptr(), n_kv, vd[i].data_ptr(), n_kv, qd[i].data_ptr(),
+                                  n_q, qh, scale, op, n_q, sp)
     else:
         qp, op, n_q = q.data_ptr(), out.data_ptr(), q.numel()
         tokens_per_step = batch
@@ -390,8 +468,12 @@ def main():
     }
     if not args.no_cpu:
         log("[bench] CPU baseline (oracle, 1 thread) ...")
-        result["cpu_baseline"] = (cpu_baseline_sessions(kivi, CONFIGS[args.config], *sessions_cfg)
-                                  if sessions_cfg else cpu_baseline(kivi, CONFIGS[args.config]))
+        if sessions_cfg:
+            result["cpu_baseline"] = cpu_baseline_sessions(kivi, CONFIGS[args.config], *sessions_cfg)
+        elif decode_steps:
+            result["cpu_baseline"] = cpu_baseline_decode(kivi, CONFIGS[args.config])
+        else:
+            result["cpu_baseline"] = cpu_baseline(kivi, CONFIGS[args.config])
         log(f"[bench] CPU {result['cpu_baseline']['value']:.3f} tokens/s")
     print(json.dumps(result), flush=True)
 

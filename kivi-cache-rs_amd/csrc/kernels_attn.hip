@@ -320,6 +320,10 @@ __global__ void __launch_bounds__(kThreads) k_attn_generic(AttnArgs a) {
 // ------------------------------------------------------------------ MFMA splits
 
 constexpr int kFastCpw = 8;  // chunks (64 tokens) per wave in the MFMA kernel
+// Packed workgroups a launch aims for at least (one per CU): below it, waves take fewer than
+// kFastCpw chunks. More workgroups than that with fewer chunks each measured slower (4-bit,
+// 8 units x 131072 tokens: 1024 workgroups of 4 chunks per wave 62 us, 512 of 8 55 us).
+constexpr uint32_t kFastGroups = 256;
 constexpr int kRowPad = 4;  // floats of padding per logit row (LDS bank spread)
 constexpr int kRowStride1 = 64 + kRowPad;  // logits row stride of the one-chunk (MIXED) path
 
@@ -1460,10 +1464,11 @@ __global__ void __launch_bounds__(kShThreads) k_attn_shared(AttnArgs a) {
 // ------------------------------------------------------------------ planning
 
 constexpr size_t kMaxMergeLds = 48 * 1024;  // in-kernel merge up to ~12K splits per unit
-// The in-kernel merge is correct but measured slower at C2 (137 us kernel vs 122 + 8.5 us for
-// the two launches): every split then waits for its stores and a device-scope atomic before
-// it retires, and the last split of a unit merges on the critical path.
-constexpr bool kUseInKernelMerge = false;
+// In-kernel merge: 0 never, 1 always, 2 when the launch is a single round of workgroups. It
+// measured slower at C2 (137 us kernel vs 122 + 8.5 us for the two launches): every split
+// then waits for its stores and a device-scope atomic before it retires, and the last split
+// of a unit merges on the critical path.
+constexpr int kUseInKernelMerge = 0;
 
 uint32_t split_tokens(uint32_t gq) {
   uint32_t s = 256;
@@ -1505,7 +1510,14 @@ AttnArgs make_args(const AttnProblem& p, float* ws) {
   a.chunk_end = fast ? static_cast<uint32_t>(p.st.vq / 64) : 0;
   a.win_begin = a.chunk_end;
   a.win_end = fast ? static_cast<uint32_t>((a.total + 63) / 64) : 0;
-  a.nsplit_fast = (a.chunk_end + 4 * kFastCpw - 1) / (4 * kFastCpw);
+  // packed splits per unit: at most kFastCpw chunks per wave, at least one, and at least
+  // kFastGroups workgroups when the chunks allow
+  {
+    const uint32_t units = p.cache.geo.units;
+    const uint32_t fewest = (a.chunk_end + 4 * kFastCpw - 1) / (4 * kFastCpw);
+    const uint32_t most = (a.chunk_end + 3) / 4;
+    a.nsplit_fast = std::min(most, std::max(fewest, (kFastGroups + units - 1) / units));
+  }
   a.nsplit_win = a.win_end - a.win_begin;  // one chunk per workgroup, a quarter per wave
   a.t_begin = fast ? a.total : 0;
   a.nsplit_gen = static_cast<uint32_t>((a.total - a.t_begin + a.S - 1) / a.S);
@@ -1517,7 +1529,9 @@ AttnArgs make_args(const AttnProblem& p, float* ws) {
   a.q_sess_stride = a.ws_sess_stride = 0;
   // With kUseInKernelMerge the last split of each unit merges it in the same launch (partials
   // exchanged through agent-scope accesses, no L2 write-back or invalidation).
-  a.counters = kUseInKernelMerge && (size_t)4 * a.nsplit_total * sizeof(float) <= kMaxMergeLds ? p.counters : nullptr;
+  const bool in_kernel = kUseInKernelMerge == 1 ||
+                         (kUseInKernelMerge == 2 && (uint64_t)a.units * a.nsplit_total <= kFastGroups);
+  a.counters = in_kernel && (size_t)4 * a.nsplit_total * sizeof(float) <= kMaxMergeLds ? p.counters : nullptr;
   return a;
 }
 

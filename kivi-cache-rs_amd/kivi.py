@@ -685,6 +685,12 @@ class RuntimeKv:
                      q.size, num_q_heads, C.c_float(scale), _fptr(out), out.size)
         return out
 
+    def decode_device(self, k_ptr, k_len, v_ptr, v_len, q_ptr, q_len, num_q_heads, scale, out_ptr,
+                      out_len, stream=0):
+        self._b.call("runtime_decode_device", self._h, C.c_void_p(k_ptr), k_len, C.c_void_p(v_ptr),
+                     v_len, C.c_void_p(q_ptr), q_len, num_q_heads, C.c_float(scale),
+                     C.c_void_p(out_ptr), out_len, C.c_void_p(stream))
+
 
 PER_CHANNEL, PER_TOKEN = 0, 1
 
