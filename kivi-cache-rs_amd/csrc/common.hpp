@@ -133,6 +133,15 @@ hipError_t launch_quant_keys(const CacheView& c, RowSource src, uint64_t g0, uin
 hipError_t launch_quant_values(const CacheView& c, RowSource ring, uint32_t n_ring, RowSource in,
                                uint64_t n_in, uint64_t vq0, hipStream_t stream);
 
+// One decode token per unit in one launch (KiviCache::append with one token,
+// src/cache.rs:382-484, without a key flush): key row -> residual slot `kslot`; when `evict`,
+// the window row in slot `vslot` (stream token `vq`) is quantized into the packed values
+// first; the value row then goes to slot `vslot`. keys/values are [units][D]. Needs
+// D % 64 == 0, D <= 256 and G dividing 64 (returns hipErrorNotSupported otherwise).
+hipError_t launch_decode_append(const CacheView& c, const float* keys, const float* values,
+                                uint32_t kslot, uint32_t vslot, bool evict, uint64_t vq,
+                                hipStream_t stream);
+
 // Re-pack native streams into the reference PackedStream order, [units][...] concatenated.
 hipError_t launch_export_keys(const CacheView& c, uint64_t kq, uint32_t* codes, float* params,
                               hipStream_t stream);

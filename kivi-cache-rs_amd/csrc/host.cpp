@@ -380,6 +380,31 @@ struct CacheCore {
     const uint64_t vq_after = total > R ? total - R : 0;
     KIVI_TRY(ensure_capacity(std::max(kq_after, vq_after), s));
     const CacheView cv = view();
+    // one decode token: residual copy, window eviction and window write in one launch
+    if (n == 1 && vres_len <= R) {
+      const bool evict = vres_len == R;
+      const uint32_t vslot = evict ? vhead : static_cast<uint32_t>((vhead + vres_len) % R);
+      const hipError_t e = launch_decode_append(cv, keys, values, kres_len, vslot, evict, vq, s);
+      if (e == hipSuccess) {
+        kres_len += 1;
+        if (kres_len == R) {
+          HIP_TRY(launch_quant_keys(cv, RowSource{cv.kres, R * D, 0, 0}, kq / G,
+                                    static_cast<uint32_t>(R / G), s), "key flush");
+          kq += R;
+          kres_len = 0;
+        }
+        if (evict) {
+          vq += 1;
+          vhead = static_cast<uint32_t>((vhead + 1) % R);
+        } else {
+          vres_len += 1;
+        }
+        seq += 1;
+        return Status{};
+      }
+      if (e != hipErrorNotSupported) HIP_TRY(e, "decode append");
+      (void)hipGetLastError();  // unsupported shape: the general path below
+    }
     const RowSource kin{keys, n * D, 0, 0};
     // ---- keys: fill the residual, flush every R tokens, quantize whole R-blocks of the
     // input in place (the same groups the reference forms by copy-then-flush).

@@ -93,6 +93,50 @@ __global__ void __launch_bounds__(kThreads)
   }
 }
 
+// One decode token (see launch_decode_append): one workgroup per unit, thread d owns channel
+// d. The value group min/max (src/quant.rs:349-375) reduces over the G lanes of a channel
+// group by shuffles (G divides 64). Each channel's code word is read, OR-ed and written by
+// its own thread (the words of a 64-token block fill across appends; later tokens' bits are
+// still zero).
+__global__ void __launch_bounds__(256)
+    k_decode_append(CacheView c, const float* keys, const float* values, uint32_t kslot,
+                    uint32_t vslot, uint32_t evict, uint64_t vq) {
+  const Geometry& geo = c.geo;
+  const uint32_t unit = blockIdx.x, d = threadIdx.x, D = geo.D, R = geo.R;
+  c.kres[((uint64_t)unit * R + kslot) * D + d] = keys[(uint64_t)unit * D + d];
+  const float v = values[(uint64_t)unit * D + d];
+  float* slot = c.vring + ((uint64_t)unit * R + vslot) * D + d;
+  if (evict) {
+    const uint32_t G = geo.G, bits = geo.bits;
+    const float levels = static_cast<float>(geo.levels());
+    const float x = *slot;  // stream token vq, the oldest of the window
+    float mn = x, mx = x;
+    for (uint32_t o = 1; o < G; o <<= 1) {
+      mn = fminf(mn, __shfl_xor(mn, o));
+      mx = fmaxf(mx, __shfl_xor(mx, o));
+    }
+    const float scale = scale_of(mx - mn, levels);
+    const uint32_t code = quant_code(x, mn, scale, levels);
+    const uint64_t tb = vq / kValueBlock;
+    const uint32_t tt = static_cast<uint32_t>(vq % kValueBlock), ppw = geo.ppw(), vw = geo.vwords_per_channel();
+    float2* params = reinterpret_cast<float2*>(c.vparams + unit * geo.vparams_unit());
+    if (d % G == 0) params[(tb * geo.ncg() + d / G) * kValueBlock + tt] = make_float2(scale, mn);
+    uint32_t* w = c.vcodes + unit * geo.vcodes_unit() + tb * D * vw + (uint64_t)d * vw + tt / ppw;
+    *w = (tt % ppw == 0 ? 0u : *w) | (code << code_shift(bits, tt % ppw));
+    // per-wave maxima of the scale and |x| (every lane holds its group's), one atomic each
+    float sm = scale, am = fmaxf(fabsf(mn), fabsf(mx));
+    for (int o = 32; o > 0; o >>= 1) {
+      sm = fmaxf(sm, __shfl_xor(sm, o));
+      am = fmaxf(am, __shfl_xor(am, o));
+    }
+    if (d % 64 == 0) {
+      atomicMax(c.smax + 4 * unit + 1, __float_as_uint(sm));
+      atomicMax(c.smax + 4 * unit + 3, __float_as_uint(am));
+    }
+  }
+  *slot = v;
+}
+
 // Rows are staged through LDS as floats [rows][D+1] (the odd stride spreads a column over the
 // banks) by coalesced reads, float4 when `vec4`; at most kStageFloats floats per pass.
 constexpr uint32_t kStageFloats = 8704;  // 34 KiB
@@ -652,6 +696,15 @@ hipError_t launch_copy_rows(const Geometry& g, RowSource src, float* dst, uint32
     const uint64_t work = (uint64_t)g.units * count * g.D;
     k_copy_rows<1><<<grid_for(work), kThreads, 0, stream>>>(src, dst, g.R, g.D, g.units, dst_slot, count);
   }
+  return hipGetLastError();
+}
+
+hipError_t launch_decode_append(const CacheView& c, const float* keys, const float* values,
+                                uint32_t kslot, uint32_t vslot, bool evict, uint64_t vq,
+                                hipStream_t stream) {
+  const Geometry& g = c.geo;
+  if (g.D % 64 != 0 || g.D > 256 || 64 % g.G != 0) return hipErrorNotSupported;
+  k_decode_append<<<g.units, g.D, 0, stream>>>(c, keys, values, kslot, vslot, evict ? 1u : 0u, vq);
   return hipGetLastError();
 }
 
