@@ -142,6 +142,12 @@ hipError_t launch_decode_append(const CacheView& c, const float* keys, const flo
                                 uint32_t kslot, uint32_t vslot, bool evict, uint64_t vq,
                                 hipStream_t stream);
 
+// Raise each unit's |x| maxima (smax [2] keys, [3] values) over its fp32 rows: key residual
+// slots [0, kres), value window slots vhead .. vhead+vres-1 (mod R). A shared prefix does
+// this once, so its maxima bound every element its attention dequantizes.
+hipError_t launch_raise_row_max(const CacheView& c, uint32_t kres, uint32_t vres, uint32_t vhead,
+                                hipStream_t stream);
+
 // Re-pack native streams into the reference PackedStream order, [units][...] concatenated.
 hipError_t launch_export_keys(const CacheView& c, uint64_t kq, uint32_t* codes, float* params,
                               hipStream_t stream);

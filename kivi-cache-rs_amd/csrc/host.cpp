@@ -1192,6 +1192,10 @@ kivi_status kivi_cache_share_prefix(const kivi_cache* cache, kivi_prefix** out, 
     DeviceScope scope(cache->core.device);
     auto st = std::make_shared<kivi_prefix_state>();
     KIVI_TRY(cache->core.copy_into(st->core, cache->core.stream));
+    // the prefix's |x| maxima also bound its fp32 residual / window rows (batched attention
+    // dequantizes those into range-scaled f16 operands)
+    HIP_TRY(launch_raise_row_max(st->core.view(), st->core.kres_len, st->core.vres_len, st->core.vhead,
+                                 cache->core.stream), "prefix row maxima");
     KIVI_TRY(st->batch.init(st->core.units(), cache->core.stream));
     KIVI_TRY(sync(cache->core.stream, "share_prefix"));
     st->prefix_bytes = compressed_bytes(st->core.memory());

@@ -66,6 +66,11 @@ struct AttnArgs {
   // batched sessions (0 otherwise): session count and the strides between consecutive
   // sessions' queries, partials and outputs
   uint32_t nsess;
+  // window / suffix workgroups mask tokens below t_min (0, or the prefix length when the
+  // shared-prefix GEMM covers the prefix's own fp32 band); the GEMM covers prefix chunks
+  // [0, gemm_end)
+  uint64_t t_min;
+  uint32_t gemm_end;
   uint64_t q_sess_stride, ws_sess_stride;
   uint32_t* counters;      // [units] finished splits (0 between calls), or null: separate merge
   float* out;              // [batch][QH][D]
@@ -814,7 +819,7 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
         for (int i = 0; i < 4; ++i) lg[rs][i] = 0.f;
       if (packed) key_mfma<BITS, NRS>(cur, A, lg);
       if (MIXED && t0 + 64 > kq && t0 < total) key_fp32<NRS>(a, unit, t0, lane, qv, kUnit, lg);
-      const bool live = !MIXED || (t0 + lane < total && lane / 16 == quarter);
+      const bool live = !MIXED || (t0 + lane < total && t0 + lane >= a.t_min && lane / 16 == quarter);
 #pragma unroll
       for (int rs = 0; rs < NRS; ++rs)
 #pragma unroll
@@ -1284,9 +1289,19 @@ __device__ __forceinline__ void shared_logits(const _Float16* buf, const hx8 (&q
 }
 
 // Online softmax of one chunk's logits and the value mix for a wave's 32 rows.
-__device__ __forceinline__ void shared_mix(const _Float16* buf, const fx16& s0, const fx16& s1,
-                                           float s_unscale, float& m, float& l, fx16 (&o)[4]) {
+__device__ __forceinline__ void shared_mix(const _Float16* buf, fx16 s0, fx16 s1,
+                                           float s_unscale, float& m, float& l, fx16 (&o)[4],
+                                           uint32_t valid = 64) {
   const uint32_t lane = threadIdx.x % 64, h = lane / 32, r = lane % 32;
+  if (valid < 64) {
+    // S^T value v of tile T is token 32T + 8(v/4) + 4h + v%4 of the chunk
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const uint32_t t = 8 * (v / 4) + 4 * h + v % 4;
+      if (t >= valid) s0[v] = -INFINITY;
+      if (32 + t >= valid) s1[v] = -INFINITY;
+    }
+  }
   const _Float16* vhi = buf + 2 * 64 * kShKRow;
   const _Float16* vlo = vhi + 128 * kShVRow;
   // online softmax over the chunk (the lane pair r, r + 32 holds the row's 64 logits); the
@@ -1336,6 +1351,93 @@ __device__ __forceinline__ void shared_mix(const _Float16* buf, const fx16& s0, 
     for (int mt = 0; mt < 4; ++mt) o[mt] = mfma32(vh[mt], pll, o[mt]);
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) o[mt] = mfma32(vl[mt], phh, o[mt]);
+  }
+}
+
+// A prefix chunk that holds fp32 rows (the key residual / value window band), dequantized
+// directly into buffer `buf` (no pipelining; these are the last one or two chunks of a
+// prefix): tokens below kq / vq from the packed arrays, the rest from the residual / ring;
+// tokens from `seq` on are zero (and masked in the softmax).
+template <int BITS>
+__device__ void shared_dequant_mixed(const AttnArgs& a, uint32_t unit, uint32_t chunk, float kf, float vf,
+                                     _Float16* buf) {
+  constexpr uint32_t D = 128, PPW = 32 / BITS, KWT = D / PPW, VWC = 64 / PPW, MASK = (1u << BITS) - 1u;
+  const Geometry& g = a.c.geo;
+  const uint64_t kq = a.st.kq, vq = a.st.vq, seq = a.seq;
+  const uint32_t R = g.R;
+  _Float16* khi = buf;
+  _Float16* klo = khi + 64 * kShKRow;
+  _Float16* vhi = klo + 64 * kShKRow;
+  _Float16* vlo = vhi + 128 * kShVRow;
+  const uint32_t tid = threadIdx.x;
+  {
+    const uint32_t o = tid % 16, tp = tid / 16;
+#pragma unroll
+    for (int x = 0; x < 2; ++x) {
+      const uint64_t t = (uint64_t)chunk * 64 + 2 * tp + x;
+      float d[8];
+      if (t < kq) {
+        const float4* pk = reinterpret_cast<const float4*>(a.c.kparams + unit * g.kparams_unit() + (t / 32) * D * 2 + 16 * o);
+        const uint32_t* wp = a.c.kcodes + unit * g.kcodes_unit() + t * KWT;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t ch = 8 * o + e;
+          const uint32_t code = (wp[ch / PPW] >> code_shift(BITS, ch % PPW)) & MASK;
+          const float4 p = pk[e / 2];
+          d[e] = fmaf(static_cast<float>(code), e % 2 ? p.z : p.x, e % 2 ? p.w : p.y) * kf;
+        }
+      } else if (t < seq) {
+        const float4* r = reinterpret_cast<const float4*>(a.c.kres + ((uint64_t)unit * R + (t - kq)) * D + 8 * o);
+        const float4 r0 = r[0], r1 = r[1];
+        d[0] = r0.x * kf; d[1] = r0.y * kf; d[2] = r0.z * kf; d[3] = r0.w * kf;
+        d[4] = r1.x * kf; d[5] = r1.y * kf; d[6] = r1.z * kf; d[7] = r1.w * kf;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) d[e] = 0.f;
+      }
+      ux4 hi, lo;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint2 t2 = split2(d[2 * q], d[2 * q + 1]);
+        hi[q] = t2.x;
+        lo[q] = t2.y;
+      }
+      *reinterpret_cast<ux4*>(khi + (2 * tp + x) * kShKRow + 8 * o) = hi;
+      *reinterpret_cast<ux4*>(klo + (2 * tp + x) * kShKRow + 8 * o) = lo;
+    }
+  }
+  {
+    const uint32_t c = tid % 128, j = tid / 128;
+    const float2* vp = reinterpret_cast<const float2*>(a.c.vparams + unit * g.vparams_unit()) +
+                       ((uint64_t)chunk * g.ncg() + c / 32) * 64;
+    const uint32_t* wc = a.c.vcodes + unit * g.vcodes_unit() + (uint64_t)chunk * D * VWC + c * VWC;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      float d[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t k = 16 * j + 8 * (i / 4) + 4 * h + i % 4;  // token within the chunk
+        const uint64_t t = (uint64_t)chunk * 64 + k;
+        if (t < vq) {
+          const uint32_t code = (wc[k / PPW] >> code_shift(BITS, k % PPW)) & MASK;
+          const float2 p = vp[k];
+          d[i] = fmaf(static_cast<float>(code), p.x, p.y) * vf;
+        } else if (t < seq) {
+          d[i] = a.c.vring[((uint64_t)unit * R + (a.st.vhead + (t - vq)) % R) * D + c] * vf;
+        } else {
+          d[i] = 0.f;
+        }
+      }
+      ux4 hi, lo;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint2 t2 = split2(d[2 * q], d[2 * q + 1]);
+        hi[q] = t2.x;
+        lo[q] = t2.y;
+      }
+      *reinterpret_cast<ux4*>(vhi + c * kShVRow + 16 * j + 8 * h) = hi;
+      *reinterpret_cast<ux4*>(vlo + c * kShVRow + 16 * j + 8 * h) = lo;
+    }
   }
 }
 
@@ -1392,9 +1494,11 @@ __device__ __forceinline__ void shared_split(const AttnArgs& a, uint32_t unit, u
   const float s_unscale = ldexpf(1.f, -ek - eq);
   const float o_unscale = ldexpf(1.f, -ev) / kShPScale;  // O and l carry the 2^14 of P
 
-  const uint32_t cps = (a.chunk_end + a.nsplit_fast - 1) / a.nsplit_fast;
-  const uint32_t c0 = std::min(a.chunk_end, split * cps);
-  const uint32_t c1 = std::min(a.chunk_end, c0 + cps);
+  // contiguous chunk ranges over [0, gemm_end); chunks from chunk_end on hold fp32 rows
+  const uint32_t cps = (a.gemm_end + a.nsplit_fast - 1) / a.nsplit_fast;
+  const uint32_t c0 = std::min(a.gemm_end, split * cps);
+  const uint32_t c1 = std::min(a.gemm_end, c0 + cps);
+  const uint32_t p1 = std::min(c1, a.chunk_end);  // packed part [c0, p1)
   float m = -INFINITY, l = 0.f;
   fx16 o[4];
 #pragma unroll
@@ -1402,8 +1506,8 @@ __device__ __forceinline__ void shared_split(const AttnArgs& a, uint32_t unit, u
 #pragma unroll
     for (int v = 0; v < 16; ++v) o[mt][v] = 0.f;
 
-  if (c0 < c1) {
-    // Chunks past the split's end are clamped to its last chunk: their loads stay in bounds and
+  if (c0 < p1) {
+    // Chunks past the packed range's end are clamped to its last chunk: their loads stay in bounds and
     // their dequant goes to the buffer no later iteration reads.
     const ShSrc<BITS> src = shared_src<BITS>(a, unit);
     ShRaw<BITS> cur, nxt;
@@ -1411,14 +1515,14 @@ __device__ __forceinline__ void shared_split(const AttnArgs& a, uint32_t unit, u
     shared_store_params<BITS>(cur, kf, vf, prms + (c0 % 2) * kShParamFloats);
     __syncthreads();
     shared_dequant<BITS>(cur, prms + (c0 % 2) * kShParamFloats, bufs + (c0 % 2) * kShBufHalves);
-    shared_load<BITS>(src, std::min(c0 + 1, c1 - 1), cur);
+    shared_load<BITS>(src, std::min(c0 + 1, p1 - 1), cur);
     shared_store_params<BITS>(cur, kf, vf, prms + ((c0 + 1) % 2) * kShParamFloats);
     __syncthreads();
     // Top of iteration c: buffer c%2 holds chunk c; params (c+1)%2 and `cur` hold chunk c+1.
     // The dequant of chunk c+1 comes first, so `cur` is dead before the logit registers are
     // live (no spills at 256 VGPRs).
-    for (uint32_t c = c0; c < c1; ++c) {
-      shared_load<BITS>(src, std::min(c + 2, c1 - 1), nxt);
+    for (uint32_t c = c0; c < p1; ++c) {
+      shared_load<BITS>(src, std::min(c + 2, p1 - 1), nxt);
       const _Float16* buf = bufs + (c % 2) * kShBufHalves;
       shared_dequant<BITS>(cur, prms + ((c + 1) % 2) * kShParamFloats, bufs + ((c + 1) % 2) * kShBufHalves);
       fx16 s0, s1;
@@ -1428,6 +1532,16 @@ __device__ __forceinline__ void shared_split(const AttnArgs& a, uint32_t unit, u
       cur = nxt;
       __syncthreads();
     }
+  }
+  // the prefix's fp32 band (the split covering the last chunks): direct dequant, masked tail
+  for (uint32_t c = std::max(c0, a.chunk_end); c < c1; ++c) {
+    shared_dequant_mixed<BITS>(a, unit, c, kf, vf, bufs);
+    __syncthreads();
+    fx16 s0, s1;
+    shared_logits(bufs, qhi, qlo, s0, s1);
+    const uint64_t left = a.seq - (uint64_t)c * 64;
+    shared_mix(bufs, s0, s1, s_unscale, m, l, o, left < 64 ? static_cast<uint32_t>(left) : 64u);
+    __syncthreads();  // the buffer is rewritten by the next chunk
   }
   l += __shfl_xor(l, 32);
   if (!live) return;
@@ -1526,6 +1640,8 @@ AttnArgs make_args(const AttnProblem& p, float* ws) {
   a.out = p.out;
   a.units = p.cache.geo.units;
   a.nsess = 0;
+  a.t_min = 0;
+  a.gemm_end = 0;
   a.q_sess_stride = a.ws_sess_stride = 0;
   // With kUseInKernelMerge the last split of each unit merges it in the same launch (partials
   // exchanged through agent-scope accesses, no L2 write-back or invalidation).
@@ -1664,13 +1780,21 @@ bool use_shared(const SessionsProblem& sp, uint32_t nsess) {
 // The GEMM form's splits: the packed chunks of a unit in nsplit contiguous ranges, nsplit a
 // multiple of 8 (the XCD count) where the chunks allow, so about kSharedTargetGroups
 // workgroups cover units x row blocks x splits.
+// The GEMM form covers every prefix chunk, [0, ceil(seq/64)) (the fp32 band of the prefix
+// too, as the prefix's smax covers those rows); the per-session window workgroups cover the
+// suffix only: chunks from floor(seq/64), tokens below seq masked.
 AttnArgs make_shared_args(const SessionsProblem& sp, uint32_t nsess, uint64_t max_suffix, float* ws) {
   AttnArgs a = make_session_args(sp, nsess, max_suffix, ws);
   const uint32_t rblocks = (nsess * a.gq + kShRows - 1) / kShRows;
   const uint32_t per = a.units * rblocks;
   uint32_t ns = (kSharedTargetGroups + per - 1) / per;
   ns = (ns + 7) / 8 * 8;
-  a.nsplit_fast = a.chunk_end == 0 ? 0 : std::max(1u, std::min(ns, a.chunk_end));
+  a.gemm_end = static_cast<uint32_t>((sp.seq + 63) / 64);
+  a.nsplit_fast = a.gemm_end == 0 ? 0 : std::max(1u, std::min(ns, a.gemm_end));
+  a.t_min = sp.seq;
+  a.win_begin = static_cast<uint32_t>(sp.seq / 64);
+  a.win_end = static_cast<uint32_t>((sp.seq + max_suffix + 63) / 64);
+  a.nsplit_win = max_suffix > 0 ? a.win_end - a.win_begin : 0;
   a.nsplit_total = a.nsplit_fast + a.nsplit_win + a.nsplit_gen;
   a.ws_sess_stride = (uint64_t)sp.cache.geo.units * a.nsplit_total * a.gq * (sp.cache.geo.D + 2);
   return a;

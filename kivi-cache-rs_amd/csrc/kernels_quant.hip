@@ -137,6 +137,23 @@ __global__ void __launch_bounds__(256)
   *slot = v;
 }
 
+// Workgroup (unit, kind): kind 0 scans the key residual rows, kind 1 the value window rows.
+__global__ void __launch_bounds__(kThreads)
+    k_raise_row_max(CacheView c, uint32_t kres, uint32_t vres, uint32_t vhead) {
+  const Geometry& geo = c.geo;
+  const uint32_t unit = blockIdx.x / 2, kind = blockIdx.x % 2, D = geo.D, R = geo.R;
+  const uint32_t rows = kind == 0 ? kres : vres;
+  const float* base = (kind == 0 ? c.kres : c.vring) + (uint64_t)unit * R * D;
+  float m = 0.f;
+  for (uint32_t i = threadIdx.x; i < rows * D; i += blockDim.x) {
+    const uint32_t r = i / D, d = i % D;
+    const uint32_t slot = kind == 0 ? r : (vhead + r) % R;
+    m = fmaxf(m, fabsf(base[(uint64_t)slot * D + d]));
+  }
+  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+  if (threadIdx.x % 64 == 0) atomicMax(c.smax + 4 * unit + 2 + kind, __float_as_uint(m));
+}
+
 // Rows are staged through LDS as floats [rows][D+1] (the odd stride spreads a column over the
 // banks) by coalesced reads, float4 when `vec4`; at most kStageFloats floats per pass.
 constexpr uint32_t kStageFloats = 8704;  // 34 KiB
@@ -705,6 +722,13 @@ hipError_t launch_decode_append(const CacheView& c, const float* keys, const flo
   const Geometry& g = c.geo;
   if (g.D % 64 != 0 || g.D > 256 || 64 % g.G != 0) return hipErrorNotSupported;
   k_decode_append<<<g.units, g.D, 0, stream>>>(c, keys, values, kslot, vslot, evict ? 1u : 0u, vq);
+  return hipGetLastError();
+}
+
+hipError_t launch_raise_row_max(const CacheView& c, uint32_t kres, uint32_t vres, uint32_t vhead,
+                                hipStream_t stream) {
+  if (kres == 0 && vres == 0) return hipSuccess;
+  k_raise_row_max<<<c.geo.units * 2, kThreads, 0, stream>>>(c, kres, vres, vhead);
   return hipGetLastError();
 }
 
