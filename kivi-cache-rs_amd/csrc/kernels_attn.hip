@@ -955,8 +955,13 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
 // Chunk launch: workgroups [0, units*nsplit_win) take one window / suffix chunk each (MIXED
 // path, started first), the rest a split of 4*kFastCpw packed chunks; with counters, the
 // last split of each unit merges it.
+//
+// Resident workgroups per CU asked of the register allocator per instantiation (4-wave
+// workgroups, so also waves per SIMD): it then packs the 4-bit GQA-4 kernel into 128 VGPRs
+// (4 waves) and the GQA-8 ones into 168 (3 waves) without spills.
 template <int BITS, int NRS>
-__global__ void __launch_bounds__(kThreads) k_attn_mfma(AttnArgs a) {
+__global__ void __launch_bounds__(kThreads, (NRS == 1 && BITS <= 4) ? 4 : (BITS == 8 && NRS == 2) ? 2 : 3)
+    k_attn_mfma(AttnArgs a) {
   extern __shared__ float lds[];
   const uint32_t nwin = a.units * a.nsplit_win;
   uint32_t unit;
