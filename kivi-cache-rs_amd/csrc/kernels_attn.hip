@@ -416,15 +416,16 @@ __device__ __forceinline__ h4 codes4(uint32_t w, int k) {
   }
 }
 
-// x = hi + lo with hi = f16(x) and lo = f16(x - hi): 22 significant bits in two f16 operands
-// (x must be below 2^15 in magnitude; the callers scale their operands by a power of two).
+// x = hi + lo with hi = f16(x) rounded toward zero and lo = f16(x - hi) (x - hi is exact in
+// f32): 22 significant bits in two f16 operands, two values per packed conversion (x must be
+// below 2^15 in magnitude; the callers scale their operands by a power of two).
 __device__ __forceinline__ void split4(const float* x, h4& hi, h4& lo) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const _Float16 h = (_Float16)x[i];
-    hi[i] = h;
-    lo[i] = (_Float16)(x[i] - (float)h);
-  }
+  const h2 h01 = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(x[0], x[1]));
+  const h2 h23 = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(x[2], x[3]));
+  const h2 l01 = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(x[0] - (float)h01.x, x[1] - (float)h01.y));
+  const h2 l23 = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(x[2] - (float)h23.x, x[3] - (float)h23.y));
+  hi = h4{h01.x, h01.y, h23.x, h23.y};
+  lo = h4{l01.x, l01.y, l23.x, l23.y};
 }
 
 template <int N>
