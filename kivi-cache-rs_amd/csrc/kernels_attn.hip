@@ -566,22 +566,21 @@ struct ValueA {
   h4 hi[NRS][2][2], lo[NRS][2][2];  // [rs][hv][tokens 8*la + 4j ..]
 };
 
+// The weights w arrive times 2^e already (the exponent offset of the softmax), so zacc and
+// the caller's weight sum are in those units too.
 template <int NRS>
 __device__ __forceinline__ void value_operands(const ValueParams& vp, const float (&w)[NRS][8],
-                                               float vfac, ValueA<NRS>& A, float (&zacc)[NRS][2]) {
+                                               ValueA<NRS>& A, float (&zacc)[NRS][2]) {
 #pragma unroll
   for (int rs = 0; rs < NRS; ++rs) {
-    float wv[8];
-#pragma unroll
-    for (int r = 0; r < 8; ++r) wv[r] = w[rs][r] * vfac;
 #pragma unroll
     for (int hv = 0; hv < 2; ++hv) {
       float p[8];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const float4 sz = vp.sz[hv][j];  // tokens 8*la + 2j, +1
-        p[2 * j] = wv[2 * j] * sz.x;
-        p[2 * j + 1] = wv[2 * j + 1] * sz.z;
+        p[2 * j] = w[rs][2 * j] * sz.x;
+        p[2 * j + 1] = w[rs][2 * j + 1] * sz.z;
         zacc[rs][hv] = fmaf(w[rs][2 * j], sz.y, zacc[rs][hv]);
         zacc[rs][hv] = fmaf(w[rs][2 * j + 1], sz.w, zacc[rs][hv]);
       }
@@ -854,6 +853,11 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
   float moff[NRS];
 #pragma unroll
   for (int rs = 0; rs < NRS; ++rs) moff[rs] = mrow[rs] == -INFINITY ? 0.f : mrow[rs];
+  // the packed value pass takes its weights times 2^ev straight from the exponential
+  float evoff[NRS];
+#pragma unroll
+  for (int rs = 0; rs < NRS; ++rs) evoff[rs] = static_cast<float>(ev) - moff[rs];
+  const float vinv = ldexpf(1.f, -ev);
 
   // ---------------- phase 2: value mix
   v4f vacc[NRS][2];
@@ -881,11 +885,11 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
         const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
         for (int r = 0; r < 8; ++r) {
-          w[rs][r] = __builtin_amdgcn_exp2f(fmaf(xs[r], kout, -moff[rs]));  // argument <= 0
+          w[rs][r] = __builtin_amdgcn_exp2f(fmaf(xs[r], kout, evoff[rs]));  // 2^ev * weight
           lsum[rs] += w[rs][r];
         }
       }
-      if (packed) value_operands<NRS>(vp, w, vfac, A, zacc);
+      if (packed) value_operands<NRS>(vp, w, A, zacc);
       if constexpr (CPW > 1) {
         const int32_t kn = std::min(chunk_of(std::min(k + 1, nch - 1)), lastv);
         load_value_params(a, unit, kn, la, lc, vp);
@@ -922,13 +926,13 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         // zero term of head i, channel group lc + 2*hv lives in lane 32*lc + i
-        const float z = __shfl(zacc[rs][hv], 32 * lc + i);
+        const float z = __shfl(zacc[rs][hv], 32 * lc + i) * vinv;
         cw[(rs * 4 + i) * (D + 2) + lane + 64 * hv] = fmaf(vacc[rs][hv][i], vout, z);
       }
     }
     if (lane < 4) {  // lanes 0..3 hold row li = lane after the reductions
       cw[(rs * 4 + lane) * (D + 2) + D] = nch > 0 ? mrow[rs] : -INFINITY;
-      cw[(rs * 4 + lane) * (D + 2) + D + 1] = nch > 0 ? lsum[rs] : 0.f;
+      cw[(rs * 4 + lane) * (D + 2) + D + 1] = nch > 0 ? lsum[rs] * vinv : 0.f;
     }
   }
   __syncthreads();
