@@ -442,23 +442,35 @@ __device__ __forceinline__ void load_words(const uint32_t* p, uint32_t* w) {
 }
 
 // One chunk's key data for the lane's token: its code words, and the (scale, zero) pairs of
-// its group (half lc) for channels 16*la .. +15.
+// its group (half lc) for channels 16*la + 4*li .. +3 (the quad's four lanes hold the block's
+// 16 channels between them; quad_bcast shares them).
 template <int BITS>
 struct KeyWords {
   uint32_t w[128 * BITS / 32];
 };
 struct KeyParams {
-  float4 sz[8];
+  float4 sz[2];
 };
 // One chunk's value data: the code words of channels lane and 64+lane, and (scale, zero) of
-// tokens 8*la .. +7 for channel groups lc and lc+2.
+// tokens 8*la + 2*li, +1 for channel groups lc and lc+2 (the quad holds tokens 8*la .. +7).
 template <int BITS>
 struct ValueWords {
   uint32_t w[2][64 * BITS / 32];
 };
 struct ValueParams {
-  float4 sz[2][4];
+  float4 sz[2];
 };
+
+// v as held by lane q of each quad (DPP quad_perm broadcast; every lane is active here).
+__device__ __forceinline__ float quad_bcast(float v, int q) {
+  const int x = __float_as_int(v);
+  switch (q) {
+    case 0: return __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0x00, 0xF, 0xF, true));
+    case 1: return __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0x55, 0xF, 0xF, true));
+    case 2: return __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0xAA, 0xF, 0xF, true));
+    default: return __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0xFF, 0xF, 0xF, true));
+  }
+}
 
 template <int BITS>
 __device__ __forceinline__ void load_key_words(const AttnArgs& a, uint32_t unit, uint32_t ch,
@@ -467,11 +479,11 @@ __device__ __forceinline__ void load_key_words(const AttnArgs& a, uint32_t unit,
   load_words<KW>(a.c.kcodes + unit * a.c.geo.kcodes_unit() + ((uint64_t)ch * 64 + lane) * KW, kw.w);
 }
 __device__ __forceinline__ void load_key_params(const AttnArgs& a, uint32_t unit, uint32_t ch,
-                                                uint32_t la, uint32_t lc, KeyParams& kp) {
+                                                uint32_t la, uint32_t lc, uint32_t li, KeyParams& kp) {
   const float4* pp = reinterpret_cast<const float4*>(
-      a.c.kparams + unit * a.c.geo.kparams_unit() + ((uint64_t)(2 * ch + lc) * 128 + 16 * la) * 2);
-#pragma unroll
-  for (int j = 0; j < 8; ++j) kp.sz[j] = pp[j];
+      a.c.kparams + unit * a.c.geo.kparams_unit() + ((uint64_t)(2 * ch + lc) * 128 + 16 * la + 4 * li) * 2);
+  kp.sz[0] = pp[0];
+  kp.sz[1] = pp[1];
 }
 template <int BITS>
 __device__ __forceinline__ void load_value_words(const AttnArgs& a, uint32_t unit, uint32_t tb,
@@ -483,14 +495,11 @@ __device__ __forceinline__ void load_value_words(const AttnArgs& a, uint32_t uni
                    vw.w[hv]);
 }
 __device__ __forceinline__ void load_value_params(const AttnArgs& a, uint32_t unit, uint32_t tb,
-                                                  uint32_t la, uint32_t lc, ValueParams& vp) {
+                                                  uint32_t la, uint32_t lc, uint32_t li, ValueParams& vp) {
 #pragma unroll
-  for (int hv = 0; hv < 2; ++hv) {
-    const float4* pp = reinterpret_cast<const float4*>(
-        a.c.vparams + unit * a.c.geo.vparams_unit() + (((uint64_t)tb * 4 + lc + 2 * hv) * 64 + 8 * la) * 2);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) vp.sz[hv][j] = pp[j];
-  }
+  for (int hv = 0; hv < 2; ++hv)
+    vp.sz[hv] = *reinterpret_cast<const float4*>(
+        a.c.vparams + unit * a.c.geo.vparams_unit() + (((uint64_t)tb * 4 + lc + 2 * hv) * 64 + 8 * la + 2 * li) * 2);
 }
 
 // Key-side A operands of one chunk: q * scale (already times 2^e) per (head, channel) of the
@@ -511,12 +520,12 @@ __device__ __forceinline__ void key_operands(const KeyParams& kp, const float (&
     float p[16];
     float bias = 0.f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float4 sz = kp.sz[j];  // (s, z) of channels 2j, 2j+1
-      p[2 * j] = qv[rs][2 * j] * sz.x;
-      p[2 * j + 1] = qv[rs][2 * j + 1] * sz.z;
-      bias = fmaf(qv[rs][2 * j], sz.y, bias);
-      bias = fmaf(qv[rs][2 * j + 1], sz.w, bias);
+    for (int c = 0; c < 16; ++c) {
+      const float4 sz = kp.sz[(c % 4) / 2];  // channel c lives in quad lane c / 4
+      const float sc = quad_bcast(c % 2 ? sz.z : sz.x, c / 4);
+      const float zc = quad_bcast(c % 2 ? sz.w : sz.y, c / 4);
+      p[c] = qv[rs][c] * sc;
+      bias = fmaf(qv[rs][c], zc, bias);
     }
 #pragma unroll
     for (int k = 0; k < 4; ++k) split4(p + 4 * k, A.hi[rs][k], A.lo[rs][k]);
@@ -577,12 +586,12 @@ __device__ __forceinline__ void value_operands(const ValueParams& vp, const floa
     for (int hv = 0; hv < 2; ++hv) {
       float p[8];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float4 sz = vp.sz[hv][j];  // tokens 8*la + 2j, +1
-        p[2 * j] = w[rs][2 * j] * sz.x;
-        p[2 * j + 1] = w[rs][2 * j + 1] * sz.z;
-        zacc[rs][hv] = fmaf(w[rs][2 * j], sz.y, zacc[rs][hv]);
-        zacc[rs][hv] = fmaf(w[rs][2 * j + 1], sz.w, zacc[rs][hv]);
+      for (int r = 0; r < 8; ++r) {
+        const float4 sz = vp.sz[hv];  // token 8*la + r lives in quad lane r / 2
+        const float sc = quad_bcast(r % 2 ? sz.z : sz.x, r / 2);
+        const float zc = quad_bcast(r % 2 ? sz.w : sz.y, r / 2);
+        p[r] = w[rs][r] * sc;
+        zacc[rs][hv] = fmaf(w[rs][r], zc, zacc[rs][hv]);
       }
       split4(p, A.hi[rs][hv][0], A.lo[rs][hv][0]);
       split4(p + 4, A.hi[rs][hv][1], A.lo[rs][hv][1]);
@@ -809,7 +818,7 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
       // unconditional (clamped to packed chunks; the last step re-reads an L2-resident chunk)
       if constexpr (CPW > 1) {
         const int32_t kn = std::min(chunk_of(std::min(k + 1, nch - 1)), lastk);
-        load_key_params(a, unit, kn, la, lc, kp);
+        load_key_params(a, unit, kn, la, lc, li, kp);
         load_key_words<BITS>(a, unit, kn, lane, next);
       }
       float lg[NRS][4];
@@ -831,7 +840,7 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
     };
     if (nch > 0) {
       const int32_t k0 = std::min(chunk_of(0), lastk);
-      load_key_params(a, unit, k0, la, lc, kp);
+      load_key_params(a, unit, k0, la, lc, li, kp);
       load_key_words<BITS>(a, unit, k0, lane, kw0);
     }
     for (int k = 0; k < nch; k += 2) {
@@ -892,7 +901,7 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
       if (packed) value_operands<NRS>(vp, w, A, zacc);
       if constexpr (CPW > 1) {
         const int32_t kn = std::min(chunk_of(std::min(k + 1, nch - 1)), lastv);
-        load_value_params(a, unit, kn, la, lc, vp);
+        load_value_params(a, unit, kn, la, lc, li, vp);
         load_value_words<BITS>(a, unit, kn, lane, next);
       }
       if (packed) value_mfma<BITS, NRS>(cur, A, vacc);
@@ -901,7 +910,7 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
     };
     if (nch > 0) {
       const int32_t k0 = std::min(chunk_of(0), lastv);
-      load_value_params(a, unit, k0, la, lc, vp);
+      load_value_params(a, unit, k0, la, lc, li, vp);
       load_value_words<BITS>(a, unit, k0, lane, vw0);
     }
     for (int k = 0; k < nch; k += 2) {
@@ -1029,17 +1038,25 @@ __global__ void __launch_bounds__(kThreads) k_attn_sessions(AttnArgs a, SessionT
   }
 }
 
-// Log-sum-exp merge of the split partials: one workgroup of D threads per (session, unit,
-// head). Every wave reduces the splits' (m, l) pairs itself (no barrier), then thread d sums
-// channel d over the splits with the factors 2^(m_s - M); no LDS, so any split count fits.
-__global__ void __launch_bounds__(256)
+// Log-sum-exp merge of the split partials: one workgroup per (session, unit, head) of
+// `parts` groups of dt = ceil(D/64)*64 threads. Every wave reduces the splits' (m, l) pairs
+// itself (no barrier); thread (part, d) then sums channel d over splits part, part + parts,
+// ... with the factors 2^(m_s - M), kMergeBatch splits per round of independent loads, and
+// the parts meet in LDS. A merge is a few rounds of load latency whatever the split count.
+constexpr uint32_t kMergeBatch = 16;
+constexpr uint32_t kMergeThreads = 1024;
+
+__global__ void __launch_bounds__(kMergeThreads)
     k_attn_merge(const float* ws, uint32_t nsplit, uint32_t gq, uint32_t D, uint32_t heads,
                  uint32_t qh, float* out, uint32_t units, uint64_t ws_sess_stride,
                  uint64_t out_sess_stride) {
+  __shared__ float red[kMergeThreads];
   const uint32_t lane = threadIdx.x % 64;
   const uint32_t sess = blockIdx.x / (units * gq);
   const uint32_t unit = (blockIdx.x / gq) % units, h = blockIdx.x % gq;
   const uint32_t b = unit / heads, kvh = unit % heads;
+  const uint32_t dt = std::min(kMergeThreads, (D + 63) / 64 * 64);
+  const uint32_t parts = blockDim.x / dt, part = threadIdx.x / dt, dl = threadIdx.x % dt;
   const uint64_t stride = (uint64_t)gq * (D + 2);
   const float* base = ws + sess * ws_sess_stride + (uint64_t)unit * nsplit * stride + h * (D + 2);
   float m = -INFINITY, l = 0.f;
@@ -1057,16 +1074,46 @@ __global__ void __launch_bounds__(256)
   l = m == -INFINITY ? 0.f : l * __builtin_amdgcn_exp2f(m - M);
   const float inv = 1.0f / warp_sum(l);
   float* o = out + sess * out_sess_stride + ((uint64_t)b * qh + kvh * gq + h) * D;
-  for (uint32_t d = threadIdx.x; d < D; d += blockDim.x) {
+  for (uint32_t d0 = 0; d0 < D; d0 += dt) {
+    const uint32_t d = d0 + dl;
     float acc = 0.f;
-#pragma unroll 4
-    for (uint32_t s = 0; s < nsplit; ++s) {
-      const float ms = base[s * stride + D];
-      const float f = ms == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms - M);
-      acc = fmaf(base[s * stride + d], f, acc);
+    if (d < D) {
+      for (uint32_t s0 = part; s0 < nsplit; s0 += parts * kMergeBatch) {
+        float v[kMergeBatch], f[kMergeBatch];
+#pragma unroll
+        for (uint32_t j = 0; j < kMergeBatch; ++j) {
+          const uint32_t s = s0 + j * parts;
+          const float* ps = base + (uint64_t)(s < nsplit ? s : 0u) * stride;
+          const float x = ps[d], ms = ps[D];
+          f[j] = s < nsplit && ms != -INFINITY ? __builtin_amdgcn_exp2f(ms - M) : 0.f;
+          v[j] = s < nsplit ? x : 0.f;
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < kMergeBatch; ++j) acc = fmaf(v[j], f[j], acc);
+      }
     }
-    o[d] = acc * inv;
+    if (parts > 1) {
+      red[threadIdx.x] = acc;
+      __syncthreads();
+      if (part == 0) {
+        for (uint32_t q = 1; q < parts; ++q) acc += red[q * dt + dl];
+      }
+      __syncthreads();
+    }
+    if (part == 0 && d < D) o[d] = acc * inv;
   }
+}
+
+// Merge launch for `count` sessions of `units` units: split parts sized so each thread sums
+// about kMergeBatch splits.
+hipError_t launch_merge(const float* ws, uint32_t nsplit, uint32_t gq, uint32_t D, uint32_t heads,
+                        uint32_t qh, float* out, uint32_t units, uint32_t count,
+                        uint64_t ws_sess_stride, uint64_t out_sess_stride, hipStream_t stream) {
+  const uint32_t dt = std::min(kMergeThreads, (D + 63) / 64 * 64);
+  const uint32_t parts = std::max(1u, std::min(kMergeThreads / dt, (nsplit + kMergeBatch - 1) / kMergeBatch));
+  k_attn_merge<<<count * units * gq, parts * dt, 0, stream>>>(ws, nsplit, gq, D, heads, qh, out, units,
+                                                              ws_sess_stride, out_sess_stride);
+  return hipGetLastError();
 }
 
 // ------------------------------------------------------------------ shared-prefix GEMM splits
@@ -1730,8 +1777,8 @@ hipError_t launch_attention(const AttnProblem& p, float* workspace, hipStream_t 
   if (a.counters == nullptr) {
     const double bytes = (double)units * a.gq * ((double)a.nsplit_total * (g.D + 2) + g.D) * 4.0;
     TimedLaunch timed(KIVI_KERNEL_ATTN_MERGE, stream, bytes);
-    k_attn_merge<<<units * a.gq, std::min(256u, (g.D + 63) / 64 * 64), 0, stream>>>(
-        workspace, a.nsplit_total, a.gq, g.D, p.heads, p.qh, p.out, units, 0, 0);
+    return launch_merge(workspace, a.nsplit_total, a.gq, g.D, p.heads, p.qh, p.out, units, 1, 0, 0,
+                        stream);
   }
   return hipGetLastError();
 }
@@ -1915,10 +1962,8 @@ hipError_t launch_sessions_attention(const SessionsProblem& p, float* workspace,
     if (e != hipSuccess) return e;
     const double bytes = (double)count * g.units * a.gq * ((double)a.nsplit_total * (g.D + 2) + g.D) * 4.0;
     TimedLaunch timed(KIVI_KERNEL_ATTN_MERGE, stream, bytes);
-    k_attn_merge<<<count * g.units * a.gq, 128, 0, stream>>>(
-        workspace, a.nsplit_total, a.gq, g.D, p.heads, p.qh, a.out, g.units, a.ws_sess_stride,
-        a.q_sess_stride);
-    e = hipGetLastError();
+    e = launch_merge(workspace, a.nsplit_total, a.gq, g.D, p.heads, p.qh, a.out, g.units, count,
+                     a.ws_sess_stride, a.q_sess_stride, stream);
     if (e != hipSuccess) return e;
   }
   return hipSuccess;
