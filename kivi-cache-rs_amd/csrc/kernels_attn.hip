@@ -643,45 +643,66 @@ __device__ __forceinline__ const float* value_row(const AttnArgs& a, uint32_t un
   return a.c.vring + ((uint64_t)unit * R + slot) * D;
 }
 
-// Logit contribution of the chunk's fp32 keys (tokens kq <= t < total) for the lane's token,
-// added to lg in the packed pass's units: f32 MFMAs (v_mfma_f32_4x4x1_16B), A = q * 2^e
-// broadcast from block a2 (channels 16*a2 + r), B = the token's key row times
-// unit_scale = 2^kExp (0 for other tokens), accumulated onto lg.
+// fp32 key rows of a MIXED wave's quarter: lane l holds token 16*quarter + l%16, channels
+// 32*(l/16) .. +31 (every token of the quarter is read once, four lanes per row).
+struct KeyRows {
+  float4 x[8];
+};
+__device__ __forceinline__ void load_key_rows(const AttnArgs& a, uint32_t unit, uint64_t t0,
+                                              uint32_t quarter, uint32_t lane, KeyRows& kr) {
+  const float4* row = reinterpret_cast<const float4*>(key_row(a, unit, t0 + 16 * quarter + lane % 16)) +
+                      8 * (lane / 16);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) kr.x[j] = row[j];
+}
+
+// Logit contribution of the quarter's fp32 keys (tokens kq <= t < total), added to lg in the
+// packed pass's units, for the lanes of the quarter (l/16 == quarter: token l of the chunk).
+// f32 MFMAs without broadcast (v_mfma_f32_4x4x1_16B): block b = l/4 multiplies q of heads
+// 0..3 (A, lane 4b+i holds head i) by tokens 16*quarter + 4*(b%4) + c (B, lane 4b+c) at
+// channel 32*(b/4) + r; the q values come from the lanes holding them in qv (ds_bpermute),
+// and the four channel groups' sums meet across lanes 16 and 32 apart.
 template <int NRS>
-__device__ __forceinline__ void key_fp32(const AttnArgs& a, uint32_t unit, uint64_t t0, uint32_t lane,
-                                         const float (&qv)[NRS][16], float unit_scale,
-                                         float (&lg)[NRS][4]) {
-  const uint64_t t = t0 + lane;
+__device__ __forceinline__ void key_fp32(const AttnArgs& a, uint64_t t0, uint32_t quarter, uint32_t lane,
+                                         const float (&qv)[NRS][16], const KeyRows& kr,
+                                         float unit_scale, float (&lg)[NRS][4]) {
+  const uint64_t t = t0 + 16 * quarter + lane % 16;
   const float m = t >= a.st.kq && t < a.total ? unit_scale : 0.f;  // mask times 2^kExp
-  const float4* row = reinterpret_cast<const float4*>(key_row(a, unit, t));
-  v4f acc[NRS];
+  // qv of head l%4 at channels 16*la' + c sits in lane 4*la' + l%4 (la' = 2*(l/16) + c/16)
+  const int src0 = static_cast<int>(8 * (lane / 16) + lane % 4);
+  const int src1 = src0 + 4;
 #pragma unroll
-  for (int rs = 0; rs < NRS; ++rs) acc[rs] = v4f{lg[rs][0], lg[rs][1], lg[rs][2], lg[rs][3]};
-  // channels 16*a2 .. +15 per step; the next step's row segment is in flight meanwhile
-  float4 cur[4], nxt[4];
+  for (int rs = 0; rs < NRS; ++rs) {
+    v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int j = 0; j < 4; ++j) cur[j] = row[j];
-#pragma unroll
-  for (int a2 = 0; a2 < 8; ++a2) {
-    if (a2 + 1 < 8) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) nxt[j] = row[4 * (a2 + 1) + j];
+    for (int r = 0; r < 32; ++r) {
+      const float x = (r % 4 == 0 ? kr.x[r / 4].x : r % 4 == 1 ? kr.x[r / 4].y : r % 4 == 2 ? kr.x[r / 4].z : kr.x[r / 4].w) * m;
+      const float q = __shfl(qv[rs][r % 16], r < 16 ? src0 : src1);
+      acc = __builtin_amdgcn_mfma_f32_4x4x1f32(q, x, acc, 0, 0, 0);
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float x[4] = {cur[j].x * m, cur[j].y * m, cur[j].z * m, cur[j].w * m};
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-#pragma unroll
-        for (int rs = 0; rs < NRS; ++rs) acc[rs] = mfma_bcast(qv[rs][4 * j + r], x[r], acc[rs], a2);
+    for (int i = 0; i < 4; ++i) {
+      float v = acc[i];
+      v += __shfl_xor(v, 16);
+      v += __shfl_xor(v, 32);
+      lg[rs][i] += v;
     }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) cur[j] = nxt[j];
   }
+}
+
+// The quarter's fp32 value rows for channels lane and 64+lane (tokens 16*quarter .. +15, all
+// 32 values requested at once).
+struct ValueRows {
+  float b[16][2];
+};
+__device__ __forceinline__ void load_value_rows(const AttnArgs& a, uint32_t unit, uint64_t t0,
+                                                uint32_t quarter, uint32_t lane, ValueRows& vr) {
 #pragma unroll
-  for (int rs = 0; rs < NRS; ++rs)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) lg[rs][i] = acc[rs][i];
+  for (int r = 0; r < 16; ++r) {
+    const float* row = value_row(a, unit, t0 + 16 * quarter + r);
+    vr.b[r][0] = row[lane];
+    vr.b[r][1] = row[lane + 64];
+  }
 }
 
 // Value contribution of the chunk's fp32 values (tokens vq <= t < total) among tokens
@@ -689,10 +710,10 @@ __device__ __forceinline__ void key_fp32(const AttnArgs& a, uint32_t unit, uint6
 // for the lane's tokens 8*la + r (0 for other tokens), broadcast from block t/8; B = the
 // token's value row.
 template <int NRS>
-__device__ __forceinline__ void value_fp32(const AttnArgs& a, uint32_t unit, uint64_t t0,
-                                           uint32_t quarter, uint32_t lane, uint32_t la,
-                                           const float* wrow, const float (&moff)[NRS],
-                                           float kout, float wscale, v4f (&vacc)[NRS][2]) {
+__device__ __forceinline__ void value_fp32(const AttnArgs& a, uint64_t t0, uint32_t quarter,
+                                           uint32_t la, const float* wrow, const float (&moff)[NRS],
+                                           float kout, float wscale, const ValueRows& vr,
+                                           v4f (&vacc)[NRS][2]) {
   // A: lanes of block la hold the weights of tokens 16*quarter + 8*(la%2) + r, so the
   // quarter's 16 tokens sit in blocks 0 and 1 (ABID 0, 1) whatever the quarter
   const uint32_t tq = 16 * quarter + 8 * (la % 2);
@@ -709,20 +730,12 @@ __device__ __forceinline__ void value_fp32(const AttnArgs& a, uint32_t unit, uin
       am[rs][r] = __builtin_amdgcn_exp2f(fmaf(xs[r], kout, -moff[rs])) * m;
     }
   }
-  // tokens 16*quarter .. +15, all 32 values in flight at once
-  float b[16][2];
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const float* row = value_row(a, unit, t0 + 16 * quarter + r);
-    b[r][0] = row[lane];
-    b[r][1] = row[lane + 64];
-  }
 #pragma unroll
   for (int r = 0; r < 16; ++r)
 #pragma unroll
     for (int rs = 0; rs < NRS; ++rs) {
-      vacc[rs][0] = mfma_bcast(am[rs][r % 8], b[r][0], vacc[rs][0], r / 8);
-      vacc[rs][1] = mfma_bcast(am[rs][r % 8], b[r][1], vacc[rs][1], r / 8);
+      vacc[rs][0] = mfma_bcast(am[rs][r % 8], vr.b[r][0], vacc[rs][0], r / 8);
+      vacc[rs][1] = mfma_bcast(am[rs][r % 8], vr.b[r][1], vacc[rs][1], r / 8);
     }
 }
 
@@ -759,6 +772,19 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
   const int32_t nch = std::min<int32_t>(CPW, std::max<int32_t>(0, (span - slot + slots - 1) / slots));
   auto chunk_of = [&](int32_t k) { return static_cast<int32_t>(c_lo) + slot + k * slots; };
   const uint32_t quarter = MIXED ? wave : 0;
+  const uint64_t kq = a.st.kq, vq = a.st.vq, total = a.total;
+  const int32_t lastk = static_cast<int32_t>((kq - 1) / 64);  // kq > 0 on this path
+  const int32_t lastv = vq > 0 ? static_cast<int32_t>((vq - 1) / 64) : 0;
+
+  // The first chunk's key data are requested before anything else, so their latency
+  // overlaps the query loads and the range set-up.
+  KeyParams kp;
+  KeyWords<BITS> kw0, kw1;
+  if (nch > 0) {
+    const int32_t k0 = std::min(chunk_of(0), lastk);
+    load_key_params(a, unit, k0, la, lc, li, kp);
+    load_key_words<BITS>(a, unit, k0, lane, kw0);
+  }
 
   // q in base-2 logit units for the lane's head, channels 16*la .. +15 (0 for padded heads).
   float qv[NRS][16];
@@ -799,17 +825,12 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
   // zero (scale, zero) beyond kq (and vq), so each pass contributes nothing outside its range
   // and the fp32 passes mask theirs. Tokens past `total` get logit -inf.
   constexpr float kUnit = kExp == 0 ? 1.0f : kExp == -1 ? 0.5f : 0.001953125f;
-  const uint64_t kq = a.st.kq, vq = a.st.vq, total = a.total;
-  const int32_t lastk = static_cast<int32_t>((kq - 1) / 64);  // kq > 0 on this path
-  const int32_t lastv = vq > 0 ? static_cast<int32_t>((vq - 1) / 64) : 0;
   float mx[NRS][4];
 #pragma unroll
   for (int rs = 0; rs < NRS; ++rs)
 #pragma unroll
     for (int i = 0; i < 4; ++i) mx[rs][i] = -INFINITY;
   {
-    KeyParams kp;
-    KeyWords<BITS> kw0, kw1;
     KeyA<NRS> A;
     auto step = [&](int k, const KeyWords<BITS>& cur, KeyWords<BITS>& next) {
       const uint64_t t0 = (uint64_t)chunk_of(k) * 64;
@@ -827,7 +848,11 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
 #pragma unroll
         for (int i = 0; i < 4; ++i) lg[rs][i] = 0.f;
       if (packed) key_mfma<BITS, NRS>(cur, A, lg);
-      if (MIXED && t0 + 64 > kq && t0 < total) key_fp32<NRS>(a, unit, t0, lane, qv, kUnit, lg);
+      if (MIXED && t0 + 64 > kq && t0 < total) {
+        KeyRows kr;  // one round of loads: the quarter's rows, four lanes per row
+        load_key_rows(a, unit, t0, quarter, lane, kr);
+        key_fp32<NRS>(a, t0, quarter, lane, qv, kr, kUnit, lg);
+      }
       const bool live = !MIXED || (t0 + lane < total && t0 + lane >= a.t_min && lane / 16 == quarter);
 #pragma unroll
       for (int rs = 0; rs < NRS; ++rs)
@@ -838,11 +863,6 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
           mx[rs][i] = fmaxf(mx[rs][i], v);
         }
     };
-    if (nch > 0) {
-      const int32_t k0 = std::min(chunk_of(0), lastk);
-      load_key_params(a, unit, k0, la, lc, li, kp);
-      load_key_words<BITS>(a, unit, k0, lane, kw0);
-    }
     for (int k = 0; k < nch; k += 2) {
       step(k, kw0, kw1);
       if (k + 1 < nch) step(k + 1, kw1, kw0);
@@ -905,13 +925,16 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
         load_value_words<BITS>(a, unit, kn, lane, next);
       }
       if (packed) value_mfma<BITS, NRS>(cur, A, vacc);
-      if (MIXED && t0 + 16 * quarter + 16 > vq && t0 + 16 * quarter < total)
-        value_fp32<NRS>(a, unit, t0, quarter, lane, la, wl + li * ROW, moff, kout, vfac * kUnit, vacc);
+      if (MIXED && t0 + 16 * quarter + 16 > vq && t0 + 16 * quarter < total) {
+        ValueRows vr;
+        load_value_rows(a, unit, t0, quarter, lane, vr);
+        value_fp32<NRS>(a, t0, quarter, la, wl + li * ROW, moff, kout, vfac * kUnit, vr, vacc);
+      }
     };
     if (nch > 0) {
-      const int32_t k0 = std::min(chunk_of(0), lastv);
-      load_value_params(a, unit, k0, la, lc, li, vp);
-      load_value_words<BITS>(a, unit, k0, lane, vw0);
+      const int32_t v0 = std::min(chunk_of(0), lastv);
+      load_value_params(a, unit, v0, la, lc, li, vp);
+      load_value_words<BITS>(a, unit, v0, lane, vw0);
     }
     for (int k = 0; k < nch; k += 2) {
       step(k, vw0, vw1);
