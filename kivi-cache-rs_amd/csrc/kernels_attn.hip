@@ -284,9 +284,20 @@ __device__ void merge_unit(const float* ws, uint32_t unit, uint32_t nsplit, uint
     }
     const float inv = 1.0f / warp_sum(l);
     float* o = out + ((uint64_t)b * qh + kvh * gq + h) * D;
+    constexpr uint32_t kBatch = 16;  // splits per round of independent loads
     for (uint32_t d = lane; d < D; d += 64) {
       float acc = 0.f;
-      for (uint32_t s = 0; s < nsplit; ++s) acc = fmaf(load_partial(base + s * stride + d), fw[s], acc);
+      for (uint32_t s0 = 0; s0 < nsplit; s0 += kBatch) {
+        float v[kBatch];
+#pragma unroll
+        for (uint32_t j = 0; j < kBatch; ++j) {
+          const uint32_t s = s0 + j < nsplit ? s0 + j : 0u;
+          v[j] = load_partial(base + s * stride + d);
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < kBatch; ++j)
+          if (s0 + j < nsplit) acc = fmaf(v[j], fw[s0 + j], acc);
+      }
       o[d] = acc * inv;
     }
   }

@@ -31,6 +31,69 @@ __device__ __forceinline__ uint32_t quant_code(float x, float zero, float scale,
   return static_cast<uint32_t>(r);
 }
 
+// Reciprocal for quant_code_fast: 0 for a zero scale (every code is then 0).
+__device__ __forceinline__ float quant_inv(float scale) {
+  return scale == 0.0f ? 0.0f : __builtin_amdgcn_rcpf(scale);
+}
+
+// quant_code from a reciprocal, bit-identical to it. With v_rcp_f32's 1-ulp reciprocal,
+// q = (x - zero) * inv lies within q * 2^-22 <= 2^-14 of the correctly rounded quotient
+// (x - zero) / scale for q <= 256, so both round to the same integer unless q is within 2^-12
+// of a half-integer (or is not a finite value <= 256); those lanes divide.
+// x >= zero here (zero is the group minimum), so r >= 0 and the clamp is an integer min.
+__device__ __forceinline__ uint32_t quant_code_fast(float x, float zero, float scale, float inv,
+                                                    uint32_t levels) {
+#pragma clang fp contract(off)
+  const float d = x - zero;
+  const float q = d * inv;
+  float r = rintf(q);
+  const bool clear = fabsf((q - floorf(q)) - 0.5f) > 0x1p-12f && q <= 256.0f;
+  if (!clear) r = scale == 0.0f ? 0.0f : rintf(d / scale);
+  const uint32_t u = static_cast<uint32_t>(r);
+  return u < levels ? u : levels;
+}
+
+// DPP lane exchanges inside rows of 16 lanes (every lane active): quad_perm xor 1 and xor 2,
+// then mirrors that pair each lane with the other half of its 8- or 16-lane group.
+constexpr int kDppXor1 = 0xB1;
+constexpr int kDppXor2 = 0x4E;
+constexpr int kDppHalfMirror = 0x141;
+constexpr int kDppMirror = 0x140;
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
+  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, 0xF, 0xF, true));
+}
+
+// min and max over aligned groups of L lanes (L a power of two, 1 <= L <= 64; wave-uniform),
+// as compare-and-select (src/quant.rs:356 f32::min / max on finite values).
+__device__ __forceinline__ void minmax_with(float& mn, float& mx, float omn, float omx) {
+  mn = omn < mn ? omn : mn;
+  mx = omx > mx ? omx : mx;
+}
+template <uint32_t L>
+__device__ __forceinline__ void group_minmax(float& mn, float& mx) {
+  if constexpr (L >= 2) minmax_with(mn, mx, dpp_f<kDppXor1>(mn), dpp_f<kDppXor1>(mx));
+  if constexpr (L >= 4) minmax_with(mn, mx, dpp_f<kDppXor2>(mn), dpp_f<kDppXor2>(mx));
+  if constexpr (L >= 8) minmax_with(mn, mx, dpp_f<kDppHalfMirror>(mn), dpp_f<kDppHalfMirror>(mx));
+  if constexpr (L >= 16) minmax_with(mn, mx, dpp_f<kDppMirror>(mn), dpp_f<kDppMirror>(mx));
+  if constexpr (L >= 32) minmax_with(mn, mx, __shfl_xor(mn, 16), __shfl_xor(mx, 16));
+  if constexpr (L >= 64) minmax_with(mn, mx, __shfl_xor(mn, 32), __shfl_xor(mx, 32));
+}
+
+// OR over aligned groups of L lanes (L a power of two <= 16).
+template <uint32_t L>
+__device__ __forceinline__ uint32_t group_or(uint32_t v) {
+  if constexpr (L >= 2) v |= dpp_u<kDppXor1>(v);
+  if constexpr (L >= 4) v |= dpp_u<kDppXor2>(v);
+  if constexpr (L >= 8) v |= dpp_u<kDppHalfMirror>(v);
+  if constexpr (L >= 16) v |= dpp_u<kDppMirror>(v);
+  return v;
+}
+
 __device__ __forceinline__ const float* source_row(const RowSource& s, uint32_t unit, uint64_t i,
                                                    uint32_t R, uint32_t D) {
   uint64_t tok = s.offset + i;
@@ -38,8 +101,11 @@ __device__ __forceinline__ const float* source_row(const RowSource& s, uint32_t 
   return s.base + unit * s.stride_unit + tok * D;
 }
 
+// m = max(m, v) for a float v >= 0 kept as its bit pattern (device-scope atomic).
+__device__ __forceinline__ void raise_to(uint32_t* m, float v) { atomicMax(m, __float_as_uint(v)); }
+
 // Raise the unit's running maxima m[0] (largest scale) and m[2] (largest |x|) to the largest
-// `scale` / `amax` of the workgroup (one atomic each per workgroup).
+// `scale` / `amax` of the workgroup.
 __device__ __forceinline__ void raise_max(uint32_t* m, float scale, float amax) {
   __shared__ float red[2][kThreads / 64];
   for (int o = 32; o > 0; o >>= 1) {
@@ -57,8 +123,8 @@ __device__ __forceinline__ void raise_max(uint32_t* m, float scale, float amax) 
       a = fmaxf(a, red[0][w]);
       b = fmaxf(b, red[1][w]);
     }
-    atomicMax(m, __float_as_uint(a));
-    atomicMax(m + 2, __float_as_uint(b));
+    raise_to(m, a);
+    raise_to(m + 2, b);
   }
 }
 
@@ -330,33 +396,40 @@ __device__ __forceinline__ void wave_raise_max(uint32_t* m, float scale, float a
     amax = fmaxf(amax, __shfl_xor(amax, o));
   }
   if (threadIdx.x % 64 == 0) {
-    atomicMax(m, __float_as_uint(scale));
-    atomicMax(m + 2, __float_as_uint(amax));
+    raise_to(m, scale);
+    raise_to(m + 2, amax);
   }
 }
 
-// Keys: wave w of a workgroup takes item blockIdx.x*4 + w = (unit, group); the lane keeps its
-// channels of all GG rows in registers for the per-channel min/max (src/quant.rs:296-311).
-template <int CPL, int GG>
+// Keys: workgroup (unit, span) takes groups span*kKeySpan .. +kKeySpan-1 of the unit, wave w
+// those = w (mod 4); the lane keeps its channels of a group's GG rows in registers for the
+// per-channel min/max (src/quant.rs:296-311). Codes are packed in registers: the LPW lanes
+// whose channels share a token-major word OR their parts together (DPP), lane m of the group
+// keeps the words of tokens t = m (mod LPW), and each store writes 64 consecutive words. The
+// unit's running maxima are raised once per workgroup (a few units' maxima are hot addresses).
+constexpr uint32_t kKeySpan = 16;
+template <int BITS, int CPL, int GG>
 __global__ void __launch_bounds__(kThreads)
-    k_quant_keys_wave(CacheView c, RowSource src, uint64_t g0, uint32_t ngroups, uint32_t items) {
-  constexpr uint32_t D = 64 * CPL;
-  __shared__ uint8_t codes_all[4][GG * D];  // per wave [G][D]
+    k_quant_keys_wave(CacheView c, RowSource src, uint64_t g0, uint32_t ngroups, uint32_t spans) {
+  constexpr uint32_t D = 64 * CPL, PPW = 32 / BITS;
+  constexpr uint32_t LPW = PPW / CPL;   // lanes per code word
+  constexpr uint32_t KW = D / PPW;      // words per token (= 64 / LPW)
+  constexpr uint32_t NS = GG / LPW;     // words kept per lane
+  constexpr uint32_t kLevels = (1u << BITS) - 1u;
+  constexpr float levels = static_cast<float>(kLevels);
   const Geometry& geo = c.geo;
-  const uint32_t bits = geo.bits;
-  const float levels = static_cast<float>(geo.levels());
   const uint32_t lane = threadIdx.x % 64, wave = threadIdx.x / 64;
-  const uint32_t item = blockIdx.x * 4 + wave;
-  const bool active = item < items;
-  const uint32_t unit = active ? item / ngroups : 0, g = active ? item % ngroups : 0;
-  uint8_t* codes = codes_all[wave];
-  if (active) {
+  const uint32_t unit = blockIdx.x / spans;
+  const uint32_t g_end = std::min(ngroups, (blockIdx.x % spans + 1) * kKeySpan);
+  float smax = 0.f, amax = 0.f;
+  for (uint32_t g = (blockIdx.x % spans) * kKeySpan + wave; g < g_end; g += 4) {
     const float* rows = src.base + unit * src.stride_unit + (src.offset + (uint64_t)g * GG) * D;
     float x[GG][CPL];
 #pragma unroll
     for (int t = 0; t < GG; ++t) load_lane<CPL>(rows + (uint64_t)t * D, lane, x[t]);
-    float smax = 0.f, amax = 0.f;
     float2 sz[CPL];
+    float inv[CPL];
+    uint32_t sh[CPL];
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
       float mn = INFINITY, mx = -INFINITY;
@@ -366,111 +439,124 @@ __global__ void __launch_bounds__(kThreads)
         mx = fmaxf(mx, x[t][j]);
       }
       sz[j] = make_float2(scale_of(mx - mn, levels), mn);
+      inv[j] = quant_inv(sz[j].x);
+      sh[j] = code_shift(BITS, (CPL * lane + j) % PPW);
       smax = fmaxf(smax, sz[j].x);
       amax = fmaxf(amax, fmaxf(fabsf(mn), fabsf(mx)));
-#pragma unroll
-      for (int t = 0; t < GG; ++t)
-        codes[t * D + CPL * lane + j] = static_cast<uint8_t>(quant_code(x[t][j], sz[j].y, sz[j].x, levels));
     }
     float2* params = reinterpret_cast<float2*>(c.kparams + unit * geo.kparams_unit() + (g0 + g) * D * 2);
 #pragma unroll
     for (int j = 0; j < CPL; ++j) params[CPL * lane + j] = sz[j];
-    wave_raise_max(c.smax + 4 * unit, smax, amax);
-  }
-  __syncthreads();
-  if (active) {
-    const uint32_t ppw = geo.ppw(), kw = D / ppw;
-    uint32_t* words = c.kcodes + unit * geo.kcodes_unit() + (g0 + g) * GG * kw;
-    for (uint32_t w = lane; w < GG * kw; w += 64) {
-      const uint32_t t = w / kw, jw = w % kw;
-      const uint8_t* cc = codes + t * D + jw * ppw;
-      uint32_t word = 0;
-      for (uint32_t i = 0; i < ppw; ++i) word |= static_cast<uint32_t>(cc[i]) << code_shift(bits, i);
-      words[w] = word;
+    const uint32_t m = lane % LPW;
+    uint32_t keep[NS];
+#pragma unroll
+    for (int t = 0; t < GG; ++t) {
+      uint32_t part = 0;
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) part |= quant_code_fast(x[t][j], sz[j].y, sz[j].x, inv[j], kLevels) << sh[j];
+      part = group_or<LPW>(part);
+      if (t % LPW == 0) keep[t / LPW] = part;
+      else if (m == t % LPW) keep[t / LPW] = part;
     }
+    uint32_t* words = c.kcodes + unit * geo.kcodes_unit() + (g0 + g) * GG * KW;
+#pragma unroll
+    for (int s2 = 0; s2 < (int)NS; ++s2) words[(s2 * LPW + m) * KW + lane / LPW] = keep[s2];
   }
+  raise_max(c.smax + 4 * unit, smax, amax);
 }
 
-// Values: one workgroup per (unit, 64-token block); wave w takes rows w, w+4, ...; the group
-// min/max (src/quant.rs:349-375) reduces over the G/CPL lanes of a channel group by shuffles.
-template <int CPL>
+// Values: workgroup (unit, span) takes the unit's 64-token blocks span*kValueSpan .. +kValueSpan-1
+// of this call; in each, wave w takes the block's tokens 16w .. 16w+15 that lie in the call's
+// range. A lane holds channels CPL*lane .. +CPL-1 of each row; the group min/max
+// (src/quant.rs:349-375) reduces over the G/CPL lanes of a channel group (DPP), and the lane
+// packs its channels' codes of the 16 tokens into their channel-major words in registers
+// (16/PPW words per channel). The four waves' words meet in LDS (two buffers, one barrier per
+// block) so each block's words are stored contiguously; words that already hold earlier tokens
+// of the block are read and OR-ed (blocks fill across appends). The unit's running maxima are
+// raised once per workgroup.
+constexpr uint32_t kValueSpan = 4;
+template <int BITS, int CPL, int GG>
 __global__ void __launch_bounds__(kThreads)
     k_quant_values_wave(CacheView c, RowSource ring, uint32_t n_ring, RowSource in, uint64_t vq0,
-                        uint64_t n, uint64_t blk0, uint32_t nblk) {
-  constexpr uint32_t D = 64 * CPL;
-  __shared__ uint8_t codes_lds[kValueBlock * D];
+                        uint64_t n, uint64_t blk0, uint32_t nblk, uint32_t spans) {
+  constexpr uint32_t D = 64 * CPL, PPW = 32 / BITS, WPW = 16 / PPW;
+  constexpr uint32_t kLevels = (1u << BITS) - 1u;
+  constexpr float levels = static_cast<float>(kLevels);
+  constexpr uint32_t L = GG / CPL;  // lanes per channel group
+  constexpr uint32_t VW = kValueBlock / PPW, VWP = VW + 1;  // words per channel (LDS row padded)
+  __shared__ uint32_t words_lds[2][D * VWP];
   const Geometry& geo = c.geo;
-  const uint32_t G = geo.G, bits = geo.bits, R = geo.R, ncg = geo.ncg();
-  const uint32_t L = G / CPL;  // lanes per channel group (a power of two)
-  const float levels = static_cast<float>(geo.levels());
+  const uint32_t R = geo.R, ncg = geo.ncg();
   const uint32_t lane = threadIdx.x % 64, wave = threadIdx.x / 64;
-  const uint32_t unit = blockIdx.x / nblk;
-  const uint64_t tb = blk0 + blockIdx.x % nblk;
-  const uint64_t t_lo = vq0 > tb * kValueBlock ? vq0 : tb * kValueBlock;
-  const uint64_t t_end = vq0 + n;
-  const uint64_t t_hi = t_end < (tb + 1) * kValueBlock ? t_end : (tb + 1) * kValueBlock;
-  const uint32_t ntok = static_cast<uint32_t>(t_hi - t_lo);
+  const uint32_t unit = blockIdx.x / spans;
+  const uint32_t b_first = (blockIdx.x % spans) * kValueSpan;
+  const uint32_t b_end = std::min(nblk, b_first + kValueSpan);
   float2* params = reinterpret_cast<float2*>(c.vparams + unit * geo.vparams_unit());
-  const uint32_t cg = CPL * lane / G;
+  const uint32_t cg = CPL * lane / GG;
   float smax = 0.f, amax = 0.f;
-  // rows wave, wave+4, ... in batches of kRows, every batch's loads issued before its math
-  constexpr uint32_t kRows = 4;
-  for (uint32_t r0 = wave; r0 < ntok; r0 += 4 * kRows) {
-    float x[kRows][CPL];
+  for (uint32_t bi = b_first; bi < b_end; ++bi) {
+    const uint64_t tb = blk0 + bi;
+    uint32_t* wl = words_lds[bi % 2];
+    const uint64_t t0 = tb * kValueBlock + 16 * wave;  // first token of the wave's slot
+    const uint64_t t_lo = vq0 > t0 ? vq0 : t0;
+    const uint64_t t_hi = vq0 + n < t0 + 16 ? vq0 + n : t0 + 16;
+    if (t_lo < t_hi) {
+      float x[16][CPL];
 #pragma unroll
-    for (uint32_t b = 0; b < kRows; ++b) {
-      const uint32_t r = std::min<uint32_t>(r0 + 4 * b, ntok - 1);  // clamped: always a valid row
-      const uint64_t i = t_lo + r - vq0;
-      const float* row = i < n_ring ? source_row(ring, unit, i, R, D) : source_row(in, unit, i - n_ring, R, D);
-      load_lane<CPL>(row, lane, x[b]);
-    }
-#pragma unroll
-    for (uint32_t b = 0; b < kRows; ++b) {
-      const uint32_t r = r0 + 4 * b;
-      if (r >= ntok) break;
-      float mn = x[b][0], mx = x[b][0];
-#pragma unroll
-      for (int j = 1; j < CPL; ++j) {
-        mn = fminf(mn, x[b][j]);
-        mx = fmaxf(mx, x[b][j]);
+      for (int p = 0; p < 16; ++p) {
+        const uint64_t t = t0 + p < t_lo ? t_lo : t0 + p >= t_hi ? t_hi - 1 : t0 + p;  // a valid row
+        const uint64_t i = t - vq0;
+        const float* row = i < n_ring ? source_row(ring, unit, i, R, D) : source_row(in, unit, i - n_ring, R, D);
+        load_lane<CPL>(row, lane, x[p]);
       }
-      for (uint32_t o = 1; o < L; o <<= 1) {
-        mn = fminf(mn, __shfl_xor(mn, o));
-        mx = fmaxf(mx, __shfl_xor(mx, o));
-      }
-      const float scale = scale_of(mx - mn, levels);
-      smax = fmaxf(smax, scale);
-      amax = fmaxf(amax, fmaxf(fabsf(mn), fabsf(mx)));
-      const uint32_t tt = static_cast<uint32_t>((t_lo + r) % kValueBlock);
-      if (lane % L == 0) params[(tb * ncg + cg) * kValueBlock + tt] = make_float2(scale, mn);
+      uint32_t word[CPL][WPW];
 #pragma unroll
       for (int j = 0; j < CPL; ++j)
-        codes_lds[tt * D + CPL * lane + j] = static_cast<uint8_t>(quant_code(x[b][j], mn, scale, levels));
-    }
-  }
-  raise_max(c.smax + 4 * unit + 1, smax, amax);  // includes the barrier before the packing below
-  const uint32_t ppw = geo.ppw();
-  const uint32_t vw = geo.vwords_per_channel();
-  const uint32_t w_lo = static_cast<uint32_t>(t_lo % kValueBlock) / ppw;
-  const uint32_t w_hi = static_cast<uint32_t>((t_hi - 1) % kValueBlock) / ppw + 1;
-  const uint32_t nw = w_hi - w_lo;
-  uint32_t* base = c.vcodes + unit * geo.vcodes_unit() + tb * D * vw;
-  for (uint32_t idx = threadIdx.x; idx < D * nw; idx += blockDim.x) {
-    const uint32_t d = idx / nw, w = w_lo + idx % nw;
-    uint32_t word = 0;
-    bool keep_old = false;
-    for (uint32_t k = 0; k < ppw; ++k) {
-      const uint64_t t = tb * kValueBlock + w * ppw + k;
-      if (t >= t_lo && t < t_hi) {
-        word |= static_cast<uint32_t>(codes_lds[(t % kValueBlock) * D + d]) << code_shift(bits, k);
-      } else if (t < t_lo) {
-        keep_old = true;
+#pragma unroll
+        for (int k = 0; k < (int)WPW; ++k) word[j][k] = 0;
+#pragma unroll
+      for (int p = 0; p < 16; ++p) {
+        const bool valid = t0 + p >= t_lo && t0 + p < t_hi;
+        float mn = x[p][0], mx = x[p][0];
+#pragma unroll
+        for (int j = 1; j < CPL; ++j) {
+          mn = fminf(mn, x[p][j]);
+          mx = fmaxf(mx, x[p][j]);
+        }
+        group_minmax<L>(mn, mx);
+        const float scale = scale_of(mx - mn, levels);
+        const float inv = quant_inv(scale);
+        if (valid) {
+          smax = fmaxf(smax, scale);
+          amax = fmaxf(amax, fmaxf(fabsf(mn), fabsf(mx)));
+          if (lane % L == 0) params[(tb * ncg + cg) * kValueBlock + 16 * wave + p] = make_float2(scale, mn);
+        }
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+          const uint32_t code = quant_code_fast(x[p][j], mn, scale, inv, kLevels);
+          word[j][p / PPW] |= (valid ? code : 0u) << code_shift(BITS, p % PPW);
+        }
       }
+#pragma unroll
+      for (int j = 0; j < CPL; ++j)
+#pragma unroll
+        for (int k = 0; k < (int)WPW; ++k) wl[(CPL * lane + j) * VWP + 16 * wave / PPW + k] = word[j][k];
     }
-    uint32_t* dst = base + (uint64_t)d * vw + w;
-    if (keep_old) word |= *dst;
-    *dst = word;
+    __syncthreads();  // the block's words are in wl (the other buffer is free for the next block)
+    // the block's words with a token of this call: [b_lo, b_hi) is the call's range in the block
+    const uint64_t blk = tb * kValueBlock;
+    const uint64_t b_lo = vq0 > blk ? vq0 : blk;
+    const uint64_t b_hi = vq0 + n < blk + kValueBlock ? vq0 + n : blk + kValueBlock;
+    uint32_t* base = c.vcodes + unit * geo.vcodes_unit() + tb * D * VW;
+    for (uint32_t idx = threadIdx.x; idx < D * VW; idx += blockDim.x) {
+      const uint32_t d = idx / VW, wi = idx % VW;
+      const uint64_t w0 = blk + wi * PPW;  // first token of word wi
+      if (w0 + PPW <= b_lo || w0 >= b_hi) continue;
+      const uint32_t v = wl[d * VWP + wi];
+      base[idx] = w0 < b_lo ? (v | base[idx]) : v;
+    }
   }
+  raise_max(c.smax + 4 * unit + 1, smax, amax);
 }
 
 // ------------------------------------------------------------------ export to reference order
@@ -736,6 +822,51 @@ bool rows_vec4(const RowSource& r, uint32_t D) {
   return reinterpret_cast<uintptr_t>(r.base) % 16 == 0 && D % 4 == 0 && r.stride_unit % 4 == 0;
 }
 
+template <int BITS>
+bool keys_wave_bits(uint32_t cpl, uint32_t G, unsigned grid, hipStream_t stream, const CacheView& c,
+                    const RowSource& src, uint64_t g0, uint32_t ngroups, uint32_t spans) {
+  switch (cpl * 1000 + G) {
+    case 1016: k_quant_keys_wave<BITS, 1, 16><<<grid, kThreads, 0, stream>>>(c, src, g0, ngroups, spans); return true;
+    case 1032: k_quant_keys_wave<BITS, 1, 32><<<grid, kThreads, 0, stream>>>(c, src, g0, ngroups, spans); return true;
+    case 1064: k_quant_keys_wave<BITS, 1, 64><<<grid, kThreads, 0, stream>>>(c, src, g0, ngroups, spans); return true;
+    case 2016: k_quant_keys_wave<BITS, 2, 16><<<grid, kThreads, 0, stream>>>(c, src, g0, ngroups, spans); return true;
+    case 2032: k_quant_keys_wave<BITS, 2, 32><<<grid, kThreads, 0, stream>>>(c, src, g0, ngroups, spans); return true;
+    case 2064: k_quant_keys_wave<BITS, 2, 64><<<grid, kThreads, 0, stream>>>(c, src, g0, ngroups, spans); return true;
+    case 4016: k_quant_keys_wave<BITS, 4, 16><<<grid, kThreads, 0, stream>>>(c, src, g0, ngroups, spans); return true;
+    case 4032: k_quant_keys_wave<BITS, 4, 32><<<grid, kThreads, 0, stream>>>(c, src, g0, ngroups, spans); return true;
+    default: return false;
+  }
+}
+
+bool keys_wave_dispatch(uint32_t bits, uint32_t cpl, uint32_t G, unsigned grid, hipStream_t stream,
+                        const CacheView& c, const RowSource& src, uint64_t g0, uint32_t ngroups,
+                        uint32_t spans) {
+  switch (bits) {
+    case 2: return keys_wave_bits<2>(cpl, G, grid, stream, c, src, g0, ngroups, spans);
+    case 4: return keys_wave_bits<4>(cpl, G, grid, stream, c, src, g0, ngroups, spans);
+    case 8: return keys_wave_bits<8>(cpl, G, grid, stream, c, src, g0, ngroups, spans);
+    default: return false;
+  }
+}
+
+template <int BITS>
+bool values_wave_bits(uint32_t cpl, uint32_t G, unsigned grid, uint32_t spans, hipStream_t stream, const CacheView& c,
+                      const RowSource& ring, uint32_t n_ring, const RowSource& in, uint64_t vq0,
+                      uint64_t n, uint64_t blk0, uint32_t nblk) {
+#define KIVI_VW(C, GG)                                                                              \
+  case C * 1000 + GG:                                                                               \
+    k_quant_values_wave<BITS, C, GG><<<grid, kThreads, 0, stream>>>(c, ring, n_ring, in, vq0, n,  \
+                                                                    blk0, nblk, spans);            \
+    return true;
+  switch (cpl * 1000 + G) {
+    KIVI_VW(1, 16) KIVI_VW(1, 32) KIVI_VW(1, 64)
+    KIVI_VW(2, 16) KIVI_VW(2, 32) KIVI_VW(2, 64)
+    KIVI_VW(4, 16) KIVI_VW(4, 32)
+    default: return false;
+  }
+#undef KIVI_VW
+}
+
 hipError_t launch_quant_keys(const CacheView& c, RowSource src, uint64_t g0, uint32_t ngroups,
                              hipStream_t stream) {
   if (ngroups == 0) return hipSuccess;
@@ -750,19 +881,10 @@ hipError_t launch_quant_keys(const CacheView& c, RowSource src, uint64_t g0, uin
   const bool lane_aligned = c.geo.D % 64 == 0 && reinterpret_cast<uintptr_t>(src.base) % (4 * cpl) == 0 &&
                             src.stride_unit % (4 * cpl) == 0 && blocks <= (1ull << 31);
   if (lane_aligned) {
-    const uint32_t items = static_cast<uint32_t>(blocks);
-    const unsigned grid = (items + 3) / 4;
-    switch (cpl * 1000 + c.geo.G) {
-      case 1016: k_quant_keys_wave<1, 16><<<grid, kThreads, 0, stream>>>(c, src, g0, ngroups, items); return hipGetLastError();
-      case 1032: k_quant_keys_wave<1, 32><<<grid, kThreads, 0, stream>>>(c, src, g0, ngroups, items); return hipGetLastError();
-      case 1064: k_quant_keys_wave<1, 64><<<grid, kThreads, 0, stream>>>(c, src, g0, ngroups, items); return hipGetLastError();
-      case 2016: k_quant_keys_wave<2, 16><<<grid, kThreads, 0, stream>>>(c, src, g0, ngroups, items); return hipGetLastError();
-      case 2032: k_quant_keys_wave<2, 32><<<grid, kThreads, 0, stream>>>(c, src, g0, ngroups, items); return hipGetLastError();
-      case 2064: k_quant_keys_wave<2, 64><<<grid, kThreads, 0, stream>>>(c, src, g0, ngroups, items); return hipGetLastError();
-      case 4016: k_quant_keys_wave<4, 16><<<grid, kThreads, 0, stream>>>(c, src, g0, ngroups, items); return hipGetLastError();
-      case 4032: k_quant_keys_wave<4, 32><<<grid, kThreads, 0, stream>>>(c, src, g0, ngroups, items); return hipGetLastError();
-      default: break;
-    }
+    const uint32_t spans = (ngroups + kKeySpan - 1) / kKeySpan;
+    const unsigned grid = c.geo.units * spans;
+    if (keys_wave_dispatch(c.geo.bits, cpl, c.geo.G, grid, stream, c, src, g0, ngroups, spans))
+      return hipGetLastError();
   }
   k_quant_keys<<<static_cast<unsigned>(blocks), kThreads, lds, stream>>>(c, src, g0, ngroups, staged ? 1u : 0u,
                                                                         rows_vec4(src, c.geo.D) ? 1u : 0u);
@@ -796,13 +918,17 @@ hipError_t launch_quant_values(const CacheView& c, RowSource ring, uint32_t n_ri
   };
   if (D % 64 == 0 && (cpl == 1 || cpl == 2 || cpl == 4) && c.geo.G % cpl == 0 && lanes_per_group <= 64 &&
       (lanes_per_group & (lanes_per_group - 1)) == 0 && aligned(ring) && (n_in == 0 || aligned(in))) {
-    if (cpl == 1)
-      k_quant_values_wave<1><<<static_cast<unsigned>(blocks), kThreads, 0, stream>>>(c, ring, n_ring, in, vq0, n, blk0, nblk);
-    else if (cpl == 2)
-      k_quant_values_wave<2><<<static_cast<unsigned>(blocks), kThreads, 0, stream>>>(c, ring, n_ring, in, vq0, n, blk0, nblk);
-    else
-      k_quant_values_wave<4><<<static_cast<unsigned>(blocks), kThreads, 0, stream>>>(c, ring, n_ring, in, vq0, n, blk0, nblk);
-    return hipGetLastError();
+    const uint32_t spans = (nblk + kValueSpan - 1) / kValueSpan;
+    const unsigned nb = c.geo.units * spans;
+    const uint32_t G = c.geo.G;
+    bool done = false;
+    switch (c.geo.bits) {
+      case 2: done = values_wave_bits<2>(cpl, G, nb, spans, stream, c, ring, n_ring, in, vq0, n, blk0, nblk); break;
+      case 4: done = values_wave_bits<4>(cpl, G, nb, spans, stream, c, ring, n_ring, in, vq0, n, blk0, nblk); break;
+      case 8: done = values_wave_bits<8>(cpl, G, nb, spans, stream, c, ring, n_ring, in, vq0, n, blk0, nblk); break;
+      default: break;
+    }
+    if (done) return hipGetLastError();
   }
   k_quant_values<<<static_cast<unsigned>(blocks), kThreads, lds, stream>>>(c, ring, n_ring, in, vq0, n,
                                                                          blk0, nblk, TB, vec4 ? 1u : 0u);
