@@ -115,6 +115,61 @@ def test_attention_parity_long(amd, oracle, bits, gqa):
     assert max_abs(got, dense_attend(kh, vh, q, batch, heads, heads * gqa, seq, dim, scale)) < 1e-4
 
 
+def near_ties(levels, group, rows, cols, per_row, rng):
+    """[rows][cols] f32 whose quotients (x - min) / scale sit within a few ulps of a
+    half-integer: each group of `group` elements (along a row when per_row, down a column
+    otherwise) holds its min m and m + levels*s, so scale = s, and the rest are
+    m + (n + 0.5 + e)*s for random n < levels, with e = k*2^-21 (k in [-4, 4]) or, for half
+    of them, e = +-(2^-12 + j*2^-17) (j in [0, 16]): just outside the band the kernels divide in."""
+    m = rng.uniform(-3, 3, size=(rows, cols)).astype(np.float32)
+    s = rng.uniform(0.01, 2, size=(rows, cols)).astype(np.float32)
+    if per_row:  # one (m, s) per group of columns
+        m = np.repeat(m[:, ::group], group, axis=1)[:, :cols]
+        s = np.repeat(s[:, ::group], group, axis=1)[:, :cols]
+    else:
+        m = np.repeat(m[::group], group, axis=0)[:rows]
+        s = np.repeat(s[::group], group, axis=0)[:rows]
+    n = rng.integers(0, levels, size=(rows, cols)).astype(np.float64)
+    e = rng.integers(-4, 5, size=(rows, cols)) * 2.0 ** -21
+    edge = (2.0 ** -12 + rng.integers(0, 17, size=(rows, cols)) * 2.0 ** -17) * rng.choice([-1.0, 1.0], size=(rows, cols))
+    e = np.where(rng.random((rows, cols)) < 0.5, e, edge)
+    x = (m.astype(np.float64) + (n + 0.5 + e) * s.astype(np.float64)).astype(np.float32)
+    lo = m
+    hi = (m.astype(np.float64) + levels * s.astype(np.float64)).astype(np.float32)
+    if per_row:
+        x[:, 0::group], x[:, 1::group] = lo[:, 0::group], hi[:, 1::group]
+    else:
+        x[0::group], x[1::group] = lo[0::group], hi[1::group]
+    return x
+
+
+@pytest.mark.parametrize("bits", [2, 4, 8])
+def test_near_tie_codes_parity(amd, oracle, bits):
+    """Codes whose quotients lie within a few ulps of a rounding boundary (the quantize
+    kernels' reciprocal fast path hands those to an exact division): bit-exact streams through
+    bulk appends, decode appends and value-window evictions."""
+    batch, heads, dim, group, residual = 2, 2, 128, 32, 128
+    chunks = [300, 1, 37, 64, 1, 1, 200]
+    total = sum(chunks)
+    levels = (1 << bits) - 1
+    rng = np.random.default_rng(77 + bits)
+    keys = near_ties(levels, group, batch * heads * total, dim, False, rng)  # groups of tokens
+    values = near_ties(levels, group, batch * heads * total, dim, True, rng)  # groups of channels
+    keys = keys.reshape(batch, heads, total, dim)
+    values = values.reshape(batch, heads, total, dim)
+    cfg = KiviConfig(bits, group, residual)
+    a = KiviCache(amd, cfg, batch, heads, dim)
+    o = KiviCache(oracle, cfg, batch, heads, dim)
+    off = 0
+    for n in chunks:
+        k = keys[:, :, off:off + n].copy()
+        v = values[:, :, off:off + n].copy()
+        a.append(k, v, n)
+        o.append(k, v, n)
+        off += n
+        assert_streams_equal(a, o)
+
+
 @pytest.mark.parametrize("bits,group", [(2, 32), (4, 32), (8, 32), (2, 16), (4, 64), (8, 4)])
 @pytest.mark.parametrize("dim", [32, 128])
 def test_standalone_quantize_parity(amd, oracle, bits, group, dim):
