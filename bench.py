@@ -7,7 +7,9 @@ channels (2 per KV head) scaled x10, V ~ N(0,1), fp32 inputs. A step is one deco
 over all 16 sequences (the cache and the queries already resident in HBM); value = decode
 tokens/s = 16 * steps / time. The cache build (prefill quantization) is timed once and
 reported as quantize GB/s. The CPU baseline is the oracle (C++ restatement of the
-reference CPU path, 1 core) on one of the 16 sequences.
+reference CPU path, 1 core) on one of the 16 sequences. Before the prefill and before the W
+warm-up steps the GPU runs ~0.3 s of untimed work (device copies, then the step's own
+kernels) so that its clocks have ramped up; `clock_warmup_calls` counts the second part.
 
 The roofline object is for the dominant kernel (the packed-chunk attention kernel): its
 algorithmic bytes per launch (packed codes + (scale, zero) of the chunks it covers, plus the
@@ -227,6 +229,23 @@ def recorded_traffic(kernel, workload, bytes_per_launch):
     return None
 
 
+CLOCK_WARMUP_S = 0.3
+
+
+def clock_warmup(torch, stream, fn, seconds=CLOCK_WARMUP_S, batch=20):
+    """Untimed GPU work before a measurement: the MI355X raises its clocks over tens of
+    milliseconds of load, so a few warm-up steps alone leave the timed region on the ramp
+    (C2: 137 us/step after 10 warm-up steps, 116 us after 200). Returns the calls made."""
+    t0, n = time.perf_counter(), 0
+    while time.perf_counter() - t0 < seconds:
+        with torch.cuda.stream(stream):
+            for _ in range(batch):
+                fn()
+        stream.synchronize()
+        n += batch
+    return n
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -266,6 +285,11 @@ def main():
     warm.attention_device(wq.data_ptr(), wq.numel(), qh, 0.1, wo.data_ptr(), wo.numel(), sp)
     stream.synchronize()
     del warm, wk, wq, wo
+    # clocks up before the prefill quantize is timed: device copies of the input's size
+    scratch = torch.empty_like(k)
+    clock_warmup(torch, stream, lambda: scratch.copy_(k), batch=4)
+    del scratch
+    torch.cuda.empty_cache()
     decode_steps = DECODE.get(args.config)
     if decode_steps:
         # RuntimeKv (src/runtime.rs:12-57): prefill through its cache, then decode steps
@@ -357,6 +381,10 @@ def main():
         def step():
             cache.attention_device(qp, n_q, qh, scale, op, n_q, sp)
 
+    # clocks up on the step's own kernels (C1: attention over the cache, which leaves the
+    # decode state alone), then the W warm-up steps
+    extra_warmup = clock_warmup(torch, stream, step if not decode_steps else
+                                (lambda: cache.attention_device(qd[0].data_ptr(), n_q, qh, scale, op, n_q, sp)))
     with torch.cuda.stream(stream):
         for _ in range(args.warmup):
             step()
@@ -448,6 +476,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "clock_warmup_calls": extra_warmup,
         "ms_per_step": per_step * 1e3,
         "higher_is_better": True,
         "scaling": "weak",
