@@ -38,8 +38,9 @@ __device__ __forceinline__ float quant_inv(float scale) {
 
 // quant_code from a reciprocal, bit-identical to it. With v_rcp_f32's 1-ulp reciprocal,
 // q = (x - zero) * inv lies within q * 2^-22 <= 2^-14 of the correctly rounded quotient
-// (x - zero) / scale for q <= 256, so both round to the same integer unless q is within 2^-12
-// of a half-integer (or is not a finite value <= 256); those lanes divide.
+// (x - zero) / scale (0 <= x - zero <= span keeps q <= levels (1 + 2^-22) <= 256), so both
+// round to the same integer unless q is within 2^-12 of a half-integer: |q - rint(q)| >=
+// 0.5 - 2^-12, which is also true of a non-finite q (inv = inf); those lanes divide.
 // x >= zero here (zero is the group minimum), so r >= 0 and the clamp is an integer min.
 __device__ __forceinline__ uint32_t quant_code_fast(float x, float zero, float scale, float inv,
                                                     uint32_t levels) {
@@ -47,8 +48,7 @@ __device__ __forceinline__ uint32_t quant_code_fast(float x, float zero, float s
   const float d = x - zero;
   const float q = d * inv;
   float r = rintf(q);
-  const bool clear = fabsf((q - floorf(q)) - 0.5f) > 0x1p-12f && q <= 256.0f;
-  if (!clear) r = scale == 0.0f ? 0.0f : rintf(d / scale);
+  if (!(fabsf(q - r) < 0.5f - 0x1p-12f)) r = scale == 0.0f ? 0.0f : rintf(d / scale);
   const uint32_t u = static_cast<uint32_t>(r);
   return u < levels ? u : levels;
 }
@@ -82,6 +82,19 @@ __device__ __forceinline__ void group_minmax(float& mn, float& mx) {
   if constexpr (L >= 16) minmax_with(mn, mx, dpp_f<kDppMirror>(mn), dpp_f<kDppMirror>(mx));
   if constexpr (L >= 32) minmax_with(mn, mx, __shfl_xor(mn, 16), __shfl_xor(mx, 16));
   if constexpr (L >= 64) minmax_with(mn, mx, __shfl_xor(mn, 32), __shfl_xor(mx, 32));
+}
+
+// v as held by lane p of the lane's 16-lane row (DPP row_newbcast).
+__device__ __forceinline__ float row_bcast(float v, int p) {
+  const int x = __float_as_int(v);
+  switch (p) {
+#define KIVI_RB(P) \
+  case P: return __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0x150 + P, 0xF, 0xF, true));
+    KIVI_RB(0) KIVI_RB(1) KIVI_RB(2) KIVI_RB(3) KIVI_RB(4) KIVI_RB(5) KIVI_RB(6) KIVI_RB(7)
+    KIVI_RB(8) KIVI_RB(9) KIVI_RB(10) KIVI_RB(11) KIVI_RB(12) KIVI_RB(13) KIVI_RB(14)
+#undef KIVI_RB
+    default: return __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0x15F, 0xF, 0xF, true));
+  }
 }
 
 // OR over aligned groups of L lanes (L a power of two <= 16).
@@ -487,7 +500,8 @@ __global__ void __launch_bounds__(kThreads)
   __shared__ uint32_t words_lds[2][D * VWP];
   const Geometry& geo = c.geo;
   const uint32_t R = geo.R, ncg = geo.ncg();
-  const uint32_t lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+  const uint32_t lane = threadIdx.x % 64;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);  // wave-uniform
   const uint32_t unit = blockIdx.x / spans;
   const uint32_t b_first = (blockIdx.x % spans) * kValueSpan;
   const uint32_t b_end = std::min(nblk, b_first + kValueSpan);
@@ -514,27 +528,63 @@ __global__ void __launch_bounds__(kThreads)
       for (int j = 0; j < CPL; ++j)
 #pragma unroll
         for (int k = 0; k < (int)WPW; ++k) word[j][k] = 0;
+      if constexpr (L == 16) {
+        // A channel group is a DPP row of 16 lanes and the wave has 16 rows: lane r of each
+        // group divides for row r once (one division for the 16 rows), stores row r's
+        // (scale, zero) (16 consecutive pairs per group), and row_newbcast hands each row's
+        // scale and reciprocal to the group's lanes.
+        float mnv[16];
+        const uint32_t r = lane % 16;
+        float span_r = 0.f, mn_r = 0.f;
 #pragma unroll
-      for (int p = 0; p < 16; ++p) {
-        const bool valid = t0 + p >= t_lo && t0 + p < t_hi;
-        float mn = x[p][0], mx = x[p][0];
+        for (int p = 0; p < 16; ++p) {
+          float mn = x[p][0], mx = x[p][0];
 #pragma unroll
-        for (int j = 1; j < CPL; ++j) {
-          mn = fminf(mn, x[p][j]);
-          mx = fmaxf(mx, x[p][j]);
+          for (int j = 1; j < CPL; ++j) minmax_with(mn, mx, x[p][j], x[p][j]);
+          group_minmax<L>(mn, mx);
+          mnv[p] = mn;
+          if (t0 + p >= t_lo && t0 + p < t_hi) amax = fmaxf(amax, fmaxf(fabsf(mn), fabsf(mx)));
+          if (r == (uint32_t)p) {
+            span_r = mx - mn;
+            mn_r = mn;
+          }
         }
-        group_minmax<L>(mn, mx);
-        const float scale = scale_of(mx - mn, levels);
-        const float inv = quant_inv(scale);
-        if (valid) {
-          smax = fmaxf(smax, scale);
-          amax = fmaxf(amax, fmaxf(fabsf(mn), fabsf(mx)));
-          if (lane % L == 0) params[(tb * ncg + cg) * kValueBlock + 16 * wave + p] = make_float2(scale, mn);
+        const float scale_r = scale_of(span_r, levels);
+        const float inv_r = quant_inv(scale_r);
+        if (t0 + r >= t_lo && t0 + r < t_hi) {
+          smax = fmaxf(smax, scale_r);
+          params[(tb * ncg + cg) * kValueBlock + 16 * wave + r] = make_float2(scale_r, mn_r);
         }
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) {
-          const uint32_t code = quant_code_fast(x[p][j], mn, scale, inv, kLevels);
-          word[j][p / PPW] |= (valid ? code : 0u) << code_shift(BITS, p % PPW);
+        for (int p = 0; p < 16; ++p) {
+          const bool valid = t0 + p >= t_lo && t0 + p < t_hi;
+          const float scale = row_bcast(scale_r, p), inv = row_bcast(inv_r, p);
+#pragma unroll
+          for (int j = 0; j < CPL; ++j) {
+            const uint32_t code = quant_code_fast(x[p][j], mnv[p], scale, inv, kLevels);
+            word[j][p / PPW] |= (valid ? code : 0u) << code_shift(BITS, p % PPW);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int p = 0; p < 16; ++p) {
+          const bool valid = t0 + p >= t_lo && t0 + p < t_hi;
+          float mn = x[p][0], mx = x[p][0];
+#pragma unroll
+          for (int j = 1; j < CPL; ++j) minmax_with(mn, mx, x[p][j], x[p][j]);
+          group_minmax<L>(mn, mx);
+          const float scale = scale_of(mx - mn, levels);
+          const float inv = quant_inv(scale);
+          if (valid) {
+            smax = fmaxf(smax, scale);
+            amax = fmaxf(amax, fmaxf(fabsf(mn), fabsf(mx)));
+            if (lane % L == 0) params[(tb * ncg + cg) * kValueBlock + 16 * wave + p] = make_float2(scale, mn);
+          }
+#pragma unroll
+          for (int j = 0; j < CPL; ++j) {
+            const uint32_t code = quant_code_fast(x[p][j], mn, scale, inv, kLevels);
+            word[j][p / PPW] |= (valid ? code : 0u) << code_shift(BITS, p % PPW);
+          }
         }
       }
 #pragma unroll
