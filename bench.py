@@ -10,6 +10,10 @@ reported as quantize GB/s. The CPU baseline is the oracle (C++ restatement of th
 reference CPU path, 1 core) on one of the 16 sequences. Before the prefill and before the W
 warm-up steps the GPU runs ~0.3 s of untimed work (device copies, then the step's own
 kernels) so that its clocks have ramped up; `clock_warmup_calls` counts the second part.
+Workloads whose cache is smaller than three times the 256 MB Infinity Cache (C3, C4) rotate
+over identical cache copies between steps (`cache_copies`), so each step reads its cache from
+HBM rather than from the previous step's cache lines; C0 and C1 are too small for that and
+report `cache_resident: true`.
 
 The roofline object is for the dominant kernel (the packed-chunk attention kernel): its
 algorithmic bytes per launch (packed codes + (scale, zero) of the chunks it covers, plus the
@@ -230,6 +234,8 @@ def recorded_traffic(kernel, workload, bytes_per_launch):
 
 
 CLOCK_WARMUP_S = 0.3
+ROTATE_BYTES = 768 << 20  # three times the MI355X Infinity Cache
+MAX_COPIES = 8
 
 
 def clock_warmup(torch, stream, fn, seconds=CLOCK_WARMUP_S, batch=20):
@@ -290,12 +296,11 @@ def main():
     clock_warmup(torch, stream, lambda: scratch.copy_(k), batch=4)
     del scratch
     torch.cuda.empty_cache()
-    decode_steps = DECODE.get(args.config)
-    if decode_steps:
+    if DECODE.get(args.config):
         # RuntimeKv (src/runtime.rs:12-57): prefill through its cache, then decode steps
         runtime = kivi.RuntimeKv(amd, kivi.KiviConfig(bits, G, R), batch, heads, dim)
         cache = runtime.cache()
-        cache.reserve(seq + decode_steps)
+        cache.reserve(seq + DECODE[args.config])
     else:
         cache = kivi.KiviCache(amd, kivi.KiviConfig(bits, G, R), batch, heads, dim)
         cache.reserve(seq)
@@ -319,6 +324,28 @@ def main():
     mem = cache.memory()
     quant_bytes = 2 * k.numel() * 4 + mem.compressed_bytes()
     log(f"[bench] prefill quantize {quant_bytes / t_quant / 1e9:.1f} GB/s ({t_quant * 1e3:.2f} ms)")
+
+    # A step whose cache is smaller than the 256 MB Infinity Cache (MALL) could be served
+    # from it by the previous step. Such workloads rotate over `copies` identical caches (the
+    # same prefill), so consecutive steps touch >= ROTATE_BYTES of distinct data and each step
+    # reads its cache from HBM. Decode steps (C1) and caches too small to rotate out of the
+    # MALL within MAX_COPIES report `cache_resident`.
+    decode_steps = DECODE.get(args.config)
+    step_bytes = mem.compressed_bytes() + (SESSIONS[args.config][0] * batch * heads *
+                                           SESSIONS[args.config][1] * dim * 8 if args.config in SESSIONS else 0)
+    copies = 1
+    if not decode_steps and step_bytes < ROTATE_BYTES:
+        copies = min(MAX_COPIES, -(-ROTATE_BYTES // step_bytes))
+    cache_resident = copies * step_bytes < ROTATE_BYTES
+    caches = [cache]
+    for _ in range(copies - 1):
+        c2_ = kivi.KiviCache(amd, kivi.KiviConfig(bits, G, R), batch, heads, dim)
+        c2_.reserve(seq)
+        c2_.append_device(k.data_ptr(), k.numel(), v.data_ptr(), v.numel(), seq, sp)
+        caches.append(c2_)
+    stream.synchronize()
+    if copies > 1:
+        log(f"[bench] {copies} cache copies rotate between steps ({copies * step_bytes / 1e6:.0f} MB)")
     del k, v
     torch.cuda.empty_cache()
 
@@ -328,27 +355,34 @@ def main():
         # shared prefix + RagSessions with private fp32 suffixes; a step is one batched
         # attention over all sessions (the prefix streamed once per step)
         n_sess, suffix = sessions_cfg
-        prefix = cache.share_prefix()
-        del cache
-        torch.cuda.empty_cache()
-        sessions = [prefix.session() for _ in range(n_sess)]
         gs = torch.Generator(device="cuda")
         gs.manual_seed(2002)
-        for se in sessions:
-            sk = torch.randn((batch, heads, suffix, dim), generator=gs, device="cuda")
-            sv = torch.randn((batch, heads, suffix, dim), generator=gs, device="cuda")
-            se.append_device(sk.data_ptr(), sk.numel(), sv.data_ptr(), sv.numel(), suffix, sp)
+        sks = [torch.randn((batch, heads, suffix, dim), generator=gs, device="cuda") for _ in range(n_sess)]
+        svs = [torch.randn((batch, heads, suffix, dim), generator=gs, device="cuda") for _ in range(n_sess)]
+        prefixes, all_sessions, all_handles = [], [], []
+        for cc in caches:
+            prefix = cc.share_prefix()
+            sessions = [prefix.session() for _ in range(n_sess)]
+            for se, sk, sv in zip(sessions, sks, svs):
+                se.append_device(sk.data_ptr(), sk.numel(), sv.data_ptr(), sv.numel(), suffix, sp)
+            prefixes.append(prefix)
+            all_sessions.append(sessions)
+            all_handles.append(kivi.session_handles(sessions))
+        del cache, caches, cc
+        torch.cuda.empty_cache()
         stream.synchronize()
         q = torch.randn((n_sess, batch, qh, dim), generator=gs, device="cuda")
         out = torch.empty_like(q)
-        handles = kivi.session_handles(sessions)
         qp, op, n_q = q.data_ptr(), out.data_ptr(), q.numel()
         tokens_per_step = n_sess * batch
-        kv_bytes = prefix.prefix_bytes() + n_sess * batch * heads * suffix * dim * 4 * 2
+        kv_bytes = prefixes[0].prefix_bytes() + n_sess * batch * heads * suffix * dim * 4 * 2
+        turn = [0]
 
         def step():
-            kivi.sessions_attention_device(amd, sessions, qp, n_q, qh, scale, op, n_q, sp,
-                                           handles=handles)
+            i = turn[0] % copies
+            turn[0] += 1
+            kivi.sessions_attention_device(amd, all_sessions[i], qp, n_q, qh, scale, op, n_q, sp,
+                                           handles=all_handles[i])
     elif decode_steps:
         # one decode step = append one token (key residual, value window, flush every R) and
         # attend; the plain and the evented timed regions each run `steps` of them
@@ -377,9 +411,12 @@ def main():
         qp, op, n_q = q.data_ptr(), out.data_ptr(), q.numel()
         tokens_per_step = batch
         kv_bytes = mem.compressed_bytes()
+        turn = [0]
 
         def step():
-            cache.attention_device(qp, n_q, qh, scale, op, n_q, sp)
+            i = turn[0] % copies
+            turn[0] += 1
+            caches[i].attention_device(qp, n_q, qh, scale, op, n_q, sp)
 
     # clocks up on the step's own kernels (C1: attention over the cache, which leaves the
     # decode state alone), then the W warm-up steps
@@ -477,6 +514,8 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "clock_warmup_calls": extra_warmup,
+        "cache_copies": copies,
+        "cache_resident": cache_resident,
         "ms_per_step": per_step * 1e3,
         "higher_is_better": True,
         "scaling": "weak",
