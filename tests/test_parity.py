@@ -115,6 +115,32 @@ def test_attention_parity_long(amd, oracle, bits, gqa):
     assert max_abs(got, dense_attend(kh, vh, q, batch, heads, heads * gqa, seq, dim, scale)) < 1e-4
 
 
+@pytest.mark.parametrize("bits", [2, 4, 8])
+@pytest.mark.parametrize("dim,group", [(64, 16), (64, 64), (128, 16), (256, 16), (256, 32),
+                                       (256, 64)])
+def test_quantize_lane_layouts_parity(amd, oracle, bits, dim, group):
+    """The quantize kernels' lane layouts (channels per lane 1/2/4, lanes per channel group
+    4..64, lanes per code word) through bulk, odd-sized and single-token appends."""
+    batch, heads, residual = 1, 3, 2 * group if group >= 64 else 64
+    chunks = [200, 1, 37, 130, 1, 64]
+    total = sum(chunks)
+    rng = np.random.default_rng(dim * 10 + group + bits)
+    keys = rng.standard_normal((batch, heads, total, dim)).astype(np.float32)
+    keys[:, :, :, 1] *= 10
+    values = rng.standard_normal((batch, heads, total, dim)).astype(np.float32)
+    cfg = KiviConfig(bits, group, residual)
+    a = KiviCache(amd, cfg, batch, heads, dim)
+    o = KiviCache(oracle, cfg, batch, heads, dim)
+    off = 0
+    for n in chunks:
+        k = keys[:, :, off:off + n].copy()
+        v = values[:, :, off:off + n].copy()
+        a.append(k, v, n)
+        o.append(k, v, n)
+        off += n
+        assert_streams_equal(a, o)
+
+
 def near_ties(levels, group, rows, cols, per_row, rng):
     """[rows][cols] f32 whose quotients (x - min) / scale sit within a few ulps of a
     half-integer: each group of `group` elements (along a row when per_row, down a column
