@@ -1073,10 +1073,10 @@ __global__ void __launch_bounds__(kThreads) k_attn_sessions(AttnArgs a, SessionT
 }
 
 // Log-sum-exp merge of the split partials: one workgroup per (session, unit, head) of
-// `parts` groups of dt = ceil(D/64)*64 threads. Every wave reduces the splits' (m, l) pairs
-// itself (no barrier); thread (part, d) then sums channel d over splits part, part + parts,
-// ... with the factors 2^(m_s - M), kMergeBatch splits per round of independent loads, and
-// the parts meet in LDS. A merge is a few rounds of load latency whatever the split count.
+// `parts` groups of dt = ceil(D/64)*64 threads. Thread (part, d) reads splits part, part +
+// parts, ... (kMergeBatch per round of independent loads, each split's (m, l) with its channel
+// d) and keeps a running (max, sum, channel sum) of its own; the parts meet in LDS. A merge is
+// one round of load latency for up to parts * kMergeBatch splits.
 constexpr uint32_t kMergeBatch = 16;
 constexpr uint32_t kMergeThreads = 1024;
 
@@ -1085,7 +1085,7 @@ __global__ void __launch_bounds__(kMergeThreads)
                  uint32_t qh, float* out, uint32_t units, uint64_t ws_sess_stride,
                  uint64_t out_sess_stride) {
   __shared__ float red[kMergeThreads];
-  const uint32_t lane = threadIdx.x % 64;
+  __shared__ float red_m[kMergeThreads / 64], red_l[kMergeThreads / 64];
   const uint32_t sess = blockIdx.x / (units * gq);
   const uint32_t unit = (blockIdx.x / gq) % units, h = blockIdx.x % gq;
   const uint32_t b = unit / heads, kvh = unit % heads;
@@ -1093,48 +1093,57 @@ __global__ void __launch_bounds__(kMergeThreads)
   const uint32_t parts = blockDim.x / dt, part = threadIdx.x / dt, dl = threadIdx.x % dt;
   const uint64_t stride = (uint64_t)gq * (D + 2);
   const float* base = ws + sess * ws_sess_stride + (uint64_t)unit * nsplit * stride + h * (D + 2);
-  float m = -INFINITY, l = 0.f;
-  for (uint32_t s = lane; s < nsplit; s += 64) {
-    const float ms = base[s * stride + D], ls = base[s * stride + D + 1];
-    // running (max, sum) of this lane's splits
-    if (ms > m) {
-      l = l * __builtin_amdgcn_exp2f(m - ms) + ls;  // m = -inf first: the factor is 0
-      m = ms;
-    } else if (ms != -INFINITY) {
-      l += ls * __builtin_amdgcn_exp2f(ms - m);
-    }
-  }
-  const float M = warp_max(m);
-  l = m == -INFINITY ? 0.f : l * __builtin_amdgcn_exp2f(m - M);
-  const float inv = 1.0f / warp_sum(l);
   float* o = out + sess * out_sess_stride + ((uint64_t)b * qh + kvh * gq + h) * D;
   for (uint32_t d0 = 0; d0 < D; d0 += dt) {
-    const uint32_t d = d0 + dl;
-    float acc = 0.f;
-    if (d < D) {
-      for (uint32_t s0 = part; s0 < nsplit; s0 += parts * kMergeBatch) {
-        float v[kMergeBatch], f[kMergeBatch];
+    const uint32_t d = d0 + dl, dr = d < D ? d : D - 1;
+    float mp = -INFINITY, lp = 0.f, acc = 0.f;  // this part's running max, sum, channel sum
+    for (uint32_t s0 = part; s0 < nsplit; s0 += parts * kMergeBatch) {
+      float v[kMergeBatch], ms[kMergeBatch], ls[kMergeBatch];
+#pragma unroll
+      for (uint32_t j = 0; j < kMergeBatch; ++j) {
+        const uint32_t s = s0 + j * parts;
+        const float* ps = base + (uint64_t)(s < nsplit ? s : 0u) * stride;
+        v[j] = ps[dr];
+        ms[j] = s < nsplit ? ps[D] : -INFINITY;
+        ls[j] = ps[D + 1];
+      }
+      float bm = mp;
+#pragma unroll
+      for (uint32_t j = 0; j < kMergeBatch; ++j) bm = fmaxf(bm, ms[j]);
+      if (bm != -INFINITY) {
+        const float r = __builtin_amdgcn_exp2f(mp - bm);  // 0 while mp is -inf
+        acc *= r;
+        lp *= r;
 #pragma unroll
         for (uint32_t j = 0; j < kMergeBatch; ++j) {
-          const uint32_t s = s0 + j * parts;
-          const float* ps = base + (uint64_t)(s < nsplit ? s : 0u) * stride;
-          const float x = ps[d], ms = ps[D];
-          f[j] = s < nsplit && ms != -INFINITY ? __builtin_amdgcn_exp2f(ms - M) : 0.f;
-          v[j] = s < nsplit ? x : 0.f;
+          const float f = ms[j] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms[j] - bm);
+          acc = fmaf(v[j], f, acc);
+          lp = fmaf(ls[j], f, lp);
         }
-#pragma unroll
-        for (uint32_t j = 0; j < kMergeBatch; ++j) acc = fmaf(v[j], f[j], acc);
+        mp = bm;
       }
     }
     if (parts > 1) {
       red[threadIdx.x] = acc;
+      if (dl == 0) {
+        red_m[part] = mp;
+        red_l[part] = lp;
+      }
       __syncthreads();
       if (part == 0) {
-        for (uint32_t q = 1; q < parts; ++q) acc += red[q * dt + dl];
+        float M = -INFINITY;
+        for (uint32_t q = 0; q < parts; ++q) M = fmaxf(M, red_m[q]);
+        acc = 0.f;
+        lp = 0.f;
+        for (uint32_t q = 0; q < parts; ++q) {
+          const float f = red_m[q] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(red_m[q] - M);
+          acc = fmaf(red[q * dt + dl], f, acc);
+          lp = fmaf(red_l[q], f, lp);
+        }
       }
       __syncthreads();
     }
-    if (part == 0 && d < D) o[d] = acc * inv;
+    if (part == 0 && d < D) o[d] = acc / lp;
   }
 }
 
