@@ -199,7 +199,20 @@ struct AttnProblem {
   // [units] split counters, zero between calls (calls sharing them must not overlap on the
   // device), or null to merge in a separate launch
   uint32_t* counters;
+  // RuntimeKv::decode in one attention launch (null pend_k otherwise): `st` and `seq` already
+  // count a decode token whose key and value rows are pend_k / pend_v ([units][D]). The merge
+  // writes them to residual slot pend_kslot and window slot pend_vslot afterwards; with
+  // pend_evict the token vq-1 left the window from slot pend_vslot and is quantized by the
+  // attention launch. Needs the packed-chunk path (attention_fuses_decode).
+  const float* pend_k;
+  const float* pend_v;
+  uint32_t pend_kslot, pend_vslot;
+  uint32_t pend_evict;
 };
+
+// Whether launch_attention takes the packed-chunk path for p (the one that can carry a decode
+// token appended in the same launch).
+bool attention_fuses_decode(const AttnProblem& p);
 
 // Workspace floats the attention needs for `p` (split-K partials).
 size_t attention_workspace_floats(const AttnProblem& p);

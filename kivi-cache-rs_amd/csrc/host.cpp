@@ -757,6 +757,73 @@ Status cache_attention(const kivi_cache* c, const float* query, size_t query_len
   return sync(s, "attention");
 }
 
+// RuntimeKv::decode on device pointers in one attention launch plus its merge: the attention
+// reads the new token's rows from the inputs, quantizes the token the window evicts, and the
+// merge writes the rows to the residual and the window (src/runtime.rs:46-56 = append(key,
+// value, 1) then attention, bit for bit). Taken when both calls' checks pass, no key flush is
+// due and the attention runs on the packed-chunk path; *fused is false otherwise (nothing
+// done), and the caller appends and attends in two calls.
+Status decode_fused(kivi_cache* c, const float* key, size_t key_len, const float* value,
+                    size_t value_len, const float* query, size_t query_len, size_t num_q_heads,
+                    float scale, float* out, size_t out_len, hipStream_t s, bool* fused) {
+  *fused = false;
+  if (c == nullptr) return Status{};
+  CacheCore& core = c->core;
+  size_t expected;
+  if (!mul4(core.batch, core.heads, 1, core.head_dim, &expected).ok() || key_len != expected ||
+      value_len != expected || key == nullptr || value == nullptr)
+    return Status{};
+  if (!check_attention(core.batch, core.heads, core.head_dim, query_len, num_q_heads, out_len).ok() ||
+      query == nullptr || out == nullptr)
+    return Status{};
+  std::lock_guard<std::mutex> lock(c->mu);
+  const uint32_t R = static_cast<uint32_t>(core.cfg.residual_length);
+  if (core.kres_len + 1 >= R || core.vres_len > R) return Status{};  // a key flush is due
+  const bool evict = core.vres_len == R;
+  AttnProblem p{};
+  p.cache = core.view();
+  p.st = core.state();
+  p.st.kres += 1;
+  if (evict) {
+    p.st.vq += 1;
+    p.st.vhead = (p.st.vhead + 1) % R;
+  } else {
+    p.st.vres += 1;
+  }
+  p.seq = core.seq + 1;
+  p.query = query;
+  p.out = out;
+  p.qh = static_cast<uint32_t>(num_q_heads);
+  p.heads = static_cast<uint32_t>(core.heads);
+  p.batch = static_cast<uint32_t>(core.batch);
+  p.scale = scale;
+  p.counters = c->attn.counters.as<uint32_t>();
+  p.pend_k = key;
+  p.pend_v = value;
+  p.pend_kslot = core.kres_len;
+  p.pend_vslot = evict ? core.vhead : (core.vhead + core.vres_len) % R;
+  p.pend_evict = evict ? 1u : 0u;
+  if (!attention_fuses_decode(p)) return Status{};
+  DeviceScope scope(core.device);
+  KIVI_TRY(core.ensure_capacity(p.st.vq, s));
+  p.cache = core.view();  // capacity growth moves the arrays
+  std::lock_guard<std::mutex> alock(c->attn.mu);
+  KIVI_TRY(c->attn.reserve(attention_workspace_floats(p) * sizeof(float)));
+  KIVI_TRY(c->attn.before(s));
+  HIP_TRY(launch_attention(p, c->attn.workspace.as<float>(), s), "decode attention");
+  KIVI_TRY(c->attn.after(s));
+  core.kres_len += 1;
+  if (evict) {
+    core.vq += 1;
+    core.vhead = p.st.vhead;
+  } else {
+    core.vres_len += 1;
+  }
+  core.seq += 1;
+  *fused = true;
+  return Status{};
+}
+
 Status session_attend(const kivi_session* se, const float* query, size_t query_len,
                       size_t num_q_heads, float scale, float* out, size_t out_len, bool device,
                       hipStream_t stream) {
@@ -1368,6 +1435,12 @@ kivi_status kivi_runtime_decode_device(kivi_runtime* rt, const float* key, size_
                                        size_t query_len, size_t num_q_heads, float scale,
                                        float* out, size_t out_len, void* stream,
                                        kivi_error* err) {
+  bool fused = false;
+  const kivi_status fs = guarded(err, [&] {
+    return decode_fused(rt ? &rt->cache : nullptr, key, key_len, value, value_len, query, query_len,
+                        num_q_heads, scale, out, out_len, static_cast<hipStream_t>(stream), &fused);
+  });
+  if (fs != KIVI_OK || fused) return fs;
   kivi_status st = kivi_cache_append_device(rt ? &rt->cache : nullptr, key, key_len, value,
                                             value_len, 1, stream, err);
   if (st != KIVI_OK) return st;

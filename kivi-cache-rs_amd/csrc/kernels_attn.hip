@@ -75,6 +75,16 @@ struct AttnArgs {
   uint32_t* counters;      // [units] finished splits (0 between calls), or null: separate merge
   float* out;              // [batch][QH][D]
   uint32_t units;
+  // A decode token appended by this launch (RuntimeKv::decode in one launch; null otherwise):
+  // the state above already counts it. Token seq-1's key and value rows are read from pend_k /
+  // pend_v ([units][D]) instead of the residual and the window (the merge launch writes them
+  // there afterwards); with pend_evict, token vq-1 left the window: its row is still in ring
+  // slot pend_vslot, and the workgroup whose chunk holds it quantizes it, writes its codes and
+  // (scale, zero), and uses them in place of the packed data not yet in memory.
+  const float* pend_k;
+  const float* pend_v;
+  uint32_t pend_vslot;
+  uint32_t pend_evict;
 };
 
 // Key / value element (token t, channel d) of one unit, wherever it lives. BITS, DD, GG are
@@ -642,6 +652,7 @@ __device__ __forceinline__ const float* key_row(const AttnArgs& a, uint32_t unit
   const uint32_t D = a.c.geo.D;
   if (t >= a.seq && t < a.total && a.suffix_k != nullptr)
     return a.suffix_k + unit * a.suffix_stride + (t - a.seq) * D;
+  if (a.pend_k != nullptr && t + 1 == a.seq) return a.pend_k + (uint64_t)unit * D;
   const uint64_t r = t >= a.st.kq && t < a.seq ? t - a.st.kq : 0;
   return a.c.kres + ((uint64_t)unit * a.c.geo.R + r) * D;
 }
@@ -649,6 +660,7 @@ __device__ __forceinline__ const float* value_row(const AttnArgs& a, uint32_t un
   const uint32_t D = a.c.geo.D, R = a.c.geo.R;
   if (t >= a.seq && t < a.total && a.suffix_v != nullptr)
     return a.suffix_v + unit * a.suffix_stride + (t - a.seq) * D;
+  if (a.pend_v != nullptr && t + 1 == a.seq) return a.pend_v + (uint64_t)unit * D;
   uint32_t slot = a.st.vhead + (t >= a.st.vq && t < a.seq ? static_cast<uint32_t>(t - a.st.vq) : 0u);
   if (slot >= R) slot -= R;
   return a.c.vring + ((uint64_t)unit * R + slot) * D;
@@ -750,6 +762,45 @@ __device__ __forceinline__ void value_fp32(const AttnArgs& a, uint64_t t0, uint3
     }
 }
 
+// The value row evicted by a decode token appended in the same launch (pend_evict): lane
+// holds channels lane and 64+lane, and (min, scale) of their 32-channel groups lc and lc+2,
+// computed as the value quantizer does (src/quant.rs:349-375, 453-472).
+struct EvictRow {
+  float x[2], mn[2], sc[2];
+};
+__device__ __forceinline__ uint32_t evict_code(float x, float zero, float scale, float levels) {
+  if (scale == 0.0f) return 0u;
+  float r = rintf((x - zero) / scale);
+  if (r < 0.0f) {
+    r = 0.0f;
+  } else if (r > levels) {
+    r = levels;
+  }
+  return static_cast<uint32_t>(r);
+}
+// Group min / max over the 32 lanes of each half-wave; returns the row's largest scale and
+// largest |x| (whole wave).
+__device__ __forceinline__ void evict_groups(EvictRow& e, float levels, float& smax, float& amax) {
+  smax = 0.f;
+  amax = 0.f;
+#pragma unroll
+  for (int hv = 0; hv < 2; ++hv) {
+    float mn = e.x[hv], mx = e.x[hv];
+#pragma unroll
+    for (int o = 1; o < 32; o <<= 1) {
+      mn = fminf(mn, __shfl_xor(mn, o));
+      mx = fmaxf(mx, __shfl_xor(mx, o));
+    }
+    const float span = mx - mn;
+    e.mn[hv] = mn;
+    e.sc[hv] = span == 0.0f ? 0.0f : span / levels;
+    smax = fmaxf(smax, e.sc[hv]);
+    amax = fmaxf(amax, fmaxf(fabsf(mn), fabsf(mx)));
+  }
+  smax = fmaxf(smax, __shfl_xor(smax, 32));
+  amax = fmaxf(amax, __shfl_xor(amax, 32));
+}
+
 // One workgroup = 4 waves; wave w of split s owns packed chunks [s*4*CPW + w*CPW, +CPW) of its
 // unit (chunks whose 64 keys and 64 values are all packed). D = 128, G = 32. Per chunk the
 // operands are prepared from the (scale, zero) registers first, then the next chunk's data
@@ -797,6 +848,14 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
     load_key_words<BITS>(a, unit, k0, lane, kw0);
   }
 
+  // a decode token appended by this launch evicts token vq-1 from the window: its row
+  EvictRow er{};
+  if (a.pend_evict) {
+    const float* row = a.c.vring + ((uint64_t)unit * a.c.geo.R + a.pend_vslot) * D;
+    er.x[0] = row[lane];
+    er.x[1] = row[lane + 64];
+  }
+
   // q in base-2 logit units for the lane's head, channels 16*la .. +15 (0 for padded heads).
   float qv[NRS][16];
   float qmax = 0.f;
@@ -820,7 +879,13 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
   // operand |w * scale| * 2^ev (w <= 1) stays below 2^15, from the unit's largest scales.
   qmax = warp_max(qmax);
   const float kmax = __uint_as_float(a.c.smax[4 * unit]);
-  const float vmax = __uint_as_float(a.c.smax[4 * unit + 1]);
+  float vmax = __uint_as_float(a.c.smax[4 * unit + 1]);
+  constexpr float kLevels = static_cast<float>((1 << BITS) - 1);
+  float ev_scale = 0.f, ev_amax = 0.f;  // the evicted row's largest scale and |x|
+  if (a.pend_evict) {
+    evict_groups(er, kLevels, ev_scale, ev_amax);
+    vmax = fmaxf(vmax, ev_scale);  // the maximum its quantization raises (as the append would)
+  }
   const int ek = std::min(60, std::max(-100, 15 - __builtin_amdgcn_frexp_expf(qmax * kmax)));
   const int ev = std::min(60, std::max(-100, 15 - __builtin_amdgcn_frexp_expf(vmax)));
   constexpr int kExp = CodeUnit<BITS>::kExp;
@@ -914,9 +979,45 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
     ValueParams vp;
     ValueWords<BITS> vw0, vw1;
     ValueA<NRS> A;
-    auto step = [&](int k, const ValueWords<BITS>& cur, ValueWords<BITS>& next) {
+    auto step = [&](int k, ValueWords<BITS>& cur, ValueWords<BITS>& next) {
       const uint64_t t0 = (uint64_t)chunk_of(k) * 64;
       const bool packed = !MIXED || t0 < vq;
+      if (a.pend_evict && t0 + 64 >= vq && t0 < vq) {
+        // the evicted token vq-1 is in this chunk: its codes and (scale, zero) join the chunk's
+        // registers and go to memory (the only reader of those words this launch is here)
+        constexpr int PPW = 32 / BITS, VW = 64 * BITS / 32;
+        const uint32_t tt = static_cast<uint32_t>(vq - 1 - t0);
+        const uint32_t sh = code_shift(BITS, tt % PPW);
+        const uint32_t tb = static_cast<uint32_t>(t0 / 64);
+#pragma unroll
+        for (int hv = 0; hv < 2; ++hv) {
+          const uint32_t code = evict_code(er.x[hv], er.mn[hv], er.sc[hv], kLevels) << sh;
+#pragma unroll
+          for (int qq = 0; qq < VW; ++qq)
+            if (qq == (int)(tt / PPW)) {
+              cur.w[hv][qq] |= code;
+              a.c.vcodes[unit * a.c.geo.vcodes_unit() + ((uint64_t)tb * 128 + lane + 64 * hv) * VW + qq] =
+                  cur.w[hv][qq];
+            }
+          const uint32_t mine = 8 * la + 2 * li;  // the lane's (scale, zero) tokens: mine, mine+1
+          if (mine == tt || mine + 1 == tt) {
+            if (mine == tt) {
+              vp.sz[hv].x = er.sc[hv];
+              vp.sz[hv].y = er.mn[hv];
+            } else {
+              vp.sz[hv].z = er.sc[hv];
+              vp.sz[hv].w = er.mn[hv];
+            }
+            *reinterpret_cast<float2*>(a.c.vparams + unit * a.c.geo.vparams_unit() +
+                                       (((uint64_t)tb * 4 + lc + 2 * hv) * 64 + tt) * 2) =
+                make_float2(er.sc[hv], er.mn[hv]);
+          }
+        }
+        if (lane == 0) {
+          atomicMax(a.c.smax + 4 * unit + 1, __float_as_uint(ev_scale));
+          atomicMax(a.c.smax + 4 * unit + 3, __float_as_uint(ev_amax));
+        }
+      }
       float w[NRS][8];
 #pragma unroll
       for (int rs = 0; rs < NRS; ++rs) {
@@ -1080,10 +1181,20 @@ __global__ void __launch_bounds__(kThreads) k_attn_sessions(AttnArgs a, SessionT
 constexpr uint32_t kMergeBatch = 16;
 constexpr uint32_t kMergeThreads = 1024;
 
+// Rows of a decode token the attention launch consumed from its inputs, written to the key
+// residual and the value window once that launch is over (null k: nothing to write).
+struct PendRows {
+  const float* k;
+  const float* v;
+  float* kres;
+  float* vring;
+  uint32_t kslot, vslot, R;
+};
+
 __global__ void __launch_bounds__(kMergeThreads)
     k_attn_merge(const float* ws, uint32_t nsplit, uint32_t gq, uint32_t D, uint32_t heads,
                  uint32_t qh, float* out, uint32_t units, uint64_t ws_sess_stride,
-                 uint64_t out_sess_stride) {
+                 uint64_t out_sess_stride, PendRows pend) {
   __shared__ float red[kMergeThreads];
   __shared__ float red_m[kMergeThreads / 64], red_l[kMergeThreads / 64];
   const uint32_t sess = blockIdx.x / (units * gq);
@@ -1094,6 +1205,12 @@ __global__ void __launch_bounds__(kMergeThreads)
   const uint64_t stride = (uint64_t)gq * (D + 2);
   const float* base = ws + sess * ws_sess_stride + (uint64_t)unit * nsplit * stride + h * (D + 2);
   float* o = out + sess * out_sess_stride + ((uint64_t)b * qh + kvh * gq + h) * D;
+  if (pend.k != nullptr && sess == 0 && h == 0) {
+    for (uint32_t d = threadIdx.x; d < D; d += blockDim.x) {
+      pend.kres[((uint64_t)unit * pend.R + pend.kslot) * D + d] = pend.k[(uint64_t)unit * D + d];
+      pend.vring[((uint64_t)unit * pend.R + pend.vslot) * D + d] = pend.v[(uint64_t)unit * D + d];
+    }
+  }
   for (uint32_t d0 = 0; d0 < D; d0 += dt) {
     const uint32_t d = d0 + dl, dr = d < D ? d : D - 1;
     float mp = -INFINITY, lp = 0.f, acc = 0.f;  // this part's running max, sum, channel sum
@@ -1151,11 +1268,12 @@ __global__ void __launch_bounds__(kMergeThreads)
 // about kMergeBatch splits.
 hipError_t launch_merge(const float* ws, uint32_t nsplit, uint32_t gq, uint32_t D, uint32_t heads,
                         uint32_t qh, float* out, uint32_t units, uint32_t count,
-                        uint64_t ws_sess_stride, uint64_t out_sess_stride, hipStream_t stream) {
+                        uint64_t ws_sess_stride, uint64_t out_sess_stride, hipStream_t stream,
+                        PendRows pend = PendRows{}) {
   const uint32_t dt = std::min(kMergeThreads, (D + 63) / 64 * 64);
   const uint32_t parts = std::max(1u, std::min(kMergeThreads / dt, (nsplit + kMergeBatch - 1) / kMergeBatch));
   k_attn_merge<<<count * units * gq, parts * dt, 0, stream>>>(ws, nsplit, gq, D, heads, qh, out, units,
-                                                              ws_sess_stride, out_sess_stride);
+                                                              ws_sess_stride, out_sess_stride, pend);
   return hipGetLastError();
 }
 
@@ -1703,6 +1821,10 @@ AttnArgs make_args(const AttnProblem& p, float* ws) {
   AttnArgs a{};
   a.c = p.cache;
   a.st = p.st;
+  a.pend_k = p.pend_k;
+  a.pend_v = p.pend_v;
+  a.pend_vslot = p.pend_vslot;
+  a.pend_evict = p.pend_k != nullptr ? p.pend_evict : 0u;
   a.seq = p.seq;
   a.L = p.suffix_len;
   a.total = p.seq + p.suffix_len;
@@ -1785,6 +1907,12 @@ hipError_t dispatch_generic(const AttnArgs& a, hipStream_t stream) {
 
 }  // namespace
 
+bool attention_fuses_decode(const AttnProblem& p) {
+  if (kUseInKernelMerge != 0) return false;  // the merge launch writes the token's rows
+  const AttnArgs a = make_args(p, nullptr);
+  return a.total > 0 && a.nsplit_gen == 0 && (a.nsplit_fast > 0 || a.nsplit_win > 0);
+}
+
 size_t attention_workspace_floats(const AttnProblem& p) {
   const AttnArgs a = make_args(p, nullptr);
   return (size_t)p.cache.geo.units * a.nsplit_total * a.gq * (p.cache.geo.D + 2);
@@ -1820,8 +1948,11 @@ hipError_t launch_attention(const AttnProblem& p, float* workspace, hipStream_t 
   if (a.counters == nullptr) {
     const double bytes = (double)units * a.gq * ((double)a.nsplit_total * (g.D + 2) + g.D) * 4.0;
     TimedLaunch timed(KIVI_KERNEL_ATTN_MERGE, stream, bytes);
+    PendRows pend{};
+    if (p.pend_k != nullptr)
+      pend = PendRows{p.pend_k, p.pend_v, p.cache.kres, p.cache.vring, p.pend_kslot, p.pend_vslot, g.R};
     return launch_merge(workspace, a.nsplit_total, a.gq, g.D, p.heads, p.qh, p.out, units, 1, 0, 0,
-                        stream);
+                        stream, pend);
   }
   return hipGetLastError();
 }

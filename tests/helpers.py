@@ -59,3 +59,43 @@ def max_abs(a, b):
     a = np.asarray(a, np.float64)
     b = np.asarray(b, np.float64)
     return float(np.max(np.abs(a - b))) if a.size else 0.0
+
+
+class DeviceArrays:
+    """Device buffers for the ``*_device`` entry points, through the same HIP runtime the
+    library links (/opt/rocm/lib/libamdhip64.so.7), so the test process holds one runtime."""
+
+    def __init__(self):
+        import ctypes as C
+        self._C = C
+        self._hip = C.CDLL("libamdhip64.so.7")
+        self._ptrs = []
+
+    def _ok(self, rc, what):
+        assert rc == 0, f"{what}: hipError {rc}"
+
+    def upload(self, host):
+        C = self._C
+        host = np.ascontiguousarray(host, dtype=np.float32)
+        p = C.c_void_p()
+        self._ok(self._hip.hipMalloc(C.byref(p), C.c_size_t(max(host.nbytes, 4))), "hipMalloc")
+        self._ptrs.append(p)
+        self._ok(self._hip.hipMemcpy(p, host.ctypes.data_as(C.c_void_p), C.c_size_t(host.nbytes), 1),
+                 "hipMemcpy H2D")
+        return p.value
+
+    def empty(self, n):
+        return self.upload(np.zeros(n, np.float32))
+
+    def download(self, ptr, n):
+        C = self._C
+        out = np.empty(n, np.float32)
+        self._ok(self._hip.hipDeviceSynchronize(), "hipDeviceSynchronize")
+        self._ok(self._hip.hipMemcpy(out.ctypes.data_as(C.c_void_p), C.c_void_p(ptr), C.c_size_t(out.nbytes), 2),
+                 "hipMemcpy D2H")
+        return out
+
+    def free(self):
+        for p in self._ptrs:
+            self._hip.hipFree(p)
+        self._ptrs = []

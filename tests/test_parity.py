@@ -13,7 +13,7 @@ import pytest
 
 import kivi
 from kivi import KiviCache, KiviConfig, RuntimeKv
-from helpers import dense_attend, fill, max_abs
+from helpers import DeviceArrays, dense_attend, fill, max_abs
 
 pytestmark = pytest.mark.gpu
 
@@ -306,3 +306,43 @@ def test_runtime_decode_parity(amd, oracle):
         q = rng.standard_normal(qh * dim).astype(np.float32)
         assert_close(ra.decode(kk, vv, q, qh, scale), ro.decode(kk, vv, q, qh, scale), f"step {step}")
     assert_streams_equal(ra.cache(), ro.cache())
+
+
+@pytest.mark.parametrize("bits,residual,gqa", [(2, 64, 4), (4, 64, 8), (8, 128, 4), (2, 128, 1)])
+def test_runtime_decode_device_parity(amd, oracle, bits, residual, gqa):
+    """RuntimeKv::decode on device pointers, which runs append + attention in one attention
+    launch (the token the window evicts quantized inside it) except when a key flush is due:
+    bit for bit equal to a cache taking append_device then attention_device (tests/runtime.rs:
+    13-52), and within tolerance of the oracle's decode, streams bit-exact, across evictions
+    and flushes."""
+    heads, dim, prefill, steps = 2, 128, 3 * residual + 17, 2 * residual + 5
+    qh = heads * gqa
+    cfg = KiviConfig(bits, 32, residual)
+    rng = np.random.default_rng(300 + bits + residual + gqa)
+    k = rng.standard_normal(heads * prefill * dim).astype(np.float32)
+    v = rng.standard_normal(heads * prefill * dim).astype(np.float32)
+    k.reshape(heads, prefill, dim)[:, :, 5] *= 10
+    ra, ro = RuntimeKv(amd, cfg, 1, heads, dim), RuntimeKv(oracle, cfg, 1, heads, dim)
+    cb = KiviCache(amd, cfg, 1, heads, dim)
+    for target in (ra.cache(), ro.cache(), cb):
+        target.append(k, v, prefill)
+    scale = np.float32(1 / np.sqrt(dim))
+    mem = DeviceArrays()
+    n_kv, n_q = heads * dim, qh * dim
+    out_a, out_b = mem.empty(n_q), mem.empty(n_q)
+    for step in range(steps):
+        kk = rng.standard_normal(n_kv).astype(np.float32)
+        vv = rng.standard_normal(n_kv).astype(np.float32)
+        q = rng.standard_normal(n_q).astype(np.float32)
+        dk, dv, dq = mem.upload(kk), mem.upload(vv), mem.upload(q)
+        ra.decode_device(dk, n_kv, dv, n_kv, dq, n_q, qh, scale, out_a, n_q)
+        cb.append_device(dk, n_kv, dv, n_kv, 1)
+        cb.attention_device(dq, n_q, qh, scale, out_b, n_q)
+        got = mem.download(out_a, n_q)
+        assert np.array_equal(got.view(np.uint32), mem.download(out_b, n_q).view(np.uint32)), f"step {step}"
+        assert_close(got, ro.decode(kk, vv, q, qh, scale), f"step {step}")
+        if step % 16 == 0 or step == steps - 1:
+            assert_same_state(ra.cache(), ro.cache())
+            assert_streams_equal(ra.cache(), ro.cache())
+            assert_streams_equal(cb, ro.cache())
+    mem.free()
