@@ -288,6 +288,58 @@ kivi_status kivi_runtime_decode_device(kivi_runtime* rt, const float* key, size_
                                        float* out, size_t out_len, void* stream,
                                        kivi_error* err);
 
+/* ---------------------------------------------------------------- QualityGuard */
+/* QualityGuard (src/guard.rs:37-258): a cache plus the fp32 tape of every appended token;
+   after each key flush the guard scores cache attention against fp32 attention over the tape
+   (cosine) and, below the threshold, rebuilds the cache from the tape with wider codes or a
+   longer residual window. */
+typedef struct kivi_guard kivi_guard;
+
+/* QualityPolicy (src/guard.rs:13-19). */
+enum { KIVI_POLICY_RAISE_BITS = 0, KIVI_POLICY_LENGTHEN_RESIDUAL = 1 };
+
+/* QualityUpgrade (src/guard.rs:22-26): kind 0 = Bits{from, to}, 1 = Residual{from, to}. */
+typedef struct kivi_quality_upgrade {
+  uint32_t kind;
+  size_t from;
+  size_t to;
+} kivi_quality_upgrade;
+
+#define KIVI_MAX_UPGRADES 64
+/* FlushCheck (src/guard.rs:29-35); upgrades[0 .. num_upgrades). */
+typedef struct kivi_flush_check {
+  size_t sequence_tokens;
+  float cosine_before;
+  float cosine;
+  size_t num_upgrades;
+  kivi_quality_upgrade upgrades[KIVI_MAX_UPGRADES];
+} kivi_flush_check;
+
+/* QualityGuard::try_new (src/guard.rs:51-73). */
+kivi_status kivi_guard_new(const kivi_config* config, size_t batch, size_t num_kv_heads,
+                           size_t head_dim, float threshold, uint32_t policy, uint8_t max_bits,
+                           size_t max_residual, kivi_guard** out, kivi_error* err);
+void kivi_guard_free(kivi_guard* guard);
+/* config / cache / policy / sequence_length (src/guard.rs:75-88); the cache is borrowed and
+   replaced by a rebuild. */
+kivi_config kivi_guard_config(const kivi_guard* guard);
+kivi_cache* kivi_guard_cache(kivi_guard* guard);
+uint32_t kivi_guard_policy(const kivi_guard* guard);
+size_t kivi_guard_sequence_length(const kivi_guard* guard);
+/* QualityGuard::append (src/guard.rs:90-146), checked in the reference order (keys, values,
+   query heads, query). One check per key flush inside the append: *num_checks gets their
+   count and checks[0 .. min(count, checks_cap)) the first of them (checks may be NULL when
+   checks_cap is 0). The guard keeps every check of its last append until the next one. */
+kivi_status kivi_guard_append(kivi_guard* guard, const float* keys, size_t keys_len,
+                              const float* values, size_t values_len, size_t seq_len,
+                              const float* query, size_t query_len, size_t num_q_heads,
+                              float scale, kivi_flush_check* checks, size_t checks_cap,
+                              size_t* num_checks, kivi_error* err);
+/* Checks [first, first + cap) of the last append (fewer at its end) into `checks`; returns
+   how many were written. No counterpart in the reference, whose append returns a Vec. */
+size_t kivi_guard_last_checks(const kivi_guard* guard, size_t first, kivi_flush_check* checks,
+                              size_t cap);
+
 /* ---------------------------------------------------------------- standalone codec */
 
 typedef struct kivi_quantized kivi_quantized;

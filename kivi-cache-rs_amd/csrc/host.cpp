@@ -591,21 +591,24 @@ struct AttnSync {
 };
 
 // Attention over `core` plus an optional device suffix, writing `out` on the device.
+// With `tape_only` the cache's tokens are left out: attention over the suffix rows alone
+// (the QualityGuard's fp32 attention over its tape).
 Status attend(const CacheCore& core, AttnSync& sync, const float* suffix_k, const float* suffix_v,
               uint64_t L, uint64_t suffix_stride, const float* query, size_t qh, float scale,
-              float* out, hipStream_t s) {
+              float* out, hipStream_t s, bool tape_only = false) {
   const size_t gq = qh / core.heads;
   if (gq * core.head_dim > kMaxGqD)
     return Err(KIVI_ERR_UNSUPPORTED, gq * core.head_dim, kMaxGqD, "(num_q_heads/num_kv_heads)*head_dim");
   const size_t out_n = core.batch * qh * core.head_dim;
-  if (core.seq + L == 0) {
+  const uint64_t seq = tape_only ? 0 : core.seq;
+  if (seq + L == 0) {
     HIP_TRY(hipMemsetAsync(out, 0, out_n * sizeof(float), s), "attention zero output");
     return Status{};
   }
   AttnProblem p{};
   p.cache = core.view();
-  p.st = core.state();
-  p.seq = core.seq;
+  p.st = tape_only ? SeqState{} : core.state();
+  p.seq = seq;
   p.suffix_k = suffix_k;
   p.suffix_v = suffix_v;
   p.suffix_len = L;
@@ -1068,6 +1071,143 @@ Status quantized_read(const kivi_quantized* q, void* out, size_t out_len, size_t
 }  // namespace
 
 // ================================================================= C ABI
+// ---------------------------------------------------------------- QualityGuard
+
+// QualityGuard (src/guard.rs:37-258): the resident cache plus the fp32 tape of every appended
+// token, here on the device ([units][cap][D], grown by doubling) so the fp32 attention it is
+// scored against runs on the attention kernels (tape rows as the suffix of an empty cache).
+struct kivi_guard {
+  kivi_cache* cache = nullptr;
+  DevBuf tk, tv;
+  size_t cap = 0, seq = 0;
+  float threshold = 0.f;
+  uint32_t policy = KIVI_POLICY_RAISE_BITS;
+  uint8_t max_bits = 8;
+  size_t max_residual = 0;
+  AttnSync dense;  // split partials of the fp32 attention
+  std::vector<kivi_flush_check> last;  // checks of the last append
+  std::mutex mu;
+};
+
+namespace {
+
+// next_bits / next_residual (src/guard.rs:261-289).
+bool guard_next_bits(uint8_t current, uint8_t max_bits, uint8_t* next) {
+  const uint8_t n = current == 2 ? 4 : current == 4 ? 8 : 0;
+  if (n == 0 || n > max_bits) return false;
+  *next = n;
+  return true;
+}
+bool guard_next_residual(size_t current, size_t group, size_t max_residual, size_t* next) {
+  if (current >= max_residual) return false;
+  const size_t doubled = current > SIZE_MAX / 2 ? SIZE_MAX : current * 2;
+  const size_t n = doubled <= max_residual ? doubled : max_residual;
+  if (!(n > current && n % group == 0)) return false;
+  *next = n;
+  return true;
+}
+
+// cosine_sim (src/guard.rs:362-377), sequential f32 sums as the reference.
+float guard_cosine(const std::vector<float>& a, const std::vector<float>& b) {
+  float dot = 0.f, na = 0.f, nb = 0.f;
+  for (size_t i = 0; i < a.size() && i < b.size(); ++i) {
+    dot += a[i] * b[i];
+    na += a[i] * a[i];
+    nb += b[i] * b[i];
+  }
+  const float denom = std::sqrt(na) * std::sqrt(nb);
+  return denom == 0.f ? 1.f : dot / denom;
+}
+
+// push_history (src/guard.rs:237-245): `n` tokens of [units][n][D] host rows onto the tape.
+Status guard_push(kivi_guard* g, const float* keys, const float* values, size_t n, hipStream_t s) {
+  const CacheCore& core = g->cache->core;
+  const size_t units = core.units(), D = core.head_dim;
+  if (g->seq + n > g->cap) {
+    const size_t cap = std::max({g->cap * 2, g->seq + n, static_cast<size_t>(64)});
+    DevBuf nk, nv;
+    KIVI_TRY(nk.alloc_zero(units * cap * D * sizeof(float), s, "guard tape"));
+    KIVI_TRY(nv.alloc_zero(units * cap * D * sizeof(float), s, "guard tape"));
+    if (g->seq > 0) {
+      HIP_TRY(copy_units(nk.p, cap * D * 4, g->tk.p, g->cap * D * 4, g->seq * D * 4,
+                         static_cast<uint32_t>(units), s), "guard tape");
+      HIP_TRY(copy_units(nv.p, cap * D * 4, g->tv.p, g->cap * D * 4, g->seq * D * 4,
+                         static_cast<uint32_t>(units), s), "guard tape");
+    }
+    std::swap(g->tk.p, nk.p);
+    std::swap(g->tk.bytes, nk.bytes);
+    std::swap(g->tv.p, nv.p);
+    std::swap(g->tv.bytes, nv.bytes);
+    g->cap = cap;
+  }
+  HIP_TRY(hipMemcpy2DAsync(g->tk.as<float>() + g->seq * D, g->cap * D * 4, keys, n * D * 4, n * D * 4,
+                           units, hipMemcpyHostToDevice, s), "guard tape");
+  HIP_TRY(hipMemcpy2DAsync(g->tv.as<float>() + g->seq * D, g->cap * D * 4, values, n * D * 4,
+                           n * D * 4, units, hipMemcpyHostToDevice, s), "guard tape");
+  g->seq += n;
+  return sync(s, "guard tape");
+}
+
+// QualityGuard::cosine (src/guard.rs:218-235): cache attention against fp32 attention over
+// the tape, both on the device, compared on the host.
+Status guard_cosine_of(kivi_guard* g, const float* query, size_t query_len, size_t qh, float scale,
+                       float* cosine) {
+  kivi_cache* c = g->cache;
+  const CacheCore& core = c->core;
+  hipStream_t s = core.stream;
+  const size_t n = core.batch * qh * core.head_dim;
+  Scratch dq, dgot, dexp;
+  KIVI_TRY(dq.get(query_len * 4, s, "guard staging"));
+  KIVI_TRY(dgot.get(n * 4, s, "guard staging"));
+  KIVI_TRY(dexp.get(n * 4, s, "guard staging"));
+  HIP_TRY(hipMemcpyAsync(dq.p, query, query_len * 4, hipMemcpyHostToDevice, s), "guard H2D");
+  KIVI_TRY(attend(core, c->attn, nullptr, nullptr, 0, 0, dq.as<float>(), qh, scale,
+                  dgot.as<float>(), s));
+  KIVI_TRY(attend(core, g->dense, g->tk.as<float>(), g->tv.as<float>(), g->seq, g->cap * core.head_dim,
+                  dq.as<float>(), qh, scale, dexp.as<float>(), s, true));
+  std::vector<float> got(n), expect(n);
+  HIP_TRY(hipMemcpyAsync(got.data(), dgot.p, n * 4, hipMemcpyDeviceToHost, s), "guard D2H");
+  HIP_TRY(hipMemcpyAsync(expect.data(), dexp.p, n * 4, hipMemcpyDeviceToHost, s), "guard D2H");
+  KIVI_TRY(sync(s, "guard attention"));
+  *cosine = guard_cosine(got, expect);
+  return Status{};
+}
+
+// QualityGuard::apply (src/guard.rs:195-216): a new cache of the upgraded config holding the
+// whole tape.
+Status guard_apply(kivi_guard* g, const kivi_quality_upgrade& up) {
+  kivi_config cfg = g->cache->core.cfg;
+  if (up.kind == 0) {
+    cfg.bits = static_cast<uint8_t>(up.to);
+  } else {
+    cfg.residual_length = up.to;
+  }
+  KIVI_TRY(check_config(cfg));
+  const CacheCore& old = g->cache->core;
+  auto nc = std::make_unique<kivi_cache>();
+  KIVI_TRY(create_cache(&cfg, old.batch, old.heads, old.head_dim, nc.get()));
+  nc->core.stream = old.stream;
+  if (g->seq > 0) {
+    hipStream_t s = old.stream;
+    const size_t units = old.units(), D = old.head_dim;
+    Scratch k, v;
+    KIVI_TRY(k.get(units * g->seq * D * 4, s, "guard rebuild"));
+    KIVI_TRY(v.get(units * g->seq * D * 4, s, "guard rebuild"));
+    HIP_TRY(copy_units(k.p, g->seq * D * 4, g->tk.p, g->cap * D * 4, g->seq * D * 4,
+                       static_cast<uint32_t>(units), s), "guard rebuild");
+    HIP_TRY(copy_units(v.p, g->seq * D * 4, g->tv.p, g->cap * D * 4, g->seq * D * 4,
+                       static_cast<uint32_t>(units), s), "guard rebuild");
+    KIVI_TRY(nc->core.append_rows(k.as<float>(), v.as<float>(), g->seq, s));
+    KIVI_TRY(sync(s, "guard rebuild"));
+  }
+  kivi_cache* prev = g->cache;
+  g->cache = nc.release();
+  kivi_cache_free(prev);
+  return Status{};
+}
+
+}  // namespace
+
 extern "C" {
 
 void kivi_config_default(kivi_config* out) {
@@ -1446,6 +1586,131 @@ kivi_status kivi_runtime_decode_device(kivi_runtime* rt, const float* key, size_
   if (st != KIVI_OK) return st;
   return kivi_cache_attention_device(&rt->cache, query, query_len, num_q_heads, scale, out,
                                      out_len, stream, err);
+}
+
+kivi_status kivi_guard_new(const kivi_config* config, size_t batch, size_t num_kv_heads,
+                           size_t head_dim, float threshold, uint32_t policy, uint8_t max_bits,
+                           size_t max_residual, kivi_guard** out, kivi_error* err) {
+  return guarded(err, [&] {
+    if (policy != KIVI_POLICY_RAISE_BITS && policy != KIVI_POLICY_LENGTHEN_RESIDUAL)
+      return Err(KIVI_ERR_UNSUPPORTED, policy, 1, "policy");
+    auto g = std::make_unique<kivi_guard>();
+    auto c = std::make_unique<kivi_cache>();
+    KIVI_TRY(create_cache(config, batch, num_kv_heads, head_dim, c.get()));
+    KIVI_TRY(g->dense.init(c->core.units(), nullptr));
+    KIVI_TRY(need(out, "out"));
+    g->cache = c.release();
+    g->threshold = threshold;
+    g->policy = policy;
+    g->max_bits = max_bits;
+    g->max_residual = max_residual;
+    *out = g.release();
+    return Status{};
+  });
+}
+
+void kivi_guard_free(kivi_guard* guard) {
+  if (guard == nullptr) return;
+  {
+    DeviceScope scope(guard->cache->core.device);
+    (void)hipStreamSynchronize(guard->cache->core.stream);
+    (void)guard->dense.drain();
+  }
+  kivi_cache_free(guard->cache);
+  delete guard;
+}
+
+kivi_config kivi_guard_config(const kivi_guard* g) { return g->cache->core.cfg; }
+kivi_cache* kivi_guard_cache(kivi_guard* g) { return g ? g->cache : nullptr; }
+uint32_t kivi_guard_policy(const kivi_guard* g) { return g->policy; }
+size_t kivi_guard_sequence_length(const kivi_guard* g) { return g->seq; }
+
+kivi_status kivi_guard_append(kivi_guard* guard, const float* keys, size_t keys_len,
+                              const float* values, size_t values_len, size_t seq_len,
+                              const float* query, size_t query_len, size_t num_q_heads,
+                              float scale, kivi_flush_check* checks, size_t checks_cap,
+                              size_t* num_checks, kivi_error* err) {
+  return guarded(err, [&]() -> Status {
+    KIVI_TRY(need(guard, "guard"));
+    const CacheCore& core0 = guard->cache->core;
+    const size_t batch = core0.batch, heads = core0.heads, D = core0.head_dim;
+    size_t expected, query_elems;
+    KIVI_TRY(mul4(batch, heads, seq_len, D, &expected));
+    if (keys_len != expected) return Err(KIVI_ERR_SHAPE, expected, keys_len);
+    if (values_len != expected) return Err(KIVI_ERR_SHAPE, expected, values_len);
+    if (num_q_heads == 0 || num_q_heads % heads != 0)
+      return Err(KIVI_ERR_QUERY_HEADS, num_q_heads, heads);
+    KIVI_TRY(mul4(batch, num_q_heads, D, 1, &query_elems));
+    if (query_len != query_elems) return Err(KIVI_ERR_SHAPE, query_elems, query_len);
+    KIVI_TRY(need_slice(query, query_len, "query"));
+    if (seq_len > 0) {
+      KIVI_TRY(need_slice(keys, keys_len, "keys"));
+      KIVI_TRY(need_slice(values, values_len, "values"));
+    }
+    if (checks_cap > 0) KIVI_TRY(need(checks, "checks"));
+    KIVI_TRY(need(num_checks, "num_checks"));
+    std::lock_guard<std::mutex> lock(guard->mu);
+    DeviceScope scope(core0.device);
+    guard->last.clear();
+    const size_t units = batch * heads;
+    std::vector<float> ks, vs;
+    size_t offset = 0;
+    while (offset < seq_len) {
+      const size_t room = kivi_cache_tokens_until_key_flush(guard->cache);
+      const size_t take = std::min(room, seq_len - offset);
+      // slice_tokens (src/guard.rs:291-311): tokens [offset, offset + take) of every unit
+      ks.resize(units * take * D);
+      vs.resize(units * take * D);
+      for (size_t u = 0; u < units; ++u) {
+        std::memcpy(&ks[u * take * D], keys + (u * seq_len + offset) * D, take * D * 4);
+        std::memcpy(&vs[u * take * D], values + (u * seq_len + offset) * D, take * D * 4);
+      }
+      KIVI_TRY(cache_append(guard->cache, ks.data(), ks.size(), vs.data(), vs.size(), take, false,
+                            nullptr));
+      KIVI_TRY(guard_push(guard, ks.data(), vs.data(), take, guard->cache->core.stream));
+      if (guard->cache->core.kres_len == 0) {
+        // QualityGuard::check (src/guard.rs:148-172)
+        kivi_flush_check fc{};
+        KIVI_TRY(guard_cosine_of(guard, query, query_len, num_q_heads, scale, &fc.cosine_before));
+        fc.cosine = fc.cosine_before;
+        while (fc.cosine < guard->threshold) {
+          // QualityGuard::propose (src/guard.rs:174-193)
+          const kivi_config cfg = guard->cache->core.cfg;
+          kivi_quality_upgrade up{};
+          if (guard->policy == KIVI_POLICY_RAISE_BITS) {
+            uint8_t to;
+            if (!guard_next_bits(cfg.bits, guard->max_bits, &to)) break;
+            up = kivi_quality_upgrade{0, cfg.bits, to};
+          } else {
+            size_t to;
+            if (!guard_next_residual(cfg.residual_length, cfg.group_size, guard->max_residual, &to))
+              break;
+            up = kivi_quality_upgrade{1, cfg.residual_length, to};
+          }
+          if (fc.num_upgrades == KIVI_MAX_UPGRADES)
+            return Err(KIVI_ERR_CAPACITY, fc.num_upgrades + 1, KIVI_MAX_UPGRADES, "upgrades");
+          KIVI_TRY(guard_apply(guard, up));
+          fc.upgrades[fc.num_upgrades++] = up;
+          KIVI_TRY(guard_cosine_of(guard, query, query_len, num_q_heads, scale, &fc.cosine));
+        }
+        fc.sequence_tokens = guard->seq;
+        guard->last.push_back(fc);
+      }
+      offset += take;
+    }
+    *num_checks = guard->last.size();
+    for (size_t i = 0; i < guard->last.size() && i < checks_cap; ++i) checks[i] = guard->last[i];
+    return Status{};
+  });
+}
+
+size_t kivi_guard_last_checks(const kivi_guard* guard, size_t first, kivi_flush_check* checks,
+                              size_t cap) {
+  if (guard == nullptr || checks == nullptr) return 0;
+  std::lock_guard<std::mutex> lock(const_cast<kivi_guard*>(guard)->mu);
+  size_t n = 0;
+  for (size_t i = first; i < guard->last.size() && n < cap; ++i) checks[n++] = guard->last[i];
+  return n;
 }
 
 kivi_status kivi_quantize_per_channel(const float* data, size_t data_len, size_t batch,

@@ -80,6 +80,23 @@ class _Footprint(C.Structure):
     ]
 
 
+class _Upgrade(C.Structure):
+    _fields_ = [("kind", C.c_uint32), ("from_", C.c_size_t), ("to", C.c_size_t)]
+
+
+MAX_UPGRADES = 64  # KIVI_MAX_UPGRADES
+
+
+class _FlushCheck(C.Structure):
+    _fields_ = [
+        ("sequence_tokens", C.c_size_t),
+        ("cosine_before", C.c_float),
+        ("cosine", C.c_float),
+        ("num_upgrades", C.c_size_t),
+        ("upgrades", _Upgrade * MAX_UPGRADES),
+    ]
+
+
 # Variant names of KiviError (reference src/error.rs:5-45) by status code.
 VARIANTS = {
     1: "InvalidBits",
@@ -207,6 +224,22 @@ _SIGS = {
         C.c_int,
         [_P, _F32P, _SZ, _F32P, _SZ, _F32P, _SZ, _SZ, C.c_float, _F32P, _SZ, _ERRP],
     ),
+    "guard_new": (
+        C.c_int,
+        [C.POINTER(_Config), _SZ, _SZ, _SZ, C.c_float, C.c_uint32, C.c_uint8, _SZ,
+         C.POINTER(_P), _ERRP],
+    ),
+    "guard_free": (None, [_P]),
+    "guard_config": (_Config, [_P]),
+    "guard_cache": (_P, [_P]),
+    "guard_policy": (C.c_uint32, [_P]),
+    "guard_sequence_length": (_SZ, [_P]),
+    "guard_append": (
+        C.c_int,
+        [_P, _F32P, _SZ, _F32P, _SZ, _SZ, _F32P, _SZ, _SZ, C.c_float,
+         C.POINTER(_FlushCheck), _SZ, C.POINTER(_SZ), _ERRP],
+    ),
+    "guard_last_checks": (_SZ, [_P, _SZ, C.POINTER(_FlushCheck), _SZ]),
     "quantize_per_channel": (
         C.c_int,
         [_F32P, _SZ, _SZ, _SZ, _SZ, _SZ, C.c_uint8, _SZ, C.POINTER(_P), _ERRP],
@@ -690,6 +723,113 @@ class RuntimeKv:
         self._b.call("runtime_decode_device", self._h, C.c_void_p(k_ptr), k_len, C.c_void_p(v_ptr),
                      v_len, C.c_void_p(q_ptr), q_len, num_q_heads, C.c_float(scale),
                      C.c_void_p(out_ptr), out_len, C.c_void_p(stream))
+
+
+class QualityPolicy:
+    """``QualityPolicy`` (src/guard.rs:13-19)."""
+
+    RaiseBits = 0
+    LengthenResidual = 1
+
+
+class QualityUpgrade:
+    """``QualityUpgrade`` (src/guard.rs:22-26): ``kind`` is "Bits" or "Residual"."""
+
+    __slots__ = ("kind", "from_", "to")
+
+    def __init__(self, kind, from_, to):
+        self.kind, self.from_, self.to = kind, from_, to
+
+    @classmethod
+    def bits(cls, from_, to):
+        return cls("Bits", from_, to)
+
+    @classmethod
+    def residual(cls, from_, to):
+        return cls("Residual", from_, to)
+
+    def __eq__(self, other):
+        return isinstance(other, QualityUpgrade) and (self.kind, self.from_, self.to) == (
+            other.kind, other.from_, other.to)
+
+    def __repr__(self):
+        return f"{self.kind} {{ from: {self.from_}, to: {self.to} }}"
+
+
+class FlushCheck:
+    """``FlushCheck`` (src/guard.rs:29-35)."""
+
+    __slots__ = ("sequence_tokens", "cosine_before", "cosine", "upgrades")
+
+    def __init__(self, raw):
+        self.sequence_tokens = raw.sequence_tokens
+        self.cosine_before = raw.cosine_before
+        self.cosine = raw.cosine
+        self.upgrades = [
+            QualityUpgrade("Bits" if u.kind == 0 else "Residual", u.from_, u.to)
+            for u in raw.upgrades[: raw.num_upgrades]
+        ]
+
+    def __repr__(self):
+        return (f"FlushCheck(sequence_tokens={self.sequence_tokens}, "
+                f"cosine_before={self.cosine_before}, cosine={self.cosine}, "
+                f"upgrades={self.upgrades})")
+
+
+class QualityGuard:
+    """``QualityGuard`` (src/guard.rs:37-258): a cache plus the fp32 tape of its tokens; after
+    each key flush cache attention is scored against fp32 attention (cosine) and the cache is
+    rebuilt with wider codes or a longer residual window while the score misses ``threshold``."""
+
+    def __init__(self, backend, config, batch, num_kv_heads, head_dim, threshold, policy,
+                 max_bits, max_residual):
+        self._b = backend
+        h = C.c_void_p()
+        backend.call("guard_new", C.byref(config._c()), batch, num_kv_heads, head_dim,
+                     C.c_float(threshold), policy, max_bits, max_residual, C.byref(h))
+        self._h = h
+
+    @classmethod
+    def try_new(cls, backend, config, batch, num_kv_heads, head_dim, threshold, policy, max_bits,
+                max_residual):
+        return cls(backend, config, batch, num_kv_heads, head_dim, threshold, policy, max_bits,
+                   max_residual)
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h:
+            self._b["guard_free"](h)
+            self._h = None
+
+    def config(self):
+        c = self._b["guard_config"](self._h)
+        return KiviConfig(c.bits, c.group_size, c.residual_length)
+
+    def cache(self):
+        """The resident cache, borrowed: valid until the next append that upgrades."""
+        ch = C.c_void_p(self._b["guard_cache"](self._h))
+        c = KiviCache(self._b, None, 0, 0, 0, _handle=ch, _owner=False)
+        c._guard = self
+        return c
+
+    def policy(self):
+        return self._b["guard_policy"](self._h)
+
+    def sequence_length(self):
+        return self._b["guard_sequence_length"](self._h)
+
+    def append(self, keys, values, seq_len, query, num_q_heads, scale):
+        k, v, q = _f32(keys), _f32(values), _f32(query)
+        cap = 8
+        buf = (_FlushCheck * cap)()
+        n = _SZ(0)
+        self._b.call("guard_append", self._h, _fptr(k), k.size, _fptr(v), v.size, seq_len,
+                     _fptr(q), q.size, num_q_heads, C.c_float(scale), buf, cap, C.byref(n))
+        if n.value > cap:
+            buf = (_FlushCheck * n.value)()
+            got = self._b["guard_last_checks"](self._h, 0, buf, n.value)
+            assert got == n.value
+        return [FlushCheck(buf[i]) for i in range(n.value)]
 
 
 PER_CHANNEL, PER_TOKEN = 0, 1

@@ -755,6 +755,17 @@ struct kivi_oracle_session {
 struct kivi_oracle_runtime {
   kivi_oracle_cache cache;
 };
+// QualityGuard (src/guard.rs:37-47).
+struct kivi_oracle_guard {
+  kivi_oracle_cache cache;  // the resident cache, replaced by a rebuild
+  std::vector<float> keys, values;
+  size_t seq = 0;
+  float threshold = 0.f;
+  uint8_t max_bits = 8;
+  size_t max_residual = 0;
+  uint32_t policy = KIVI_POLICY_RAISE_BITS;
+  std::vector<kivi_flush_check> last;
+};
 struct kivi_oracle_quantized {
   std::vector<PackedStream> streams;  // QuantizedTensor (src/quant.rs:26-35)
   size_t batch = 0, heads = 0, head_dim = 0, tokens = 0;
@@ -860,6 +871,140 @@ Status quantize_impl(const float* data, size_t data_len, size_t batch, size_t he
 }  // namespace
 
 // ================================================================= C API (oracle)
+// ---------------------------------------------------------------- QualityGuard helpers
+
+// next_bits (src/guard.rs:261-272).
+bool guard_next_bits(uint8_t current, uint8_t max_bits, uint8_t* next) {
+  uint8_t n;
+  switch (current) {
+    case 2: n = 4; break;
+    case 4: n = 8; break;
+    default: return false;
+  }
+  if (n > max_bits) return false;
+  *next = n;
+  return true;
+}
+
+// next_residual (src/guard.rs:274-289).
+bool guard_next_residual(size_t current, size_t group_size, size_t max_residual, size_t* next) {
+  if (current >= max_residual) return false;
+  const size_t doubled = current > SIZE_MAX / 2 ? SIZE_MAX : current * 2;  // saturating_mul
+  const size_t n = doubled <= max_residual ? doubled : max_residual;
+  if (n > current && n % group_size == 0) {
+    *next = n;
+    return true;
+  }
+  return false;
+}
+
+// slice_tokens (src/guard.rs:291-311).
+std::vector<float> guard_slice(const float* src, size_t batch, size_t heads, size_t seq,
+                               size_t start, size_t len, size_t dim) {
+  std::vector<float> out(batch * heads * len * dim, 0.f);
+  for (size_t b = 0; b < batch; ++b)
+    for (size_t h = 0; h < heads; ++h) {
+      const size_t hi = b * heads + h;
+      std::memcpy(&out[hi * len * dim], src + hi * seq * dim + start * dim, len * dim * 4);
+    }
+  return out;
+}
+
+// concat_tokens (src/guard.rs:313-342).
+std::vector<float> guard_concat(const std::vector<float>& old, const std::vector<float>& add,
+                                size_t old_len, size_t new_len, size_t batch, size_t heads,
+                                size_t dim) {
+  const size_t total = old_len + new_len;
+  std::vector<float> dst(batch * heads * total * dim, 0.f);
+  for (size_t b = 0; b < batch; ++b)
+    for (size_t h = 0; h < heads; ++h) {
+      const size_t hi = b * heads + h;
+      if (old_len > 0)
+        std::memcpy(&dst[hi * total * dim], &old[hi * old_len * dim], old_len * dim * 4);
+      std::memcpy(&dst[hi * total * dim + old_len * dim], &add[hi * new_len * dim], new_len * dim * 4);
+    }
+  return dst;
+}
+
+// fp32_attention (src/guard.rs:344-385): f32 sums in token and dim order, expf, maxNum fold.
+std::vector<float> guard_fp32_attention(const float* query, const std::vector<float>& keys,
+                                        const std::vector<float>& values, size_t batch,
+                                        size_t kv_heads, size_t q_heads, size_t seq, size_t dim,
+                                        float scale) {
+  std::vector<float> out(batch * q_heads * dim, 0.f);
+  const size_t group = q_heads / kv_heads;
+  std::vector<float> logits(seq, 0.f);
+  for (size_t b = 0; b < batch; ++b)
+    for (size_t qh = 0; qh < q_heads; ++qh) {
+      const size_t kvh = qh / group;
+      const float* q = query + (b * q_heads + qh) * dim;
+      const size_t base = (b * kv_heads + kvh) * seq * dim;
+      for (size_t t = 0; t < seq; ++t) {
+        float dot = 0.f;
+        for (size_t d = 0; d < dim; ++d) dot += q[d] * keys[base + t * dim + d];
+        logits[t] = dot * scale;
+      }
+      float mx = -INFINITY;
+      for (float l : logits) mx = fmaxf(mx, l);
+      float sum = 0.f;
+      for (float& l : logits) {
+        l = expf(l - mx);
+        sum += l;
+      }
+      float* y = &out[(b * q_heads + qh) * dim];
+      for (size_t d = 0; d < dim; ++d) y[d] = 0.f;
+      for (size_t t = 0; t < seq; ++t) {
+        const float w = logits[t] / sum;
+        for (size_t d = 0; d < dim; ++d) y[d] += w * values[base + t * dim + d];
+      }
+    }
+  return out;
+}
+
+// cosine_sim (src/guard.rs:387-402).
+float guard_cosine_sim(const std::vector<float>& a, const std::vector<float>& b) {
+  float dot = 0.f, na = 0.f, nb = 0.f;
+  for (size_t i = 0; i < a.size() && i < b.size(); ++i) {
+    dot += a[i] * b[i];
+    na += a[i] * a[i];
+    nb += b[i] * b[i];
+  }
+  const float denom = std::sqrt(na) * std::sqrt(nb);
+  return denom == 0.f ? 1.f : dot / denom;
+}
+
+// QualityGuard::cosine (src/guard.rs:218-235).
+Status guard_cosine(const kivi_oracle_guard& g, const float* query, size_t query_len,
+                    size_t num_q_heads, float scale, float* cosine) {
+  const Cache& c = *g.cache.c;
+  std::vector<float> got(c.batch * num_q_heads * c.head_dim);
+  Status s = c.attention(query, query_len, num_q_heads, scale, got.data());
+  if (!s.ok()) return s;
+  const std::vector<float> expect = guard_fp32_attention(
+      query, g.keys, g.values, c.batch, c.heads, num_q_heads, g.seq, c.head_dim, scale);
+  *cosine = guard_cosine_sim(got, expect);
+  return Status{};
+}
+
+// QualityGuard::apply (src/guard.rs:195-216).
+Status guard_apply(kivi_oracle_guard& g, const kivi_quality_upgrade& up) {
+  const kivi_config cur = g.cache.c->config;
+  kivi_config cfg{};
+  Status s = up.kind == 0 ? config_try_new(static_cast<uint8_t>(up.to), cur.group_size, cur.residual_length)
+                          : config_try_new(cur.bits, cur.group_size, up.to);
+  if (!s.ok()) return s;
+  cfg.bits = up.kind == 0 ? static_cast<uint8_t>(up.to) : cur.bits;
+  cfg.group_size = cur.group_size;
+  cfg.residual_length = up.kind == 0 ? cur.residual_length : up.to;
+  std::unique_ptr<Cache> c;
+  if (!(s = Cache::create(cfg, g.cache.c->batch, g.cache.c->heads, g.cache.c->head_dim, &c)).ok()) return s;
+  if (g.seq > 0 &&
+      !(s = c->append(g.keys.data(), g.keys.size(), g.values.data(), g.values.size(), g.seq)).ok())
+    return s;
+  g.cache.c = std::move(c);
+  return Status{};
+}
+
 extern "C" {
 
 void kivi_oracle_config_default(kivi_config* out) {
@@ -1236,6 +1381,123 @@ kivi_status kivi_oracle_runtime_decode(kivi_oracle_runtime* rt, const float* key
   if (st != KIVI_OK) return st;
   return kivi_oracle_cache_attention(&rt->cache, query, query_len, num_q_heads, scale, out,
                                      out_len, err);
+}
+
+// QualityGuard::try_new and accessors (src/guard.rs:50-88).
+kivi_status kivi_oracle_guard_new(const kivi_config* config, size_t batch, size_t num_kv_heads,
+                                  size_t head_dim, float threshold, uint32_t policy,
+                                  uint8_t max_bits, size_t max_residual, kivi_oracle_guard** out,
+                                  kivi_error* err) {
+  return guarded(err, [&] {
+    Status s = need(config, "config");
+    if (!s.ok()) return s;
+    if (!(s = need(out, "out")).ok()) return s;
+    if (policy != KIVI_POLICY_RAISE_BITS && policy != KIVI_POLICY_LENGTHEN_RESIDUAL)
+      return Err(KIVI_ERR_UNSUPPORTED, policy, 1, "policy");
+    if (!(s = config_try_new(config->bits, config->group_size, config->residual_length)).ok())
+      return s;
+    auto g = std::make_unique<kivi_oracle_guard>();
+    if (!(s = Cache::create(*config, batch, num_kv_heads, head_dim, &g->cache.c)).ok()) return s;
+    g->threshold = threshold;
+    g->policy = policy;
+    g->max_bits = max_bits;
+    g->max_residual = max_residual;
+    *out = g.release();
+    return Status{};
+  });
+}
+void kivi_oracle_guard_free(kivi_oracle_guard* g) { delete g; }
+kivi_config kivi_oracle_guard_config(const kivi_oracle_guard* g) { return g->cache.c->config; }
+uint32_t kivi_oracle_guard_policy(const kivi_oracle_guard* g) { return g->policy; }
+size_t kivi_oracle_guard_sequence_length(const kivi_oracle_guard* g) { return g->seq; }
+kivi_oracle_cache* kivi_oracle_guard_cache(kivi_oracle_guard* g) { return g ? &g->cache : nullptr; }
+
+// QualityGuard::append / check / propose (src/guard.rs:90-193).
+kivi_status kivi_oracle_guard_append(kivi_oracle_guard* g, const float* keys, size_t keys_len,
+                                     const float* values, size_t values_len, size_t seq_len,
+                                     const float* query, size_t query_len, size_t num_q_heads,
+                                     float scale, kivi_flush_check* checks, size_t checks_cap,
+                                     size_t* num_checks, kivi_error* err) {
+  return guarded(err, [&]() -> Status {
+    Status s = need(g, "guard");
+    if (!s.ok()) return s;
+    const size_t batch = g->cache.c->batch, heads = g->cache.c->heads, dim = g->cache.c->head_dim;
+    const size_t expected = batch * heads * seq_len * dim;
+    if (keys_len != expected) return Err(KIVI_ERR_SHAPE, expected, keys_len);
+    if (values_len != expected) return Err(KIVI_ERR_SHAPE, expected, values_len);
+    const size_t query_elems = batch * num_q_heads * dim;
+    if (num_q_heads == 0 || num_q_heads % heads != 0)
+      return Err(KIVI_ERR_QUERY_HEADS, num_q_heads, heads);
+    if (query_len != query_elems) return Err(KIVI_ERR_SHAPE, query_elems, query_len);
+    if (!(s = need_slice(query, query_len, "query")).ok()) return s;
+    if (!(s = need_slice(keys, keys_len, "keys")).ok()) return s;
+    if (!(s = need_slice(values, values_len, "values")).ok()) return s;
+    if (checks_cap > 0 && !(s = need(checks, "checks")).ok()) return s;
+    if (!(s = need(num_checks, "num_checks")).ok()) return s;
+    g->last.clear();
+    size_t offset = 0;
+    while (offset < seq_len) {
+      const size_t r = g->cache.c->config.residual_length;
+      const size_t room = r > g->cache.c->key_res_len ? r - g->cache.c->key_res_len : 0;
+      const size_t take = room < seq_len - offset ? room : seq_len - offset;
+      const std::vector<float> ks = guard_slice(keys, batch, heads, seq_len, offset, take, dim);
+      const std::vector<float> vs = guard_slice(values, batch, heads, seq_len, offset, take, dim);
+      if (!(s = g->cache.c->append(ks.data(), ks.size(), vs.data(), vs.size(), take)).ok()) return s;
+      // push_history (src/guard.rs:237-245)
+      g->keys = guard_concat(g->keys, ks, g->seq, take, batch, heads, dim);
+      g->values = guard_concat(g->values, vs, g->seq, take, batch, heads, dim);
+      g->seq += take;
+      if (g->cache.c->key_res_len == 0) {
+        kivi_flush_check fc{};
+        if (!(s = guard_cosine(*g, query, query_len, num_q_heads, scale, &fc.cosine_before)).ok())
+          return s;
+        fc.cosine = fc.cosine_before;
+        while (fc.cosine < g->threshold) {
+          const kivi_config cfg = g->cache.c->config;
+          kivi_quality_upgrade up{};
+          if (g->policy == KIVI_POLICY_RAISE_BITS) {
+            uint8_t to;
+            if (!guard_next_bits(cfg.bits, g->max_bits, &to)) break;
+            up = kivi_quality_upgrade{0, cfg.bits, to};
+          } else {
+            size_t to;
+            if (!guard_next_residual(cfg.residual_length, cfg.group_size, g->max_residual, &to)) break;
+            up = kivi_quality_upgrade{1, cfg.residual_length, to};
+          }
+          if (fc.num_upgrades == KIVI_MAX_UPGRADES)
+            return Err(KIVI_ERR_CAPACITY, fc.num_upgrades + 1, KIVI_MAX_UPGRADES, "upgrades");
+          if (!(s = guard_apply(*g, up)).ok()) return s;
+          fc.upgrades[fc.num_upgrades++] = up;
+          if (!(s = guard_cosine(*g, query, query_len, num_q_heads, scale, &fc.cosine)).ok()) return s;
+        }
+        fc.sequence_tokens = g->seq;
+        g->last.push_back(fc);
+      }
+      offset += take;
+    }
+    *num_checks = g->last.size();
+    for (size_t i = 0; i < g->last.size() && i < checks_cap; ++i) checks[i] = g->last[i];
+    return Status{};
+  });
+}
+
+size_t kivi_oracle_guard_last_checks(const kivi_oracle_guard* g, size_t first,
+                                     kivi_flush_check* checks, size_t cap) {
+  if (g == nullptr || checks == nullptr) return 0;
+  size_t n = 0;
+  for (size_t i = first; i < g->last.size() && n < cap; ++i) checks[n++] = g->last[i];
+  return n;
+}
+
+// fp32_attention (src/guard.rs:344-385) over [batch*kv_heads][seq][dim] rows, for the tests.
+void kivi_oracle_fp32_attention(const float* query, const float* keys, const float* values,
+                                size_t batch, size_t kv_heads, size_t q_heads, size_t seq,
+                                size_t dim, float scale, float* out) {
+  const size_t n = batch * kv_heads * seq * dim;
+  const std::vector<float> k(keys, keys + n), v(values, values + n);
+  const std::vector<float> o =
+      guard_fp32_attention(query, k, v, batch, kv_heads, q_heads, seq, dim, scale);
+  std::memcpy(out, o.data(), o.size() * 4);
 }
 
 // quantize_per_channel / quantize_per_token (src/quant.rs:153-233).
