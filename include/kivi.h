@@ -179,6 +179,10 @@ kivi_status kivi_cache_attention_device(const kivi_cache* cache, const float* qu
  * batch*num_kv_heads*seq*head_dim floats. */
 kivi_status kivi_cache_dequantize(const kivi_cache* cache, float* keys, size_t keys_len,
                                   float* values, size_t values_len, kivi_error* err);
+/* Same, into device buffers, enqueued on `stream` (hipStream_t as void*). */
+kivi_status kivi_cache_dequantize_device(const kivi_cache* cache, float* keys, size_t keys_len,
+                                         float* values, size_t values_len, void* stream,
+                                         kivi_error* err);
 
 /* KiviCache::memory (src/cache.rs:362-380). */
 kivi_memory_report kivi_cache_memory(const kivi_cache* cache);
@@ -193,10 +197,27 @@ kivi_status kivi_cache_export_streams(const kivi_cache* cache, uint32_t* key_cod
                                       size_t key_params_len, uint32_t* value_codes,
                                       size_t value_codes_len, float* value_params,
                                       size_t value_params_len, kivi_error* err);
+/* Same, into device buffers, enqueued on `stream`. */
+kivi_status kivi_cache_export_streams_device(const kivi_cache* cache, uint32_t* key_codes,
+                                             size_t key_codes_len, float* key_params,
+                                             size_t key_params_len, uint32_t* value_codes,
+                                             size_t value_codes_len, float* value_params,
+                                             size_t value_params_len, void* stream,
+                                             kivi_error* err);
 
 /* Extension: pre-size the device arenas for `tokens` total tokens per sequence so
  * later appends never reallocate (the reference's Vec::reserve, src/quant.rs:291-292). */
 kivi_status kivi_cache_reserve(kivi_cache* cache, size_t tokens, kivi_error* err);
+
+/* Extension, arena sizing (the device counterpart of the byte model of src/budget.rs:317-347,
+   which counts occupied bytes): HBM a cache holds, packed arenas at their capacity plus the
+   fp32 key residual and value window and the per-unit counters (attention scratch, sized per
+   call, is not counted). kivi_cache_device_bytes reads a live cache; kivi_plan_device_bytes
+   gives what a cache of that shape holds after kivi_cache_reserve(tokens) (config checked as
+   kivi_cache_new checks it). */
+size_t kivi_cache_device_bytes(const kivi_cache* cache);
+kivi_status kivi_plan_device_bytes(const kivi_config* config, size_t batch, size_t num_kv_heads,
+                                   size_t head_dim, size_t tokens, size_t* out, kivi_error* err);
 
 /* ---------------------------------------------------------------- prefix / sessions */
 
@@ -383,12 +404,19 @@ kivi_status kivi_quantized_codes(const kivi_quantized* q, uint32_t* out, size_t 
 /* QuantizedTensor::pytorch_codes (src/quant.rs:77-112). code_bytes()/4 words. */
 kivi_status kivi_quantized_pytorch_codes(const kivi_quantized* q, uint32_t* out, size_t out_len,
                                          kivi_error* err);
+/* Same, into a device buffer, enqueued on `stream`: the PyTorch-KIVI layout without a host
+   round trip. */
+kivi_status kivi_quantized_pytorch_codes_device(const kivi_quantized* q, uint32_t* out,
+                                                size_t out_len, void* stream, kivi_error* err);
 /* QuantizedTensor::scale_zero (src/quant.rs:116-121). metadata_bytes()/4 floats. */
 kivi_status kivi_quantized_scale_zero(const kivi_quantized* q, float* out, size_t out_len,
                                       kivi_error* err);
 /* QuantizedTensor::dequantize (src/quant.rs:124-150). batch*heads*tokens*head_dim floats. */
 kivi_status kivi_quantized_dequantize(const kivi_quantized* q, float* out, size_t out_len,
                                       kivi_error* err);
+/* Same, into a device buffer, enqueued on `stream`. */
+kivi_status kivi_quantized_dequantize_device(const kivi_quantized* q, float* out, size_t out_len,
+                                             void* stream, kivi_error* err);
 
 /* ---------------------------------------------------------------- misc */
 

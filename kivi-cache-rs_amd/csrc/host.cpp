@@ -319,13 +319,34 @@ struct CacheCore {
   }
 
   // Allocate residual buffers (src/cache.rs:105-119 preallocates them too).
-  Status init(hipStream_t s) {
+  void set_geometry() {
     geo.bits = cfg.bits;
     geo.G = static_cast<uint32_t>(cfg.group_size);
     geo.R = static_cast<uint32_t>(cfg.residual_length);
     geo.D = static_cast<uint32_t>(head_dim);
     geo.units = static_cast<uint32_t>(batch * heads);
     geo.cap = 0;
+  }
+
+  // Packed capacity the arenas grow to when `tokens` must fit: at least double the current
+  // capacity and 256 tokens, rounded up to the granule.
+  uint64_t capacity_for(uint64_t tokens) const {
+    const uint64_t gran = granule();
+    uint64_t want = std::max<uint64_t>(tokens, geo.cap * 2);
+    want = std::max<uint64_t>(want, 256);
+    return (want + gran - 1) / gran * gran;
+  }
+
+  // Bytes of the packed arenas at the current capacity, the residual buffers and the maxima.
+  size_t device_bytes() const {
+    const size_t arenas = (geo.kcodes_unit() + geo.kparams_unit() + geo.vcodes_unit() +
+                           geo.vparams_unit()) * geo.units * 4;
+    return arenas + 2 * (size_t)geo.units * geo.R * geo.D * sizeof(float) +
+           (size_t)geo.units * 4 * sizeof(uint32_t);
+  }
+
+  Status init(hipStream_t s) {
+    set_geometry();
     const size_t rbytes = (size_t)geo.units * geo.R * geo.D * sizeof(float);
     KIVI_TRY(kres.alloc_zero(rbytes, s, "key residual"));
     KIVI_TRY(vring.alloc_zero(rbytes, s, "value window"));
@@ -336,10 +357,7 @@ struct CacheCore {
   // Grow the packed arenas to hold `tokens` per unit, keeping their contents.
   Status ensure_capacity(uint64_t tokens, hipStream_t s) {
     if (tokens <= geo.cap) return Status{};
-    const uint64_t gran = granule();
-    uint64_t want = std::max<uint64_t>(tokens, geo.cap * 2);
-    want = std::max<uint64_t>(want, 256);
-    want = (want + gran - 1) / gran * gran;
+    const uint64_t want = capacity_for(tokens);
     Geometry ng = geo;
     ng.cap = want;
     DevBuf nkc, nkp, nvc, nvp;
@@ -760,6 +778,74 @@ Status cache_attention(const kivi_cache* c, const float* query, size_t query_len
   return sync(s, "attention");
 }
 
+// KiviCache::dequantize (src/cache.rs:282-325) into host buffers (staged) or device buffers.
+Status cache_dequantize(const kivi_cache* cache, float* keys, size_t keys_len, float* values,
+                        size_t values_len, bool device, hipStream_t stream) {
+  KIVI_TRY(need(cache, "cache"));
+  const CacheCore& core = cache->core;
+  size_t n;
+  KIVI_TRY(mul4(core.batch, core.heads, core.seq, core.head_dim, &n));
+  if (keys_len != n) return Err(KIVI_ERR_SHAPE, n, keys_len);
+  if (values_len != n) return Err(KIVI_ERR_SHAPE, n, values_len);
+  if (n == 0) return Status{};
+  KIVI_TRY(need(keys, "keys"));
+  KIVI_TRY(need(values, "values"));
+  DeviceScope scope(core.device);
+  if (device) {
+    HIP_TRY(launch_dequant_cache(core.view(), core.state(), keys, values, stream), "dequantize");
+    return Status{};
+  }
+  hipStream_t s = core.stream;
+  Scratch dk, dv;
+  KIVI_TRY(dk.get(n * 4, s, "dequantize"));
+  KIVI_TRY(dv.get(n * 4, s, "dequantize"));
+  HIP_TRY(launch_dequant_cache(core.view(), core.state(), dk.as<float>(), dv.as<float>(), s), "dequantize");
+  HIP_TRY(hipMemcpyAsync(keys, dk.p, n * 4, hipMemcpyDeviceToHost, s), "dequantize D2H");
+  HIP_TRY(hipMemcpyAsync(values, dv.p, n * 4, hipMemcpyDeviceToHost, s), "dequantize D2H");
+  return sync(s, "dequantize");
+}
+
+// Packed streams in the reference PackedStream order, into host (staged) or device buffers;
+// a NULL array is skipped.
+Status cache_export(const kivi_cache* cache, uint32_t* key_codes, size_t key_codes_len,
+                    float* key_params, size_t key_params_len, uint32_t* value_codes,
+                    size_t value_codes_len, float* value_params, size_t value_params_len,
+                    bool device, hipStream_t stream) {
+  KIVI_TRY(need(cache, "cache"));
+  const CacheCore& core = cache->core;
+  const size_t u = core.units(), D = core.head_dim, G = core.cfg.group_size;
+  const size_t nkc = u * core.kq * D / (32 / core.cfg.bits);
+  const size_t nkp = u * (core.kq / G) * D * 2;
+  const size_t nvc = u * core.vq * D / (32 / core.cfg.bits);
+  const size_t nvp = u * core.vq * (D / G) * 2;
+  if (key_codes && key_codes_len != nkc) return Err(KIVI_ERR_SHAPE, nkc, key_codes_len);
+  if (key_params && key_params_len != nkp) return Err(KIVI_ERR_SHAPE, nkp, key_params_len);
+  if (value_codes && value_codes_len != nvc) return Err(KIVI_ERR_SHAPE, nvc, value_codes_len);
+  if (value_params && value_params_len != nvp) return Err(KIVI_ERR_SHAPE, nvp, value_params_len);
+  DeviceScope scope(core.device);
+  const CacheView cv = core.view();
+  if (device) {
+    HIP_TRY(launch_export_keys(cv, core.kq, nkc ? key_codes : nullptr, nkp ? key_params : nullptr, stream),
+            "export keys");
+    HIP_TRY(launch_export_values(cv, core.vq, nvc ? value_codes : nullptr, nvp ? value_params : nullptr,
+                                 stream), "export values");
+    return Status{};
+  }
+  hipStream_t s = core.stream;
+  Scratch a, b, c, d;
+  if (key_codes && nkc) KIVI_TRY(a.get(nkc * 4, s, "export"));
+  if (key_params && nkp) KIVI_TRY(b.get(nkp * 4, s, "export"));
+  if (value_codes && nvc) KIVI_TRY(c.get(nvc * 4, s, "export"));
+  if (value_params && nvp) KIVI_TRY(d.get(nvp * 4, s, "export"));
+  HIP_TRY(launch_export_keys(cv, core.kq, a.as<uint32_t>(), b.as<float>(), s), "export keys");
+  HIP_TRY(launch_export_values(cv, core.vq, c.as<uint32_t>(), d.as<float>(), s), "export values");
+  if (a.p) HIP_TRY(hipMemcpyAsync(key_codes, a.p, nkc * 4, hipMemcpyDeviceToHost, s), "export D2H");
+  if (b.p) HIP_TRY(hipMemcpyAsync(key_params, b.p, nkp * 4, hipMemcpyDeviceToHost, s), "export D2H");
+  if (c.p) HIP_TRY(hipMemcpyAsync(value_codes, c.p, nvc * 4, hipMemcpyDeviceToHost, s), "export D2H");
+  if (d.p) HIP_TRY(hipMemcpyAsync(value_params, d.p, nvp * 4, hipMemcpyDeviceToHost, s), "export D2H");
+  return sync(s, "export");
+}
+
 // RuntimeKv::decode on device pointers in one attention launch plus its merge: the attention
 // reads the new token's rows from the inputs, quantizes the token the window evicts, and the
 // merge writes the rows to the residual and the window (src/runtime.rs:46-56 = append(key,
@@ -1038,39 +1124,44 @@ Status quantize(const float* data, size_t data_len, size_t batch, size_t heads, 
   return Status{};
 }
 
+// With `device` the output is a device buffer written on `stream` (no staging, no sync).
 Status quantized_read(const kivi_quantized* q, void* out, size_t out_len, size_t want,
-                      int what /*0 codes 1 pytorch 2 params 3 dequant*/) {
+                      int what /*0 codes 1 pytorch 2 params 3 dequant*/, bool device = false,
+                      hipStream_t stream = nullptr) {
   KIVI_TRY(need(q, "quantized"));
   if (out_len != want) return Err(KIVI_ERR_SHAPE, want, out_len);
   if (want == 0) return Status{};
   KIVI_TRY(need(out, "out"));
   DeviceScope scope(q->device);
-  hipStream_t s = nullptr;
+  hipStream_t s = device ? stream : nullptr;
   const uint32_t units = static_cast<uint32_t>(q->batch * q->heads);
   if (what == 0 || what == 2) {
     const void* src = what == 0 ? q->codes.p : q->params.p;
-    HIP_TRY(hipMemcpyAsync(out, src, want * 4, hipMemcpyDeviceToHost, s), "quantized D2H");
-    return sync(s, "quantized read");
+    HIP_TRY(hipMemcpyAsync(out, src, want * 4, device ? hipMemcpyDeviceToDevice : hipMemcpyDeviceToHost, s),
+            "quantized read");
+    return device ? Status{} : sync(s, "quantized read");
   }
   Scratch tmp;
-  KIVI_TRY(tmp.get(want * 4, s, "quantized read"));
+  if (!device) KIVI_TRY(tmp.get(want * 4, s, "quantized read"));
+  void* dst = device ? out : tmp.p;
   if (what == 1) {
     HIP_TRY(launch_pytorch_order(q->codes.as<uint32_t>(), units, q->tokens, static_cast<uint32_t>(q->head_dim),
                                  q->bits, static_cast<uint32_t>(q->group_size),
-                                 q->axis == KIVI_AXIS_PER_CHANNEL, tmp.as<uint32_t>(), s), "pytorch_codes");
+                                 q->axis == KIVI_AXIS_PER_CHANNEL, static_cast<uint32_t*>(dst), s),
+            "pytorch_codes");
   } else {
     HIP_TRY(launch_dequant_ref(q->codes.as<uint32_t>(), q->params.as<float>(), units, q->tokens,
                                static_cast<uint32_t>(q->head_dim), q->bits,
                                static_cast<uint32_t>(q->group_size), q->axis == KIVI_AXIS_PER_CHANNEL,
-                               tmp.as<float>(), s), "dequantize");
+                               static_cast<float*>(dst), s), "dequantize");
   }
+  if (device) return Status{};
   HIP_TRY(hipMemcpyAsync(out, tmp.p, want * 4, hipMemcpyDeviceToHost, s), "quantized D2H");
   return sync(s, "quantized read");
 }
 
 }  // namespace
 
-// ================================================================= C ABI
 // ---------------------------------------------------------------- QualityGuard
 
 // QualityGuard (src/guard.rs:37-258): the resident cache plus the fp32 tape of every appended
@@ -1208,6 +1299,8 @@ Status guard_apply(kivi_guard* g, const kivi_quality_upgrade& up) {
 
 }  // namespace
 
+// ================================================================= C ABI
+
 extern "C" {
 
 void kivi_config_default(kivi_config* out) {
@@ -1323,25 +1416,13 @@ kivi_status kivi_cache_attention_device(const kivi_cache* cache, const float* qu
 
 kivi_status kivi_cache_dequantize(const kivi_cache* cache, float* keys, size_t keys_len,
                                   float* values, size_t values_len, kivi_error* err) {
+  return guarded(err, [&] { return cache_dequantize(cache, keys, keys_len, values, values_len, false, nullptr); });
+}
+kivi_status kivi_cache_dequantize_device(const kivi_cache* cache, float* keys, size_t keys_len,
+                                         float* values, size_t values_len, void* stream,
+                                         kivi_error* err) {
   return guarded(err, [&] {
-    KIVI_TRY(need(cache, "cache"));
-    const CacheCore& core = cache->core;
-    size_t n;
-    KIVI_TRY(mul4(core.batch, core.heads, core.seq, core.head_dim, &n));
-    if (keys_len != n) return Err(KIVI_ERR_SHAPE, n, keys_len);
-    if (values_len != n) return Err(KIVI_ERR_SHAPE, n, values_len);
-    if (n == 0) return Status{};
-    KIVI_TRY(need(keys, "keys"));
-    KIVI_TRY(need(values, "values"));
-    DeviceScope scope(core.device);
-    hipStream_t s = core.stream;
-    Scratch dk, dv;
-    KIVI_TRY(dk.get(n * 4, s, "dequantize"));
-    KIVI_TRY(dv.get(n * 4, s, "dequantize"));
-    HIP_TRY(launch_dequant_cache(core.view(), core.state(), dk.as<float>(), dv.as<float>(), s), "dequantize");
-    HIP_TRY(hipMemcpyAsync(keys, dk.p, n * 4, hipMemcpyDeviceToHost, s), "dequantize D2H");
-    HIP_TRY(hipMemcpyAsync(values, dv.p, n * 4, hipMemcpyDeviceToHost, s), "dequantize D2H");
-    return sync(s, "dequantize");
+    return cache_dequantize(cache, keys, keys_len, values, values_len, true, static_cast<hipStream_t>(stream));
   });
 }
 
@@ -1353,32 +1434,20 @@ kivi_status kivi_cache_export_streams(const kivi_cache* cache, uint32_t* key_cod
                                       size_t value_codes_len, float* value_params,
                                       size_t value_params_len, kivi_error* err) {
   return guarded(err, [&] {
-    KIVI_TRY(need(cache, "cache"));
-    const CacheCore& core = cache->core;
-    const size_t u = core.units(), D = core.head_dim, G = core.cfg.group_size;
-    const size_t nkc = u * core.kq * D / (32 / core.cfg.bits);
-    const size_t nkp = u * (core.kq / G) * D * 2;
-    const size_t nvc = u * core.vq * D / (32 / core.cfg.bits);
-    const size_t nvp = u * core.vq * (D / G) * 2;
-    if (key_codes && key_codes_len != nkc) return Err(KIVI_ERR_SHAPE, nkc, key_codes_len);
-    if (key_params && key_params_len != nkp) return Err(KIVI_ERR_SHAPE, nkp, key_params_len);
-    if (value_codes && value_codes_len != nvc) return Err(KIVI_ERR_SHAPE, nvc, value_codes_len);
-    if (value_params && value_params_len != nvp) return Err(KIVI_ERR_SHAPE, nvp, value_params_len);
-    DeviceScope scope(core.device);
-    hipStream_t s = core.stream;
-    const CacheView cv = core.view();
-    Scratch a, b, c, d;
-    if (key_codes && nkc) KIVI_TRY(a.get(nkc * 4, s, "export"));
-    if (key_params && nkp) KIVI_TRY(b.get(nkp * 4, s, "export"));
-    if (value_codes && nvc) KIVI_TRY(c.get(nvc * 4, s, "export"));
-    if (value_params && nvp) KIVI_TRY(d.get(nvp * 4, s, "export"));
-    HIP_TRY(launch_export_keys(cv, core.kq, a.as<uint32_t>(), b.as<float>(), s), "export keys");
-    HIP_TRY(launch_export_values(cv, core.vq, c.as<uint32_t>(), d.as<float>(), s), "export values");
-    if (a.p) HIP_TRY(hipMemcpyAsync(key_codes, a.p, nkc * 4, hipMemcpyDeviceToHost, s), "export D2H");
-    if (b.p) HIP_TRY(hipMemcpyAsync(key_params, b.p, nkp * 4, hipMemcpyDeviceToHost, s), "export D2H");
-    if (c.p) HIP_TRY(hipMemcpyAsync(value_codes, c.p, nvc * 4, hipMemcpyDeviceToHost, s), "export D2H");
-    if (d.p) HIP_TRY(hipMemcpyAsync(value_params, d.p, nvp * 4, hipMemcpyDeviceToHost, s), "export D2H");
-    return sync(s, "export");
+    return cache_export(cache, key_codes, key_codes_len, key_params, key_params_len, value_codes,
+                        value_codes_len, value_params, value_params_len, false, nullptr);
+  });
+}
+kivi_status kivi_cache_export_streams_device(const kivi_cache* cache, uint32_t* key_codes,
+                                             size_t key_codes_len, float* key_params,
+                                             size_t key_params_len, uint32_t* value_codes,
+                                             size_t value_codes_len, float* value_params,
+                                             size_t value_params_len, void* stream,
+                                             kivi_error* err) {
+  return guarded(err, [&] {
+    return cache_export(cache, key_codes, key_codes_len, key_params, key_params_len, value_codes,
+                        value_codes_len, value_params, value_params_len, true,
+                        static_cast<hipStream_t>(stream));
   });
 }
 
@@ -1389,6 +1458,33 @@ kivi_status kivi_cache_reserve(kivi_cache* cache, size_t tokens, kivi_error* err
     DeviceScope scope(cache->core.device);
     KIVI_TRY(cache->core.ensure_capacity(tokens, cache->core.stream));
     return sync(cache->core.stream, "reserve");
+  });
+}
+
+size_t kivi_cache_device_bytes(const kivi_cache* cache) {
+  return cache ? cache->core.device_bytes() + cache->attn.counters.bytes : 0;
+}
+
+kivi_status kivi_plan_device_bytes(const kivi_config* config, size_t batch, size_t num_kv_heads,
+                                   size_t head_dim, size_t tokens, size_t* out, kivi_error* err) {
+  return guarded(err, [&] {
+    KIVI_TRY(need(config, "config"));
+    KIVI_TRY(check_config(*config));
+    if (batch == 0) return Err(KIVI_ERR_ZERO_DIMENSION, 0, 0, "batch");
+    if (num_kv_heads == 0) return Err(KIVI_ERR_ZERO_DIMENSION, 0, 0, "num_kv_heads");
+    if (head_dim == 0 || head_dim % config->group_size != 0)
+      return Err(KIVI_ERR_HEAD_DIM, head_dim, config->group_size);
+    KIVI_TRY(check_limits(*config, batch, num_kv_heads, head_dim));
+    KIVI_TRY(need(out, "out"));
+    CacheCore core;
+    core.cfg = *config;
+    core.batch = batch;
+    core.heads = num_kv_heads;
+    core.head_dim = head_dim;
+    core.set_geometry();
+    if (tokens > 0) core.geo.cap = core.capacity_for(tokens);
+    *out = core.device_bytes() + core.units() * sizeof(uint32_t);
+    return Status{};
   });
 }
 
@@ -1782,6 +1878,19 @@ kivi_status kivi_quantized_dequantize(const kivi_quantized* q, float* out, size_
   return guarded(err, [&] {
     const size_t n = q ? q->batch * q->heads * q->tokens * q->head_dim : 0;
     return quantized_read(q, out, out_len, n, 3);
+  });
+}
+kivi_status kivi_quantized_pytorch_codes_device(const kivi_quantized* q, uint32_t* out,
+                                                size_t out_len, void* stream, kivi_error* err) {
+  return guarded(err, [&] {
+    return quantized_read(q, out, out_len, q ? q->n_codes : 0, 1, true, static_cast<hipStream_t>(stream));
+  });
+}
+kivi_status kivi_quantized_dequantize_device(const kivi_quantized* q, float* out, size_t out_len,
+                                             void* stream, kivi_error* err) {
+  return guarded(err, [&] {
+    const size_t n = q ? q->batch * q->heads * q->tokens * q->head_dim : 0;
+    return quantized_read(q, out, out_len, n, 3, true, static_cast<hipStream_t>(stream));
   });
 }
 

@@ -280,6 +280,15 @@ _DEVICE_SIGS = {
         C.c_int,
         [_P, _P, _SZ, _P, _SZ, _P, _SZ, _SZ, C.c_float, _P, _SZ, _P, _ERRP],
     ),
+    "cache_dequantize_device": (C.c_int, [_P, _P, _SZ, _P, _SZ, _P, _ERRP]),
+    "cache_export_streams_device": (
+        C.c_int,
+        [_P, _P, _SZ, _P, _SZ, _P, _SZ, _P, _SZ, _P, _ERRP],
+    ),
+    "cache_device_bytes": (_SZ, [_P]),
+    "plan_device_bytes": (C.c_int, [C.POINTER(_Config), _SZ, _SZ, _SZ, _SZ, C.POINTER(_SZ), _ERRP]),
+    "quantized_pytorch_codes_device": (C.c_int, [_P, _P, _SZ, _P, _ERRP]),
+    "quantized_dequantize_device": (C.c_int, [_P, _P, _SZ, _P, _ERRP]),
     "quantize_per_channel_device": (
         C.c_int,
         [_P, _SZ, _SZ, _SZ, _SZ, _SZ, C.c_uint8, _SZ, _P, C.POINTER(_P), _ERRP],
@@ -534,6 +543,20 @@ class KiviCache:
     def attention_device(self, q_ptr, q_len, num_q_heads, scale, out_ptr, out_len, stream=0):
         self._b.call("cache_attention_device", self._h, C.c_void_p(q_ptr), q_len, num_q_heads,
                      C.c_float(scale), C.c_void_p(out_ptr), out_len, C.c_void_p(stream))
+
+    def dequantize_device(self, k_ptr, k_len, v_ptr, v_len, stream=0):
+        self._b.call("cache_dequantize_device", self._h, C.c_void_p(k_ptr), k_len,
+                     C.c_void_p(v_ptr), v_len, C.c_void_p(stream))
+
+    def export_streams_device(self, ptrs, lens, stream=0):
+        """``ptrs``/``lens``: key codes, key params, value codes, value params (0 = skip)."""
+        args = []
+        for p, n in zip(ptrs, lens):
+            args += [C.c_void_p(p or None), n]
+        self._b.call("cache_export_streams_device", self._h, *args, C.c_void_p(stream))
+
+    def device_bytes(self):
+        return self._b["cache_device_bytes"](self._h)
 
 
 class SharedPrefix:
@@ -885,6 +908,22 @@ class QuantizedTensor:
         out = np.zeros(self.batch * self.heads * self.tokens * self.head_dim, dtype=np.float32)
         self._b.call("quantized_dequantize", self._h, _fptr(out), out.size)
         return out
+
+    def pytorch_codes_device(self, out_ptr, out_len, stream=0):
+        self._b.call("quantized_pytorch_codes_device", self._h, C.c_void_p(out_ptr), out_len,
+                     C.c_void_p(stream))
+
+    def dequantize_device(self, out_ptr, out_len, stream=0):
+        self._b.call("quantized_dequantize_device", self._h, C.c_void_p(out_ptr), out_len,
+                     C.c_void_p(stream))
+
+
+def plan_device_bytes(backend, config, batch, num_kv_heads, head_dim, tokens):
+    """HBM a cache of this shape holds after ``reserve(tokens)`` (HIP library only)."""
+    out = _SZ(0)
+    backend.call("plan_device_bytes", C.byref(config._c()), batch, num_kv_heads, head_dim, tokens,
+                 C.byref(out))
+    return out.value
 
 
 def _quantize(backend, name, data, batch, heads, tokens, head_dim, bits, group_size):
