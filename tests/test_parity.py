@@ -115,6 +115,27 @@ def test_attention_parity_long(amd, oracle, bits, gqa):
     assert max_abs(got, dense_attend(kh, vh, q, batch, heads, heads * gqa, seq, dim, scale)) < 1e-4
 
 
+@pytest.mark.parametrize("bits,gqa,batch,heads,seq", [(2, 4, 4, 8, 50000), (8, 8, 4, 8, 40000)])
+def test_attention_parity_many_rounds(amd, oracle, bits, gqa, batch, heads, seq):
+    """Caches whose packed splits need more workgroups than the chip holds at once (32 units
+    of 40-50k tokens: 800 / 640 packed workgroups of 8 chunks per wave), so the launch runs in
+    more than one round of workgroups."""
+    dim = 128
+    rng = np.random.default_rng(bits * 100 + gqa)
+    n = batch * heads * seq * dim
+    k = rng.standard_normal(n, dtype=np.float32)
+    v = rng.standard_normal(n, dtype=np.float32)
+    cfg = KiviConfig(bits, 32, 128)
+    a = KiviCache(amd, cfg, batch, heads, dim)
+    o = KiviCache(oracle, cfg, batch, heads, dim)
+    a.append(k, v, seq)
+    o.append(k, v, seq)
+    del k, v
+    q = rng.standard_normal(batch * heads * gqa * dim, dtype=np.float32)
+    scale = np.float32(1 / np.sqrt(128))
+    assert_close(a.attention(q, heads * gqa, scale), o.attention(q, heads * gqa, scale))
+
+
 @pytest.mark.parametrize("bits", [2, 4, 8])
 @pytest.mark.parametrize("dim,group", [(64, 16), (64, 64), (128, 16), (256, 16), (256, 32),
                                        (256, 64)])
