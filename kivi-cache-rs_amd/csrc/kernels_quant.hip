@@ -97,6 +97,37 @@ __device__ __forceinline__ float row_bcast(float v, int p) {
   }
 }
 
+// One exchange step of row_minmax16: of its n token pairs (lo[j], hi[j]) a lane keeps the lo
+// half when `upper` is false and the hi half otherwise, sends the other half to its DPP partner
+// (whose `upper` is the opposite) and combines what it keeps with what it receives.
+template <int CTRL, int N>
+__device__ __forceinline__ void minmax_step(const float* mn, const float* mx, bool upper, float* omn,
+                                            float* omx) {
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    const float kmn = upper ? mn[N + j] : mn[j], smn = upper ? mn[j] : mn[N + j];
+    const float kmx = upper ? mx[N + j] : mx[j], smx = upper ? mx[j] : mx[N + j];
+    const float rmn = dpp_f<CTRL>(smn), rmx = dpp_f<CTRL>(smx);
+    omn[j] = rmn < kmn ? rmn : kmn;
+    omx[j] = rmx > kmx ? rmx : kmx;
+  }
+}
+
+// Min and max of each of 16 tokens over a 16-lane row, where every lane holds its own value of
+// every token (mn[p], mx[p]): lane r of the row gets token r's. A butterfly: partners r^15
+// (mirror), r^7 (half mirror), r^2 and r^1 each differ in the bit that decides which half of
+// the remaining tokens a lane keeps, and the four steps together reach all 16 lanes. 15 lane
+// exchanges per quantity instead of 64 for a reduction of every token.
+__device__ __forceinline__ void row_minmax16(const float (&mn)[16], const float (&mx)[16], float& mn_r,
+                                             float& mx_r) {
+  const uint32_t r = threadIdx.x % 16;
+  float a[8], b[8], c[4], d[4], e[2], f[2];
+  minmax_step<kDppMirror, 8>(mn, mx, (r & 8) != 0, a, b);
+  minmax_step<kDppHalfMirror, 4>(a, b, (r & 4) != 0, c, d);
+  minmax_step<kDppXor2, 2>(c, d, (r & 2) != 0, e, f);
+  minmax_step<kDppXor1, 1>(e, f, (r & 1) != 0, &mn_r, &mx_r);
+}
+
 // OR over aligned groups of L lanes (L a power of two <= 16).
 template <uint32_t L>
 __device__ __forceinline__ uint32_t group_or(uint32_t v) {
@@ -516,12 +547,24 @@ __global__ void __launch_bounds__(kThreads)
     const uint64_t t_hi = vq0 + n < t0 + 16 ? vq0 + n : t0 + 16;
     if (t_lo < t_hi) {
       float x[16][CPL];
+      // token t0 + p reads a valid row: t clamped to [t_lo, t_hi)
+      const uint32_t p_lo = static_cast<uint32_t>(t_lo - t0), p_hi = static_cast<uint32_t>(t_hi - 1 - t0);
+      if (t_lo - vq0 >= n_ring && !in.ring) {
+        // every row from the (linear) input: consecutive rows from the slot's first valid one
+        const float* row0 = in.base + unit * in.stride_unit + (in.offset + (t_lo - vq0 - n_ring)) * D;
 #pragma unroll
-      for (int p = 0; p < 16; ++p) {
-        const uint64_t t = t0 + p < t_lo ? t_lo : t0 + p >= t_hi ? t_hi - 1 : t0 + p;  // a valid row
-        const uint64_t i = t - vq0;
-        const float* row = i < n_ring ? source_row(ring, unit, i, R, D) : source_row(in, unit, i - n_ring, R, D);
-        load_lane<CPL>(row, lane, x[p]);
+        for (int p = 0; p < 16; ++p) {
+          const uint32_t pc = (uint32_t)p < p_lo ? p_lo : (uint32_t)p > p_hi ? p_hi : (uint32_t)p;
+          load_lane<CPL>(row0 + (pc - p_lo) * D, lane, x[p]);
+        }
+      } else {
+#pragma unroll
+        for (int p = 0; p < 16; ++p) {
+          const uint32_t pc = (uint32_t)p < p_lo ? p_lo : (uint32_t)p > p_hi ? p_hi : (uint32_t)p;
+          const uint64_t i = t0 + pc - vq0;
+          const float* row = i < n_ring ? source_row(ring, unit, i, R, D) : source_row(in, unit, i - n_ring, R, D);
+          load_lane<CPL>(row, lane, x[p]);
+        }
       }
       uint32_t word[CPL][WPW];
 #pragma unroll
@@ -529,39 +572,35 @@ __global__ void __launch_bounds__(kThreads)
 #pragma unroll
         for (int k = 0; k < (int)WPW; ++k) word[j][k] = 0;
       if constexpr (L == 16) {
-        // A channel group is a DPP row of 16 lanes and the wave has 16 rows: lane r of each
-        // group divides for row r once (one division for the 16 rows), stores row r's
-        // (scale, zero) (16 consecutive pairs per group), and row_newbcast hands each row's
-        // scale and reciprocal to the group's lanes.
-        float mnv[16];
-        const uint32_t r = lane % 16;
-        float span_r = 0.f, mn_r = 0.f;
+        // A channel group is a DPP row of 16 lanes and the wave has 16 rows: the group's
+        // min/max of row r ends in lane r (row_minmax16), which divides for row r once (one
+        // division for the 16 rows) and stores row r's (scale, zero) (16 consecutive pairs per
+        // group); row_newbcast hands each row's zero, scale and reciprocal to the group's lanes.
+        float pmn[16], pmx[16];
 #pragma unroll
         for (int p = 0; p < 16; ++p) {
-          float mn = x[p][0], mx = x[p][0];
+          pmn[p] = pmx[p] = x[p][0];
 #pragma unroll
-          for (int j = 1; j < CPL; ++j) minmax_with(mn, mx, x[p][j], x[p][j]);
-          group_minmax<L>(mn, mx);
-          mnv[p] = mn;
-          if (t0 + p >= t_lo && t0 + p < t_hi) amax = fmaxf(amax, fmaxf(fabsf(mn), fabsf(mx)));
-          if (r == (uint32_t)p) {
-            span_r = mx - mn;
-            mn_r = mn;
-          }
+          for (int j = 1; j < CPL; ++j) minmax_with(pmn[p], pmx[p], x[p][j], x[p][j]);
         }
-        const float scale_r = scale_of(span_r, levels);
+        float mn_r, mx_r;
+        row_minmax16(pmn, pmx, mn_r, mx_r);
+        const uint32_t r = lane % 16;
+        const float scale_r = scale_of(mx_r - mn_r, levels);
         const float inv_r = quant_inv(scale_r);
         if (t0 + r >= t_lo && t0 + r < t_hi) {
           smax = fmaxf(smax, scale_r);
+          amax = fmaxf(amax, fmaxf(fabsf(mn_r), fabsf(mx_r)));
           params[(tb * ncg + cg) * kValueBlock + 16 * wave + r] = make_float2(scale_r, mn_r);
         }
 #pragma unroll
         for (int p = 0; p < 16; ++p) {
           const bool valid = t0 + p >= t_lo && t0 + p < t_hi;
           const float scale = row_bcast(scale_r, p), inv = row_bcast(inv_r, p);
+          const float zero = row_bcast(mn_r, p);
 #pragma unroll
           for (int j = 0; j < CPL; ++j) {
-            const uint32_t code = quant_code_fast(x[p][j], mnv[p], scale, inv, kLevels);
+            const uint32_t code = quant_code_fast(x[p][j], zero, scale, inv, kLevels);
             word[j][p / PPW] |= (valid ? code : 0u) << code_shift(BITS, p % PPW);
           }
         }
