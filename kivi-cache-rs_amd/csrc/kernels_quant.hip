@@ -272,14 +272,15 @@ __device__ __forceinline__ void stage_row(const float* src, float* dst, uint32_t
                                           uint32_t part, uint32_t parts) {
   if (vec4) {
     for (uint32_t c4 = part; c4 < D / 4; c4 += parts) {
-      const float4 v = reinterpret_cast<const float4*>(src)[c4];
+      typedef float f4v_ __attribute__((ext_vector_type(4)));
+      const f4v_ v = __builtin_nontemporal_load(reinterpret_cast<const f4v_*>(src) + c4);
       dst[4 * c4] = v.x;
       dst[4 * c4 + 1] = v.y;
       dst[4 * c4 + 2] = v.z;
       dst[4 * c4 + 3] = v.w;
     }
   } else {
-    for (uint32_t c = part; c < D; c += parts) dst[c] = src[c];
+    for (uint32_t c = part; c < D; c += parts) dst[c] = __builtin_nontemporal_load(src + c);
   }
 }
 
@@ -421,16 +422,20 @@ __global__ void __launch_bounds__(kThreads)
 // row, so every row is one coalesced wave load and the quantization runs in registers; only
 // the codes go through LDS for the packing.
 
+// The rows are read once: non-temporal loads (measured 12-17% faster quantize at the
+// benchmark shapes than cached loads).
+typedef float f2v __attribute__((ext_vector_type(2)));
+typedef float f4v __attribute__((ext_vector_type(4)));
 template <int CPL>
 __device__ __forceinline__ void load_lane(const float* row, uint32_t lane, float (&x)[CPL]) {
   if constexpr (CPL == 4) {
-    const float4 v = reinterpret_cast<const float4*>(row)[lane];
+    const f4v v = __builtin_nontemporal_load(reinterpret_cast<const f4v*>(row) + lane);
     x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
   } else if constexpr (CPL == 2) {
-    const float2 v = reinterpret_cast<const float2*>(row)[lane];
+    const f2v v = __builtin_nontemporal_load(reinterpret_cast<const f2v*>(row) + lane);
     x[0] = v.x; x[1] = v.y;
   } else {
-    x[0] = row[lane];
+    x[0] = __builtin_nontemporal_load(row + lane);
   }
 }
 
