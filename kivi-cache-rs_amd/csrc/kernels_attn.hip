@@ -346,6 +346,11 @@ __global__ void __launch_bounds__(kThreads) k_attn_generic(AttnArgs a) {
 // ------------------------------------------------------------------ MFMA splits
 
 constexpr int kFastCpw = 8;  // chunks (64 tokens) per wave in the MFMA kernel
+constexpr int kCpw6MaxBits = 4;
+// Chunks per wave per instantiation: the eight-head 2- and 4-bit ones take 6, so their logit
+// rows (49.7 KB of LDS per workgroup instead of 66 KB) let three workgroups share a CU, as
+// their registers allow (C3 4-bit: 51.8 us against 55.4 us with 8; 8-bit is slower with 6).
+constexpr int fast_cpw(int bits, int nrs) { return nrs == 2 && bits <= kCpw6MaxBits ? 6 : kFastCpw; }
 // Packed workgroups a launch aims for at least (one per CU): below it, waves take fewer than
 // kFastCpw chunks. More workgroups than that with fewer chunks each measured slower (4-bit,
 // 8 units x 131072 tokens: 1024 workgroups of 4 chunks per wave 62 us, 512 of 8 55 us).
@@ -1120,7 +1125,7 @@ __global__ void __launch_bounds__(kThreads, (NRS == 1 && BITS <= 4) ? 4 : (BITS 
   } else {
     const uint32_t blk = blockIdx.x - nwin;
     unit = blk / a.nsplit_fast;
-    mfma_split<BITS, NRS, kFastCpw, false>(a, unit, blk % a.nsplit_fast, lds);
+    mfma_split<BITS, NRS, fast_cpw(BITS, NRS), false>(a, unit, blk % a.nsplit_fast, lds);
   }
   if (a.counters != nullptr) {
     __syncthreads();
@@ -1850,7 +1855,8 @@ AttnArgs make_args(const AttnProblem& p, float* ws) {
   // kFastGroups workgroups when the chunks allow
   {
     const uint32_t units = p.cache.geo.units;
-    const uint32_t fewest = (a.chunk_end + 4 * kFastCpw - 1) / (4 * kFastCpw);
+    const uint32_t cpw = static_cast<uint32_t>(fast_cpw(static_cast<int>(p.cache.geo.bits), a.gq <= 4 ? 1 : 2));
+    const uint32_t fewest = (a.chunk_end + 4 * cpw - 1) / (4 * cpw);
     const uint32_t most = (a.chunk_end + 3) / 4;
     a.nsplit_fast = std::min(most, std::max(fewest, (kFastGroups + units - 1) / units));
   }
@@ -1876,7 +1882,7 @@ AttnArgs make_args(const AttnProblem& p, float* ws) {
 template <int BITS, int NRS>
 hipError_t launch_fast(const AttnArgs& a, double bytes, hipStream_t stream) {
   constexpr int NH = 4 * NRS;
-  const size_t logits = (size_t)4 * NH * ((a.nsplit_fast > 0 ? kFastCpw : 1) * 64 + kRowPad);
+  const size_t logits = (size_t)4 * NH * ((a.nsplit_fast > 0 ? fast_cpw(BITS, NRS) : 1) * 64 + kRowPad);
   const size_t combine = (size_t)4 * NH * (128 + 2);
   const size_t merge = a.counters != nullptr ? (size_t)4 * a.nsplit_total : 0;
   const size_t lds = std::max(std::max(logits, combine), merge) * sizeof(float);
