@@ -115,6 +115,42 @@ def test_attention_parity_long(amd, oracle, bits, gqa):
     assert max_abs(got, dense_attend(kh, vh, q, batch, heads, heads * gqa, seq, dim, scale)) < 1e-4
 
 
+@pytest.mark.parametrize("bits", [2, 4, 8])
+def test_infinite_inputs_codes_parity(amd, oracle, bits):
+    """Rows with +inf and -inf entries (the reference tests hold none): a group spanning an
+    infinity gets scale inf and codes 0 (the quotient is 0 or NaN, and NaN casts to 0), the
+    others quantize as usual. Packed streams bit-exact through bulk and decode appends, and
+    the standalone quantize of both axes. NaN inputs are not covered: the reference's min/max
+    skip a NaN, the kernels' compare-select reductions need not."""
+    batch, heads, dim, total = 1, 2, 128, 300
+    rng = np.random.default_rng(500 + bits)
+    keys = rng.standard_normal((batch, heads, total, dim)).astype(np.float32)
+    values = rng.standard_normal((batch, heads, total, dim)).astype(np.float32)
+    for arr in (keys, values):
+        flat = arr.reshape(-1)
+        idx = rng.choice(flat.size, 24, replace=False)
+        flat[idx[:12]] = np.inf
+        flat[idx[12:]] = -np.inf
+    cfg = KiviConfig(bits, 32, 128)
+    a = KiviCache(amd, cfg, batch, heads, dim)
+    o = KiviCache(oracle, cfg, batch, heads, dim)
+    off = 0
+    for n in [200, 1, 1, 98]:
+        k = keys[:, :, off:off + n].copy()
+        v = values[:, :, off:off + n].copy()
+        a.append(k, v, n)
+        o.append(k, v, n)
+        off += n
+    assert_streams_equal(a, o)
+    k288 = np.ascontiguousarray(keys[:, :, :288])  # whole groups of tokens
+    for fn, data, tokens in ((kivi.quantize_per_channel, k288, 288),
+                             (kivi.quantize_per_token, values, total)):
+        qa = fn(amd, data, batch, heads, tokens, dim, bits, 32)
+        qo = fn(oracle, data, batch, heads, tokens, dim, bits, 32)
+        assert np.array_equal(qa.codes(), qo.codes())
+        assert np.array_equal(qa.scale_zero().view(np.uint32), qo.scale_zero().view(np.uint32))
+
+
 @pytest.mark.parametrize("bits,gqa,batch,heads,seq", [(2, 4, 4, 8, 50000), (8, 8, 4, 8, 40000)])
 def test_attention_parity_many_rounds(amd, oracle, bits, gqa, batch, heads, seq):
     """Caches whose packed splits need more workgroups than the chip holds at once (32 units
