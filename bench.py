@@ -265,7 +265,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus "
-              f"{args.gpus}); the (batch, kv_head) units shard with no communication, see DESIGN.md",
+              f"{args.gpus}); the (batch, kv_head) units would shard across GPUs with no "
+              f"communication, each GPU running these kernels on its share",
               file=sys.stderr)
         sys.exit(2)
 
