@@ -6,7 +6,9 @@ head_dim 128, 32768 cached tokens per sequence, 2-bit G=32 R=128, K ~ N(0,1) wit
 channels (2 per KV head) scaled x10, V ~ N(0,1), fp32 inputs. A step is one decode attention
 over all 16 sequences (the cache and the queries already resident in HBM); value = decode
 tokens/s = 16 * steps / time. The cache build (prefill quantization) is timed once and
-reported as quantize GB/s. The CPU baseline is the oracle (C++ restatement of the
+reported as quantize GB/s; the device-side export formats (packed streams in the reference
+order, dense reconstruction) are timed once each after it (`exports`: GB/s and fraction of
+8 TB/s). The CPU baseline is the oracle (C++ restatement of the
 reference CPU path, 1 core) on one of the 16 sequences. Before the prefill and before the W
 warm-up steps the GPU runs ~0.3 s of untimed work (device copies, then the step's own
 kernels) so that its clocks have ramped up; `clock_warmup_calls` counts the second part.
@@ -326,6 +328,34 @@ def main():
     quant_bytes = 2 * k.numel() * 4 + mem.compressed_bytes()
     log(f"[bench] prefill quantize {quant_bytes / t_quant / 1e9:.1f} GB/s ({t_quant * 1e3:.2f} ms)")
 
+    # Export formats into device memory, each timed once after an untimed call: the packed
+    # streams in the reference order (packed bytes read and written) and the dense
+    # reconstruction (packed bytes read, fp32 keys and values written).
+    exports = {}
+    if not DECODE.get(args.config):
+        lens = cache.stream_lengths()
+        bufs = [torch.empty(max(n, 1), device="cuda", dtype=torch.float32) for n in lens]
+        ptrs = [b.data_ptr() if n else 0 for b, n in zip(bufs, lens)]
+        n_el = k.numel()
+        dk, dv = torch.empty_like(k), torch.empty_like(v)
+        jobs = (("export_streams", lambda: cache.export_streams_device(ptrs, lens, sp), 2 * 4 * sum(lens)),
+                ("dequantize", lambda: cache.dequantize_device(dk.data_ptr(), n_el, dv.data_ptr(), n_el, sp),
+                 mem.compressed_bytes() + 2 * n_el * 4))
+        for name, fn, nbytes in jobs:
+            fn()
+            stream.synchronize()
+            with torch.cuda.stream(stream):
+                e0.record(stream)
+                fn()
+                e1.record(stream)
+            stream.synchronize()
+            t = e0.elapsed_time(e1) / 1e3
+            exports[name] = {"ms": t * 1e3, "bytes": nbytes, "gbps": nbytes / t / 1e9,
+                             "frac": nbytes / t / (HBM_PEAK_GBPS * 1e9)}
+            log(f"[bench] {name} {nbytes / t / 1e9:.0f} GB/s ({t * 1e3:.3f} ms)")
+        del bufs, dk, dv
+        torch.cuda.empty_cache()
+
     # A step whose cache is smaller than the 256 MB Infinity Cache (MALL) could be served
     # from it by the previous step. Such workloads rotate over `copies` identical caches (the
     # same prefill), so consecutive steps touch >= ROTATE_BYTES of distinct data and each step
@@ -534,6 +564,7 @@ def main():
         "roofline": roofline,
         "kernels": kernels,
         "quantize_kernels": quant_kernels,
+        "exports": exports,
     }
     if not args.no_cpu:
         log("[bench] CPU baseline (oracle, 1 thread) ...")

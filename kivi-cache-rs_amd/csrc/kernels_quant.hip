@@ -656,73 +656,135 @@ __global__ void __launch_bounds__(kThreads)
 // ------------------------------------------------------------------ export to reference order
 
 // Key words (g*D + d)*ipc + w hold tokens g*G + w*ppw + i of channel d (src/quant.rs:312-323).
+// Grid (group slices, units): a workgroup stages a group's token-major words in LDS (one
+// coalesced read), then writes the group's channel-major words (one coalesced write).
+constexpr uint32_t kExportGroups = 8;  // groups per workgroup
 __global__ void __launch_bounds__(kThreads)
     k_export_keys(CacheView c, uint64_t kq, uint32_t* out) {
+  extern __shared__ uint32_t words[];  // [G * D / ppw]
   const Geometry& geo = c.geo;
-  const uint32_t G = geo.G, D = geo.D, bits = geo.bits, ppw = geo.ppw(), kw = geo.kwords_per_token();
-  const uint32_t ipc = G / ppw;
+  const uint32_t G = geo.G, bits = geo.bits, ppw = geo.ppw(), kw = geo.kwords_per_token();
+  const uint32_t ipc = G / ppw, n = G * kw;  // words per group, both orders
   const uint32_t mask = geo.levels();
-  const uint64_t per_unit = (kq / G) * D * ipc;
-  const uint64_t total = per_unit * geo.units;
-  for (uint64_t idx = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; idx < total;
-       idx += (uint64_t)gridDim.x * blockDim.x) {
-    const uint32_t unit = idx / per_unit;
-    const uint64_t r = idx % per_unit;
-    const uint32_t w = r % ipc;
-    const uint32_t d = (r / ipc) % D;
-    const uint64_t g = r / ((uint64_t)ipc * D);
+  const uint64_t ngroups = kq / G;
+  const uint64_t g_end = std::min<uint64_t>(ngroups, (uint64_t)(blockIdx.x + 1) * kExportGroups);
+  for (uint32_t unit = blockIdx.y; unit < geo.units; unit += gridDim.y)
+  for (uint64_t g = (uint64_t)blockIdx.x * kExportGroups; g < g_end; ++g) {
     const uint32_t* src = c.kcodes + unit * geo.kcodes_unit();
-    uint32_t word = 0;
-    for (uint32_t i = 0; i < ppw; ++i) {
-      const uint64_t t = g * G + w * ppw + i;
-      const uint32_t code = (src[t * kw + d / ppw] >> code_shift(bits, d % ppw)) & mask;
-      word |= code << (bits * i);
+    uint32_t* dst = out + (uint64_t)unit * ngroups * n;
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) words[i] = src[g * n + i];
+    __syncthreads();
+    for (uint32_t o = threadIdx.x; o < n; o += blockDim.x) {
+      const uint32_t w = o % ipc, d = o / ipc;
+      const uint32_t sh = code_shift(bits, d % ppw);
+      uint32_t word = 0;
+      for (uint32_t i = 0; i < ppw; ++i)
+        word |= ((words[(w * ppw + i) * kw + d / ppw] >> sh) & mask) << (bits * i);
+      dst[g * n + o] = word;
     }
-    out[idx] = word;
+    __syncthreads();  // the staging buffer is refilled for the next group
   }
 }
 
 // Value words (t*(D/G) + cg)*ipg + w = t*(D/ppw) + j hold channels j*ppw + i of token t
-// (src/quant.rs:362-372); params (t*(D/G) + cg)*2 (src/quant.rs:360-361).
+// (src/quant.rs:362-372); params (t*(D/G) + cg)*2 (src/quant.rs:360-361). Grid (block slices,
+// units): a workgroup stages a 64-token block's channel-major words in LDS (one coalesced read)
+// and writes the block's token-major words and (scale, zero) pairs.
+constexpr uint32_t kExportBlocks = 4;  // 64-token blocks per workgroup
 __global__ void __launch_bounds__(kThreads)
     k_export_values(CacheView c, uint64_t vq, uint32_t* out_codes, float* out_params) {
+  extern __shared__ uint32_t words[];  // [D * 64 / ppw]
   const Geometry& geo = c.geo;
   const uint32_t D = geo.D, bits = geo.bits, ppw = geo.ppw(), vw = geo.vwords_per_channel();
-  const uint32_t ncg = geo.ncg();
+  const uint32_t ncg = geo.ncg(), wpt = D / ppw, n = D * vw;
   const uint32_t mask = geo.levels();
-  const uint32_t wpt = D / ppw;
-  const uint64_t per_unit = vq * wpt;
-  const uint64_t total = per_unit * geo.units;
-  for (uint64_t idx = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; idx < total;
-       idx += (uint64_t)gridDim.x * blockDim.x) {
-    const uint32_t unit = idx / per_unit;
-    const uint64_t r = idx % per_unit;
-    const uint64_t t = r / wpt;
-    const uint32_t j = r % wpt;
-    const uint64_t tb = t / kValueBlock;
-    const uint32_t tt = t % kValueBlock;
-    const uint32_t* src = c.vcodes + unit * geo.vcodes_unit() + tb * D * vw;
-    uint32_t word = 0;
-    for (uint32_t i = 0; i < ppw; ++i) {
-      const uint32_t d = j * ppw + i;
-      const uint32_t code = (src[(uint64_t)d * vw + tt / ppw] >> code_shift(bits, tt % ppw)) & mask;
-      word |= code << (bits * i);
+  const uint64_t nblk = (vq + kValueBlock - 1) / kValueBlock;
+  const uint64_t b_end = std::min<uint64_t>(nblk, (uint64_t)(blockIdx.x + 1) * kExportBlocks);
+  for (uint32_t unit = blockIdx.y; unit < geo.units; unit += gridDim.y)
+  for (uint64_t tb = (uint64_t)blockIdx.x * kExportBlocks; tb < b_end; ++tb) {
+    const uint32_t* src = c.vcodes + unit * geo.vcodes_unit();
+    const float2* prm = reinterpret_cast<const float2*>(c.vparams + unit * geo.vparams_unit());
+    uint32_t* dst = out_codes + (uint64_t)unit * vq * wpt;
+    float2* dpar = out_params ? reinterpret_cast<float2*>(out_params) + (uint64_t)unit * vq * ncg : nullptr;
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) words[i] = src[tb * n + i];
+    __syncthreads();
+    const uint32_t ntok = static_cast<uint32_t>(std::min<uint64_t>(kValueBlock, vq - tb * kValueBlock));
+    for (uint32_t o = threadIdx.x; o < ntok * wpt; o += blockDim.x) {
+      const uint32_t tt = o / wpt, j = o % wpt;
+      const uint32_t sh = code_shift(bits, tt % ppw);
+      uint32_t word = 0;
+      for (uint32_t i = 0; i < ppw; ++i) word |= ((words[(j * ppw + i) * vw + tt / ppw] >> sh) & mask) << (bits * i);
+      dst[tb * kValueBlock * wpt + o] = word;
     }
-    out_codes[idx] = word;
-    if (out_params != nullptr && j < ncg) {
-      const float2 sz = reinterpret_cast<const float2*>(c.vparams + unit * geo.vparams_unit())
-          [(tb * ncg + j) * kValueBlock + tt];
-      reinterpret_cast<float2*>(out_params)[(unit * vq + t) * ncg + j] = sz;
-    }
+    if (dpar != nullptr)
+      for (uint32_t o = threadIdx.x; o < ntok * ncg; o += blockDim.x) {
+        const uint32_t tt = o / ncg, cg = o % ncg;
+        dpar[(tb * kValueBlock + tt) * ncg + cg] = prm[(tb * ncg + cg) * kValueBlock + tt];
+      }
+    __syncthreads();
   }
 }
 
 // ------------------------------------------------------------------ dense reconstruction
 
 // KiviCache::dequantize (src/cache.rs:282-325): packed tokens as fma(code, scale, zero)
-// (src/quant.rs:406, 443), residual tokens copied.
+// (src/quant.rs:406, 443), residual tokens copied. Grid (row slices, units); a thread writes
+// four consecutive channels of a token (D % 4 == 0).
 __global__ void __launch_bounds__(kThreads)
     k_dequant_cache(CacheView c, SeqState s, uint64_t seq, float* keys, float* values) {
+  const Geometry& geo = c.geo;
+  const uint32_t D = geo.D, G = geo.G, R = geo.R, bits = geo.bits, ppw = geo.ppw();
+  const uint32_t kw = geo.kwords_per_token(), vw = geo.vwords_per_channel(), ncg = geo.ncg();
+  const uint32_t mask = geo.levels();
+  const uint32_t q4 = D / 4;
+  const uint64_t per_unit = seq * q4;
+  for (uint32_t unit = blockIdx.y; unit < geo.units; unit += gridDim.y)
+  for (uint64_t r = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; r < per_unit;
+       r += (uint64_t)gridDim.x * blockDim.x) {
+    const uint32_t* kc = c.kcodes + unit * geo.kcodes_unit();
+    const float2* kp = reinterpret_cast<const float2*>(c.kparams + unit * geo.kparams_unit());
+    const uint32_t* vc = c.vcodes + unit * geo.vcodes_unit();
+    const float2* vp = reinterpret_cast<const float2*>(c.vparams + unit * geo.vparams_unit());
+    const uint64_t t = r / q4;
+    const uint32_t d0 = static_cast<uint32_t>(r - t * q4) * 4;
+    float k[4], v[4];
+    if (t < s.kq) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t d = d0 + e;
+        const uint32_t word = kc[t * kw + d / ppw];
+        const float2 sz = kp[(t / G) * D + d];
+        k[e] = fmaf(static_cast<float>((word >> code_shift(bits, d % ppw)) & mask), sz.x, sz.y);
+      }
+    } else {
+      const float4 x = *reinterpret_cast<const float4*>(c.kres + ((uint64_t)unit * R + (t - s.kq)) * D + d0);
+      k[0] = x.x; k[1] = x.y; k[2] = x.z; k[3] = x.w;
+    }
+    if (t < s.vq) {
+      const uint64_t tb = t / kValueBlock;
+      const uint32_t tt = static_cast<uint32_t>(t % kValueBlock);
+      const uint32_t sh = code_shift(bits, tt % ppw);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t d = d0 + e;
+        const uint32_t word = vc[(tb * D + d) * vw + tt / ppw];
+        const float2 sz = vp[(tb * ncg + d / G) * kValueBlock + tt];
+        v[e] = fmaf(static_cast<float>((word >> sh) & mask), sz.x, sz.y);
+      }
+    } else {
+      const float4 x = *reinterpret_cast<const float4*>(
+          c.vring + ((uint64_t)unit * R + (s.vhead + (t - s.vq)) % R) * D + d0);
+      v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
+    }
+    const uint64_t o = ((uint64_t)unit * seq + t) * D + d0;
+    *reinterpret_cast<float4*>(keys + o) = make_float4(k[0], k[1], k[2], k[3]);
+    *reinterpret_cast<float4*>(values + o) = make_float4(v[0], v[1], v[2], v[3]);
+  }
+}
+
+// The same, one element per thread, for output arrays not 16-byte aligned.
+__global__ void __launch_bounds__(kThreads)
+    k_dequant_cache_elem(CacheView c, SeqState s, uint64_t seq, float* keys, float* values) {
   const Geometry& geo = c.geo;
   const uint32_t D = geo.D, G = geo.G, R = geo.R, bits = geo.bits, ppw = geo.ppw();
   const uint32_t kw = geo.kwords_per_token(), vw = geo.vwords_per_channel(), ncg = geo.ncg();
@@ -1034,8 +1096,10 @@ hipError_t launch_export_keys(const CacheView& c, uint64_t kq, uint32_t* codes, 
   const Geometry& g = c.geo;
   if (kq == 0) return hipSuccess;
   if (codes != nullptr) {
-    const uint64_t work = (uint64_t)g.units * kq * g.D / g.ppw();
-    k_export_keys<<<grid_for(work), kThreads, 0, stream>>>(c, kq, codes);
+    const uint64_t slices = (kq / g.G + kExportGroups - 1) / kExportGroups;
+    const size_t lds = (size_t)g.G * g.kwords_per_token() * sizeof(uint32_t);
+    k_export_keys<<<dim3(static_cast<unsigned>(std::min<uint64_t>(slices, 1u << 30)), std::min(g.units, 65535u)),
+                    kThreads, lds, stream>>>(c, kq, codes);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
@@ -1058,8 +1122,11 @@ hipError_t launch_export_values(const CacheView& c, uint64_t vq, uint32_t* codes
     if (e != hipSuccess) return e;
     codes = tmp;
   }
-  const uint64_t work = (uint64_t)g.units * vq * (g.D / g.ppw());
-  k_export_values<<<grid_for(work), kThreads, 0, stream>>>(c, vq, codes, params);
+  const uint64_t nblk = (vq + kValueBlock - 1) / kValueBlock;
+  const uint64_t slices = (nblk + kExportBlocks - 1) / kExportBlocks;
+  const size_t lds = (size_t)g.D * g.vwords_per_channel() * sizeof(uint32_t);
+  k_export_values<<<dim3(static_cast<unsigned>(std::min<uint64_t>(slices, 1u << 30)), std::min(g.units, 65535u)),
+                     kThreads, lds, stream>>>(c, vq, codes, params);
   hipError_t e = hipGetLastError();
   if (tmp != nullptr) {
     hipError_t f = hipFreeAsync(tmp, stream);
@@ -1071,9 +1138,14 @@ hipError_t launch_export_values(const CacheView& c, uint64_t vq, uint32_t* codes
 hipError_t launch_dequant_cache(const CacheView& c, const SeqState& s, float* keys, float* values,
                                 hipStream_t stream) {
   const uint64_t seq = s.kq + s.kres;
-  const uint64_t work = (uint64_t)c.geo.units * seq * c.geo.D;
+  const uint64_t work = seq * (c.geo.D / 4);
   if (work == 0) return hipSuccess;
-  k_dequant_cache<<<grid_for(work), kThreads, 0, stream>>>(c, s, seq, keys, values);
+  if (reinterpret_cast<uintptr_t>(keys) % 16 != 0 || reinterpret_cast<uintptr_t>(values) % 16 != 0) {
+    k_dequant_cache_elem<<<grid_for(work * 4 * c.geo.units), kThreads, 0, stream>>>(c, s, seq, keys, values);
+    return hipGetLastError();
+  }
+  const unsigned slices = static_cast<unsigned>(std::min<uint64_t>((work + kThreads - 1) / kThreads, 4096));
+  k_dequant_cache<<<dim3(slices, std::min(c.geo.units, 65535u)), kThreads, 0, stream>>>(c, s, seq, keys, values);
   return hipGetLastError();
 }
 
