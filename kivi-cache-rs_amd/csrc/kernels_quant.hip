@@ -749,13 +749,15 @@ __global__ void __launch_bounds__(kThreads)
     const uint32_t d0 = static_cast<uint32_t>(r - t * q4) * 4;
     float k[4], v[4];
     if (t < s.kq) {
+      // one code word holds the four channels (ppw >= 4); their (scale, zero) pairs are 32
+      // contiguous bytes
+      const uint32_t word = kc[t * kw + d0 / ppw];
+      const float4* pp = reinterpret_cast<const float4*>(kp + (t / G) * D + d0);
+      const float4 p01 = pp[0], p23 = pp[1];
+      const float sc[4] = {p01.x, p01.z, p23.x, p23.z}, zr[4] = {p01.y, p01.w, p23.y, p23.w};
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t d = d0 + e;
-        const uint32_t word = kc[t * kw + d / ppw];
-        const float2 sz = kp[(t / G) * D + d];
-        k[e] = fmaf(static_cast<float>((word >> code_shift(bits, d % ppw)) & mask), sz.x, sz.y);
-      }
+      for (int e = 0; e < 4; ++e)
+        k[e] = fmaf(static_cast<float>((word >> code_shift(bits, (d0 + e) % ppw)) & mask), sc[e], zr[e]);
     } else {
       const float4 x = *reinterpret_cast<const float4*>(c.kres + ((uint64_t)unit * R + (t - s.kq)) * D + d0);
       k[0] = x.x; k[1] = x.y; k[2] = x.z; k[3] = x.w;
@@ -764,11 +766,10 @@ __global__ void __launch_bounds__(kThreads)
       const uint64_t tb = t / kValueBlock;
       const uint32_t tt = static_cast<uint32_t>(t % kValueBlock);
       const uint32_t sh = code_shift(bits, tt % ppw);
+      const float2 sz = vp[(tb * ncg + d0 / G) * kValueBlock + tt];  // one group holds the four (G % 4 == 0)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const uint32_t d = d0 + e;
-        const uint32_t word = vc[(tb * D + d) * vw + tt / ppw];
-        const float2 sz = vp[(tb * ncg + d / G) * kValueBlock + tt];
+        const uint32_t word = vc[(tb * D + d0 + e) * vw + tt / ppw];
         v[e] = fmaf(static_cast<float>((word >> sh) & mask), sz.x, sz.y);
       }
     } else {
