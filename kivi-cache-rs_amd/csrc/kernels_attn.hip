@@ -26,6 +26,7 @@
 #include "kivi.h"
 
 #include <algorithm>
+#include <mutex>
 
 namespace kivi {
 namespace {
@@ -2060,14 +2061,14 @@ hipError_t launch_shared(const AttnArgs& a, const SessionTable& t, hipStream_t s
     if (e != hipSuccess) return e;
   }
   if (a.nsplit_fast == 0) return hipSuccess;
-  static bool configured = false;  // the attribute is per kernel and per process
-  if (!configured) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_shared<BITS>),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize,
-                                             static_cast<int>(kShLdsBytes));
-    if (e != hipSuccess) return e;
-    configured = true;
-  }
+  // the attribute is per kernel and per process: set once, under any number of threads
+  static std::once_flag once;
+  static hipError_t configured = hipSuccess;
+  std::call_once(once, [] {
+    configured = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_shared<BITS>),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kShLdsBytes));
+  });
+  if (configured != hipSuccess) return configured;
   const uint32_t rblocks = (a.nsess * a.gq + kShRows - 1) / kShRows;
   k_attn_shared<BITS><<<a.units * rblocks * a.nsplit_fast, kShThreads, kShLdsBytes, stream>>>(a);
   return hipGetLastError();
