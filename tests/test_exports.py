@@ -69,6 +69,25 @@ def test_cache_device_exports_match_oracle(amd, oracle, case):
         dev.free()
 
 
+@pytest.mark.gpu
+def test_cache_dequantize_device_unaligned_outputs(amd, oracle):
+    """Output arrays that are not 16-byte aligned take the one-element-per-thread kernel: the
+    same bits as the oracle."""
+    bits, group, residual, batch, heads, dim, seq = 4, 32, 64, 1, 2, 128, 333
+    ca = _state_cache(amd, bits, group, residual, batch, heads, dim, seq, 21)
+    co = _state_cache(oracle, bits, group, residual, batch, heads, dim, seq, 21)
+    dev = DeviceArrays()
+    try:
+        n = batch * heads * seq * dim
+        base_k, base_v = dev.empty(n + 1), dev.empty(n + 1)
+        ca.dequantize_device(base_k + 4, n, base_v + 4, n)  # one float past the allocation start
+        ok, ov = co.dequantize()
+        assert np.array_equal(dev.download(base_k, n + 1)[1:].view(np.uint32), ok.view(np.uint32))
+        assert np.array_equal(dev.download(base_v, n + 1)[1:].view(np.uint32), ov.view(np.uint32))
+    finally:
+        dev.free()
+
+
 QUANT_CASES = [
     # per_channel, bits, group, batch, heads, tokens, dim
     (True, 2, 32, 2, 3, 256, 128),
