@@ -27,7 +27,8 @@ record matches this kernel, workload and byte count.
 
 Other workloads (a line each, same contract): --config c0 (the reference's CPU-runnable case),
 c1 (streaming decode: a step is RuntimeKv::decode = append one token + attention, after an
-8192-token prefill; warmup + 2*steps <= 512), c3_4 / c3_8 (4-/8-bit at 131072 tokens, GQA 8),
+8192-token prefill; warmup + 2*steps <= 512; its line also times one QualityGuard check,
+`guard`), c3_4 / c3_8 (4-/8-bit at 131072 tokens, GQA 8),
 c4 (64 RagSessions over one 65536-token prefix, one batched call per step).
 
 Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--config c2] [--no-cpu]
@@ -208,6 +209,43 @@ def cpu_baseline_decode(kivi, cfg_tuple, target_s=10.0):
         "ms_per_step": per_step * 1e3,
         "cpu": _cpu_model(),
     }
+
+
+def guard_check(kivi, amd, cfg_tuple):
+    """QualityGuard (src/guard.rs) on the streaming-decode shape: after a guarded prefill of
+    the workload's tokens, one append of R tokens makes exactly one key flush and one check
+    (cache attention and fp32 attention over the whole tape on the GPU, cosine on the host).
+    Timed against the plain cache doing the same append and one attention. Host-pointer API:
+    the times include the PCIe copies of the R new rows, the query and the outputs."""
+    batch, heads, qh, dim, seq, bits, G, R, _ = cfg_tuple
+    rng = np.random.default_rng(11)
+    cfg = kivi.KiviConfig(bits, G, R)
+    keys = rng.standard_normal((batch, heads, seq + 2 * R, dim), dtype=np.float32)
+    values = rng.standard_normal((batch, heads, seq + 2 * R, dim), dtype=np.float32)
+    query = rng.standard_normal((batch, qh, dim), dtype=np.float32)
+    scale = 1.0 / math.sqrt(dim)
+    pre_k, pre_v = np.ascontiguousarray(keys[:, :, :seq]), np.ascontiguousarray(values[:, :, :seq])
+    mid_k, mid_v = np.ascontiguousarray(keys[:, :, seq:seq + R]), np.ascontiguousarray(values[:, :, seq:seq + R])
+    new_k, new_v = np.ascontiguousarray(keys[:, :, seq + R:]), np.ascontiguousarray(values[:, :, seq + R:])
+    guard = kivi.QualityGuard(amd, cfg, batch, heads, dim, 0.0, kivi.QualityPolicy.RaiseBits, 8, R)
+    guard.append(pre_k, pre_v, seq, query, qh, scale)
+    guard.append(mid_k, mid_v, R, query, qh, scale)  # untimed: the tape grows past seq here
+    plain = kivi.KiviCache(amd, cfg, batch, heads, dim)
+    plain.append(pre_k, pre_v, seq)
+    plain.append(mid_k, mid_v, R)
+    t0 = time.perf_counter()
+    checks = guard.append(new_k, new_v, R, query, qh, scale)
+    t_guard = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    plain.append(new_k, new_v, R)
+    plain.attention(query, qh, scale)
+    t_plain = time.perf_counter() - t0
+    log(f"[bench] guarded append of {R} tokens with {len(checks)} check(s): {t_guard * 1e3:.2f} ms "
+        f"(plain append + attention {t_plain * 1e3:.2f} ms)")
+    return {"append_tokens": R, "checks": len(checks), "tape_tokens": seq + 2 * R,
+            "cosine": checks[0].cosine if checks else None,
+            "guarded_ms": t_guard * 1e3, "plain_append_attention_ms": t_plain * 1e3,
+            "note": "host-pointer API, PCIe copies included"}
 
 
 def _cpu_model():
@@ -566,6 +604,8 @@ def main():
         "quantize_kernels": quant_kernels,
         "exports": exports,
     }
+    if decode_steps:
+        result["guard"] = guard_check(kivi, amd, CONFIGS[args.config])
     if not args.no_cpu:
         log("[bench] CPU baseline (oracle, 1 thread) ...")
         if sessions_cfg:
