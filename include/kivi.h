@@ -211,8 +211,8 @@ kivi_status kivi_cache_reserve(kivi_cache* cache, size_t tokens, kivi_error* err
 
 /* Extension, arena sizing (the device counterpart of the byte model of src/budget.rs:317-347,
    which counts occupied bytes): HBM a cache holds, packed arenas at their capacity plus the
-   fp32 key residual and value window and the per-unit counters (attention scratch, sized per
-   call, is not counted). kivi_cache_device_bytes reads a live cache; kivi_plan_device_bytes
+   fp32 key residual and value window and the per-unit scale maxima (attention scratch, sized
+   per call, is not counted). kivi_cache_device_bytes reads a live cache; kivi_plan_device_bytes
    gives what a cache of that shape holds after kivi_cache_reserve(tokens) (config checked as
    kivi_cache_new checks it). */
 size_t kivi_cache_device_bytes(const kivi_cache* cache);

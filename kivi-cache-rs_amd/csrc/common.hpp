@@ -1,5 +1,5 @@
 // common.hpp — device layout of the KIVI cache in HBM and the launch interface shared by
-// the HIP kernels (kernels_*.hip) and the host state machine (cache.cpp).
+// the HIP kernels (kernels_*.hip) and the host state machine (host.cpp).
 //
 // Per (batch, kv_head) "unit" the cache holds four packed arrays, each with a fixed
 // per-unit capacity of `cap` tokens (cap is a multiple of lcm(64, G)):
@@ -40,6 +40,31 @@ constexpr uint32_t kValueBlock = 64;  // tokens per value code block
 // Bit offset of element i (0 <= i < 32/bits) inside a native code word.
 __host__ __device__ inline uint32_t code_shift(uint32_t bits, uint32_t i) {
   return bits == 2 ? 4u * (i & 7u) + 2u * (i >> 3) : 8u * (i & 3u) + bits * (i >> 2);
+}
+
+// Sign of a zero group minimum. The reference takes minima with f32::min in element order
+// (src/quant.rs:303 over a group's tokens, :356 over its channels), which on x86-64 is minss
+// with the running minimum as the operand passed through on ties: a group whose minimum is
+// zero keeps the sign of its FIRST zero (+0 and -0 compare equal, so a later zero never
+// replaces an earlier one). Its stored `zero` carries that sign. The quantize kernels find
+// the minimum's value with reductions in any order, and when it is zero (rare) fix its sign
+// with one of these. first_zero scans n elements `stride` apart in element order.
+__host__ __device__ inline float first_zero(const float* p, uint64_t stride, uint32_t n) {
+  for (uint32_t i = 0; i < n; ++i) {
+    const float x = p[i * stride];
+    if (x == 0.f) return x;
+  }
+  return 0.f;
+}
+// One element per lane, aligned groups of L lanes in element order (L a power of two <= 64;
+// every lane of the wave active): the group's first zero (0.f when it has none).
+__device__ inline float lane_group_first_zero(float x, uint32_t L) {
+  const uint32_t lane = __lane_id();
+  const uint32_t base = lane & ~(L - 1u);
+  const uint64_t zeros = __ballot(x == 0.f);
+  const uint64_t mine = L == 64 ? zeros : (zeros >> base) & ((1ull << L) - 1ull);
+  const float z = __shfl(x, static_cast<int>(base + (mine ? __ffsll(static_cast<long long>(mine)) - 1 : 0)));
+  return mine ? z : 0.f;
 }
 
 struct Geometry {
@@ -196,9 +221,6 @@ struct AttnProblem {
   uint32_t heads;            // kv heads
   uint32_t batch;
   float scale;
-  // [units] split counters, zero between calls (calls sharing them must not overlap on the
-  // device), or null to merge in a separate launch
-  uint32_t* counters;
   // RuntimeKv::decode in one attention launch (null pend_k otherwise): `st` and `seq` already
   // count a decode token whose key and value rows are pend_k / pend_v ([units][D]). The merge
   // writes them to residual slot pend_kslot and window slot pend_vslot afterwards; with

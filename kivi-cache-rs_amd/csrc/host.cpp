@@ -420,8 +420,9 @@ struct CacheCore {
         seq += 1;
         return Status{};
       }
+      // hipErrorNotSupported: a shape the one-launch append does not cover, refused before
+      // any launch (so HIP's last-error state is untouched); the general path below runs
       if (e != hipErrorNotSupported) HIP_TRY(e, "decode append");
-      (void)hipGetLastError();  // unsupported shape: the general path below
     }
     const RowSource kin{keys, n * D, 0, 0};
     // ---- keys: fill the residual, flush every R tokens, quantize whole R-blocks of the
@@ -558,12 +559,11 @@ size_t compressed_bytes(const kivi_memory_report& r) {
          r.key_residual_bytes + r.value_residual_bytes;
 }
 
-// Split counters and workspace of one attention target (a cache or a session). Two calls
-// sharing them must not overlap on the device: calls on one stream are ordered by the stream;
-// when a call comes on another stream, an event recorded at that moment on the previous
-// call's stream is waited for first (no per-call event, which would stall the queue).
+// Workspace of one attention target (a cache or a session). Two calls sharing it must not
+// overlap on the device: calls on one stream are ordered by the stream; when a call comes on
+// another stream, an event recorded at that moment on the previous call's stream is waited
+// for first (no per-call event, which would stall the queue).
 struct AttnSync {
-  DevBuf counters;
   DevBuf workspace;  // split partials, grown on demand
   hipEvent_t done = nullptr;
   bool used = false;
@@ -575,8 +575,7 @@ struct AttnSync {
   ~AttnSync() {
     if (done != nullptr) (void)hipEventDestroy(done);
   }
-  Status init(size_t units, hipStream_t s) {
-    KIVI_TRY(counters.alloc_zero(units * sizeof(uint32_t), s, "attention counters"));
+  Status init() {
     HIP_TRY(hipEventCreateWithFlags(&done, hipEventDisableTiming), "attention event");
     return Status{};
   }
@@ -637,7 +636,6 @@ Status attend(const CacheCore& core, AttnSync& sync, const float* suffix_k, cons
   p.heads = static_cast<uint32_t>(core.heads);
   p.batch = static_cast<uint32_t>(core.batch);
   p.scale = scale;
-  p.counters = sync.counters.as<uint32_t>();
   std::lock_guard<std::mutex> lock(sync.mu);
   KIVI_TRY(sync.reserve(attention_workspace_floats(p) * sizeof(float)));
   KIVI_TRY(sync.before(s));
@@ -728,7 +726,7 @@ Status create_cache(const kivi_config* config, size_t batch, size_t heads, size_
   c->core.head_dim = head_dim;
   c->core.device = dev;
   KIVI_TRY(c->core.init(nullptr));
-  KIVI_TRY(c->attn.init(c->core.units(), nullptr));
+  KIVI_TRY(c->attn.init());
   return sync(nullptr, "cache init");
 }
 
@@ -765,7 +763,7 @@ Status cache_attention(const kivi_cache* c, const float* query, size_t query_len
   KIVI_TRY(need_slice(query, query_len, "query"));
   KIVI_TRY(need_slice(out, out_len, "out"));
   DeviceScope scope(core.device);
-  kivi_cache* mc = const_cast<kivi_cache*>(c);  // counters only; the cache itself is read
+  kivi_cache* mc = const_cast<kivi_cache*>(c);  // its workspace only; the cache itself is read
   if (device) return attend(core, mc->attn, nullptr, nullptr, 0, 0, query, num_q_heads, scale, out, stream);
   hipStream_t s = core.stream;
   Scratch dq, dout;
@@ -886,7 +884,6 @@ Status decode_fused(kivi_cache* c, const float* key, size_t key_len, const float
   p.heads = static_cast<uint32_t>(core.heads);
   p.batch = static_cast<uint32_t>(core.batch);
   p.scale = scale;
-  p.counters = c->attn.counters.as<uint32_t>();
   p.pend_k = key;
   p.pend_v = value;
   p.pend_kslot = core.kres_len;
@@ -923,7 +920,7 @@ Status session_attend(const kivi_session* se, const float* query, size_t query_l
   KIVI_TRY(need_slice(out, out_len, "out"));
   DeviceScope scope(core.device);
   const uint64_t stride = se->cap * core.head_dim;
-  kivi_session* ms = const_cast<kivi_session*>(se);  // counters only
+  kivi_session* ms = const_cast<kivi_session*>(se);  // its workspace only
   if (device)
     return attend(core, ms->attn, se->keys.as<float>(), se->values.as<float>(), se->len, stride,
                   query, num_q_heads, scale, out, stream);
@@ -1045,7 +1042,7 @@ Status batched_sessions(const kivi_session* const* sessions, size_t n, const flo
     KIVI_TRY(sync_.after(s));
   } else {
     for (size_t i = 0; i < n; ++i) {
-      kivi_session* se = const_cast<kivi_session*>(sessions[i]);  // counters only
+      kivi_session* se = const_cast<kivi_session*>(sessions[i]);  // its workspace only
       KIVI_TRY(attend(core, se->attn, se->keys.as<float>(), se->values.as<float>(), se->len,
                       se->cap * core.head_dim, dq + i * per, num_q_heads, scale, dout + i * per, s));
     }
@@ -1462,7 +1459,7 @@ kivi_status kivi_cache_reserve(kivi_cache* cache, size_t tokens, kivi_error* err
 }
 
 size_t kivi_cache_device_bytes(const kivi_cache* cache) {
-  return cache ? cache->core.device_bytes() + cache->attn.counters.bytes : 0;
+  return cache ? cache->core.device_bytes() : 0;
 }
 
 kivi_status kivi_plan_device_bytes(const kivi_config* config, size_t batch, size_t num_kv_heads,
@@ -1483,7 +1480,7 @@ kivi_status kivi_plan_device_bytes(const kivi_config* config, size_t batch, size
     core.head_dim = head_dim;
     core.set_geometry();
     if (tokens > 0) core.geo.cap = core.capacity_for(tokens);
-    *out = core.device_bytes() + core.units() * sizeof(uint32_t);
+    *out = core.device_bytes();
     return Status{};
   });
 }
@@ -1499,7 +1496,7 @@ kivi_status kivi_cache_share_prefix(const kivi_cache* cache, kivi_prefix** out, 
     // dequantizes those into range-scaled f16 operands)
     HIP_TRY(launch_raise_row_max(st->core.view(), st->core.kres_len, st->core.vres_len, st->core.vhead,
                                  cache->core.stream), "prefix row maxima");
-    KIVI_TRY(st->batch.init(st->core.units(), cache->core.stream));
+    KIVI_TRY(st->batch.init());
     KIVI_TRY(sync(cache->core.stream, "share_prefix"));
     st->prefix_bytes = compressed_bytes(st->core.memory());
     auto p = std::make_unique<kivi_prefix>();
@@ -1559,7 +1556,7 @@ kivi_status kivi_prefix_session(kivi_prefix* prefix, kivi_session** out, kivi_er
     auto s = std::make_unique<kivi_session>();
     {
       DeviceScope scope(prefix->state->core.device);
-      KIVI_TRY(s->attn.init(prefix->state->core.units(), nullptr));
+      KIVI_TRY(s->attn.init());
       KIVI_TRY(sync(nullptr, "session init"));
     }
     s->prefix = kivi_prefix_retain(prefix);
@@ -1693,7 +1690,7 @@ kivi_status kivi_guard_new(const kivi_config* config, size_t batch, size_t num_k
     auto g = std::make_unique<kivi_guard>();
     auto c = std::make_unique<kivi_cache>();
     KIVI_TRY(create_cache(config, batch, num_kv_heads, head_dim, c.get()));
-    KIVI_TRY(g->dense.init(c->core.units(), nullptr));
+    KIVI_TRY(g->dense.init());
     KIVI_TRY(need(out, "out"));
     g->cache = c.release();
     g->threshold = threshold;

@@ -73,7 +73,6 @@ struct AttnArgs {
   uint64_t t_min;
   uint32_t gemm_end;
   uint64_t q_sess_stride, ws_sess_stride;
-  uint32_t* counters;      // [units] finished splits (0 between calls), or null: separate merge
   float* out;              // [batch][QH][D]
   uint32_t units;
   // A decode token appended by this launch (RuntimeKv::decode in one launch; null otherwise):
@@ -157,16 +156,6 @@ __device__ __forceinline__ float warp_sum(float v) {
   return v;
 }
 
-// Split partials are exchanged between workgroups that may sit on different XCDs (separate
-// L2s): they are written and read with device-coherent (agent-scope) accesses, so the merge
-// needs no L2 write-back or invalidation.
-__device__ __forceinline__ void store_partial(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float load_partial(const float* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 // ------------------------------------------------------------------ generic splits
 // One workgroup per (unit, split) over tokens [t_begin, total). LDS: q [gq][D], logits/weights
 // [gq][S]. Instantiated for every shape (BITS = DD = GG = 0) and, with the shape fixed, for the
@@ -238,8 +227,8 @@ __device__ __forceinline__ void generic_split(const AttnArgs& a, uint32_t unit, 
     }
     l = warp_sum(l);
     if (lane == 0) {
-      store_partial(part + h * (D + 2) + D, m);
-      store_partial(part + h * (D + 2) + D + 1, l);
+      part[h * (D + 2) + D] = m;
+      part[h * (D + 2) + D + 1] = l;
     }
   }
   __syncthreads();
@@ -264,73 +253,8 @@ __device__ __forceinline__ void generic_split(const AttnArgs& a, uint32_t unit, 
     }
 #pragma unroll
     for (int h = 0; h < kHeadsPerPass; ++h)
-      if (h < (int)nh) store_partial(part + (h0 + h) * (D + 2) + d, acc[h]);
+      if (h < (int)nh) part[(h0 + h) * (D + 2) + d] = acc[h];
   }
-}
-
-// Log-sum-exp merge of one unit's split partials into out: wave w merges heads w, w+4, ...
-// with wave-local reductions (LDS: nsplit factors per wave). Each split's (m, l) pair is read
-// once, then its D accumulators, so a head costs two rounds of loads.
-__device__ void merge_unit(const float* ws, uint32_t unit, uint32_t nsplit, uint32_t gq, uint32_t D,
-                           uint32_t heads, uint32_t qh, float* out, float* f_lds) {
-  const uint32_t b = unit / heads, kvh = unit % heads;
-  const uint32_t lane = threadIdx.x % 64, wave = threadIdx.x / 64, nwave = blockDim.x / 64;
-  const uint64_t stride = (uint64_t)gq * (D + 2);
-  float* fw = f_lds + wave * nsplit;
-  for (uint32_t h = wave; h < gq; h += nwave) {
-    const float* base = ws + (uint64_t)unit * nsplit * stride + h * (D + 2);
-    float m = -INFINITY;
-    for (uint32_t s = lane; s < nsplit; s += 64) {
-      const float ms = load_partial(base + s * stride + D);
-      fw[s] = ms;
-      m = fmaxf(m, ms);
-    }
-    const float M = warp_max(m);
-    float l = 0.f;
-    for (uint32_t s = lane; s < nsplit; s += 64) {
-      const float ms = fw[s];
-      const float f = ms == -INFINITY ? 0.f : exp2f(ms - M);
-      fw[s] = f;
-      l += load_partial(base + s * stride + D + 1) * f;
-    }
-    const float inv = 1.0f / warp_sum(l);
-    float* o = out + ((uint64_t)b * qh + kvh * gq + h) * D;
-    constexpr uint32_t kBatch = 16;  // splits per round of independent loads
-    for (uint32_t d = lane; d < D; d += 64) {
-      float acc = 0.f;
-      for (uint32_t s0 = 0; s0 < nsplit; s0 += kBatch) {
-        float v[kBatch];
-#pragma unroll
-        for (uint32_t j = 0; j < kBatch; ++j) {
-          const uint32_t s = s0 + j < nsplit ? s0 + j : 0u;
-          v[j] = load_partial(base + s * stride + d);
-        }
-#pragma unroll
-        for (uint32_t j = 0; j < kBatch; ++j)
-          if (s0 + j < nsplit) acc = fmaf(v[j], fw[s0 + j], acc);
-      }
-      o[d] = acc * inv;
-    }
-  }
-}
-
-// Called by every split workgroup after its partial is written (agent-scope stores): each
-// thread waits until its stores are acknowledged, then one thread counts the split in with an
-// agent-scope atomic. The last of the unit's splits to arrive merges the unit (agent-scope
-// loads) and re-arms the counter.
-__device__ void finish_split(const AttnArgs& a, uint32_t unit, float* lds) {
-  __shared__ uint32_t is_last;
-  __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed
-  __syncthreads();
-  if (threadIdx.x == 0)
-    is_last = __hip_atomic_fetch_add(&a.counters[unit], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                      a.nsplit_total - 1
-                  ? 1u
-                  : 0u;
-  __syncthreads();
-  if (is_last == 0u) return;
-  merge_unit(a.ws, unit, a.nsplit_total, a.gq, a.c.geo.D, a.heads, a.qh, a.out, lds);
-  if (threadIdx.x == 0) __hip_atomic_store(&a.counters[unit], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int BITS, int DD, int GG>
@@ -338,10 +262,6 @@ __global__ void __launch_bounds__(kThreads) k_attn_generic(AttnArgs a) {
   extern __shared__ float lds[];
   const uint32_t unit = blockIdx.x / a.nsplit_gen;
   generic_split<BITS, DD, GG>(a, unit, blockIdx.x % a.nsplit_gen, lds);
-  if (a.counters != nullptr) {
-    __syncthreads();
-    finish_split(a, unit, lds);
-  }
 }
 
 // ------------------------------------------------------------------ MFMA splits
@@ -797,6 +717,8 @@ __device__ __forceinline__ void evict_groups(EvictRow& e, float levels, float& s
       mn = fminf(mn, __shfl_xor(mn, o));
       mx = fmaxf(mx, __shfl_xor(mx, o));
     }
+    const float fz = lane_group_first_zero(e.x[hv], 32);  // a zero minimum: the first zero's sign
+    if (mn == 0.f) mn = fz;
     const float span = mx - mn;
     e.mn[hv] = mn;
     e.sc[hv] = span == 0.0f ? 0.0f : span / levels;
@@ -1103,13 +1025,13 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
         v += (d == D + 1 ? c[D + 1] : c[d]) * f;
       }
     }
-    store_partial(part + h * (D + 2) + d, v);
+    part[h * (D + 2) + d] = v;
   }
 }
 
 // Chunk launch: workgroups [0, units*nsplit_win) take one window / suffix chunk each (MIXED
-// path, started first), the rest a split of 4*kFastCpw packed chunks; with counters, the
-// last split of each unit merges it.
+// path, started first), the rest a split of 4*kFastCpw packed chunks. Every split writes its
+// partial with plain stores; the merge launch that follows on the stream reads them.
 //
 // Resident workgroups per CU asked of the register allocator per instantiation (4-wave
 // workgroups, so also waves per SIMD): it then packs the 4-bit GQA-4 kernel into 128 VGPRs
@@ -1119,18 +1041,11 @@ __global__ void __launch_bounds__(kThreads, (NRS == 1 && BITS <= 4) ? 4 : (BITS 
     k_attn_mfma(AttnArgs a) {
   extern __shared__ float lds[];
   const uint32_t nwin = a.units * a.nsplit_win;
-  uint32_t unit;
   if (blockIdx.x < nwin) {
-    unit = blockIdx.x / a.nsplit_win;
-    mfma_split<BITS, NRS, 1, true>(a, unit, blockIdx.x % a.nsplit_win, lds);
+    mfma_split<BITS, NRS, 1, true>(a, blockIdx.x / a.nsplit_win, blockIdx.x % a.nsplit_win, lds);
   } else {
     const uint32_t blk = blockIdx.x - nwin;
-    unit = blk / a.nsplit_fast;
-    mfma_split<BITS, NRS, fast_cpw(BITS, NRS), false>(a, unit, blk % a.nsplit_fast, lds);
-  }
-  if (a.counters != nullptr) {
-    __syncthreads();
-    finish_split(a, unit, lds);
+    mfma_split<BITS, NRS, fast_cpw(BITS, NRS), false>(a, blk / a.nsplit_fast, blk % a.nsplit_fast, lds);
   }
 }
 
@@ -1801,13 +1716,6 @@ __global__ void __launch_bounds__(kShThreads) k_attn_shared(AttnArgs a) {
 
 // ------------------------------------------------------------------ planning
 
-constexpr size_t kMaxMergeLds = 48 * 1024;  // in-kernel merge up to ~12K splits per unit
-// In-kernel merge: 0 never, 1 always, 2 when the launch is a single round of workgroups. It
-// measured slower at C2 (137 us kernel vs 122 + 8.5 us for the two launches): every split
-// then waits for its stores and a device-scope atomic before it retires, and the last split
-// of a unit merges on the critical path.
-constexpr int kUseInKernelMerge = 0;
-
 uint32_t split_tokens(uint32_t gq) {
   uint32_t s = 256;
   while (s > 32 && (uint64_t)gq * s > 8192) s >>= 1;
@@ -1872,11 +1780,6 @@ AttnArgs make_args(const AttnProblem& p, float* ws) {
   a.t_min = 0;
   a.gemm_end = 0;
   a.q_sess_stride = a.ws_sess_stride = 0;
-  // With kUseInKernelMerge the last split of each unit merges it in the same launch (partials
-  // exchanged through agent-scope accesses, no L2 write-back or invalidation).
-  const bool in_kernel = kUseInKernelMerge == 1 ||
-                         (kUseInKernelMerge == 2 && (uint64_t)a.units * a.nsplit_total <= kFastGroups);
-  a.counters = in_kernel && (size_t)4 * a.nsplit_total * sizeof(float) <= kMaxMergeLds ? p.counters : nullptr;
   return a;
 }
 
@@ -1885,8 +1788,7 @@ hipError_t launch_fast(const AttnArgs& a, double bytes, hipStream_t stream) {
   constexpr int NH = 4 * NRS;
   const size_t logits = (size_t)4 * NH * ((a.nsplit_fast > 0 ? fast_cpw(BITS, NRS) : 1) * 64 + kRowPad);
   const size_t combine = (size_t)4 * NH * (128 + 2);
-  const size_t merge = a.counters != nullptr ? (size_t)4 * a.nsplit_total : 0;
-  const size_t lds = std::max(std::max(logits, combine), merge) * sizeof(float);
+  const size_t lds = std::max(logits, combine) * sizeof(float);
   TimedLaunch timed(KIVI_KERNEL_ATTN_PACKED, stream, bytes);
   k_attn_mfma<BITS, NRS><<<a.units * (a.nsplit_win + a.nsplit_fast), kThreads, lds, stream>>>(a);
   return hipGetLastError();
@@ -1906,8 +1808,7 @@ hipError_t dispatch_fast(const AttnArgs& a, double bytes, hipStream_t stream) {
 }
 
 hipError_t dispatch_generic(const AttnArgs& a, hipStream_t stream) {
-  const size_t merge = a.counters != nullptr ? (size_t)4 * a.nsplit_total : 0;
-  const size_t lds = std::max((size_t)a.gq * a.c.geo.D + (size_t)a.gq * a.S, merge) * sizeof(float);
+  const size_t lds = ((size_t)a.gq * a.c.geo.D + (size_t)a.gq * a.S) * sizeof(float);
   k_attn_generic<0, 0, 0><<<a.units * a.nsplit_gen, kThreads, lds, stream>>>(a);
   return hipGetLastError();
 }
@@ -1915,7 +1816,6 @@ hipError_t dispatch_generic(const AttnArgs& a, hipStream_t stream) {
 }  // namespace
 
 bool attention_fuses_decode(const AttnProblem& p) {
-  if (kUseInKernelMerge != 0) return false;  // the merge launch writes the token's rows
   const AttnArgs a = make_args(p, nullptr);
   return a.total > 0 && a.nsplit_gen == 0 && (a.nsplit_fast > 0 || a.nsplit_win > 0);
 }
@@ -1935,7 +1835,6 @@ hipError_t launch_attention(const AttnProblem& p, float* workspace, hipStream_t 
   const double val_tok = g.D * g.bits / 8.0 + g.ncg() * 8.0;
   const double row = g.D * 4.0;
   const double q_bytes = (double)units * a.gq * g.D * 4.0;
-  const double out_bytes = a.counters != nullptr ? q_bytes : 0.0;  // the merge writes out
   const uint64_t t0 = a.t_begin, kq = p.st.kq, vq = p.st.vq;
   const double kp = kq > t0 ? (double)(kq - t0) : 0.0, vp = vq > t0 ? (double)(vq - t0) : 0.0;
   const double kd = (double)(p.seq - std::max(kq, t0)), vd = (double)(p.seq - std::max(vq, t0));
@@ -1945,23 +1844,20 @@ hipError_t launch_attention(const AttnProblem& p, float* workspace, hipStream_t 
     const double kpt = (double)std::min<uint64_t>(kq, p.seq), vpt = (double)vq;
     const double fp32_rows = (double)(p.seq - kq) + (double)(p.seq - vq) + 2.0 * p.suffix_len;
     hipError_t e = dispatch_fast(
-        a, units * (kpt * key_tok + vpt * val_tok + fp32_rows * row) + q_bytes + out_bytes, stream);
+        a, units * (kpt * key_tok + vpt * val_tok + fp32_rows * row) + q_bytes, stream);
     if (e != hipSuccess) return e;
   } else {
-    TimedLaunch timed(KIVI_KERNEL_ATTN_TAIL, stream, tail_bytes + q_bytes + out_bytes);
+    TimedLaunch timed(KIVI_KERNEL_ATTN_TAIL, stream, tail_bytes + q_bytes);
     hipError_t e = dispatch_generic(a, stream);
     if (e != hipSuccess) return e;
   }
-  if (a.counters == nullptr) {
-    const double bytes = (double)units * a.gq * ((double)a.nsplit_total * (g.D + 2) + g.D) * 4.0;
-    TimedLaunch timed(KIVI_KERNEL_ATTN_MERGE, stream, bytes);
-    PendRows pend{};
-    if (p.pend_k != nullptr)
-      pend = PendRows{p.pend_k, p.pend_v, p.cache.kres, p.cache.vring, p.pend_kslot, p.pend_vslot, g.R};
-    return launch_merge(workspace, a.nsplit_total, a.gq, g.D, p.heads, p.qh, p.out, units, 1, 0, 0,
-                        stream, pend);
-  }
-  return hipGetLastError();
+  const double bytes = (double)units * a.gq * ((double)a.nsplit_total * (g.D + 2) + g.D) * 4.0;
+  TimedLaunch timed(KIVI_KERNEL_ATTN_MERGE, stream, bytes);
+  PendRows pend{};
+  if (p.pend_k != nullptr)
+    pend = PendRows{p.pend_k, p.pend_v, p.cache.kres, p.cache.vring, p.pend_kslot, p.pend_vslot, g.R};
+  return launch_merge(workspace, a.nsplit_total, a.gq, g.D, p.heads, p.qh, p.out, units, 1, 0, 0,
+                      stream, pend);
 }
 
 namespace {
@@ -1981,7 +1877,6 @@ AttnArgs make_session_args(const SessionsProblem& sp, uint32_t nsess, uint64_t m
   p.batch = sp.batch;
   p.scale = sp.scale;
   AttnArgs a = make_args(p, ws);
-  a.counters = nullptr;
   a.nsplit_fast = (a.chunk_end + 4 * kSessCpw - 1) / (4 * kSessCpw);
   a.nsplit_total = a.nsplit_fast + a.nsplit_win + a.nsplit_gen;
   a.nsess = nsess;

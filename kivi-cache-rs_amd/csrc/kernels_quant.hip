@@ -225,6 +225,8 @@ __global__ void __launch_bounds__(256)
       mn = fminf(mn, __shfl_xor(mn, o));
       mx = fmaxf(mx, __shfl_xor(mx, o));
     }
+    const float fz = lane_group_first_zero(x, G);  // whole wave: the ballot needs every lane
+    if (mn == 0.f) mn = fz;
     const float scale = scale_of(mx - mn, levels);
     const uint32_t code = quant_code(x, mn, scale, levels);
     const uint64_t tb = vq / kValueBlock;
@@ -314,7 +316,7 @@ __global__ void __launch_bounds__(kThreads)
     float mn = INFINITY, mx = -INFINITY;
     for (uint32_t t = 0; t < G; ++t) {
       const float x = staged ? xs[t * (D + 1) + d] : rows[(uint64_t)t * D + d];
-      mn = fminf(mn, x);
+      mn = x < mn ? x : mn;  // keeps the first of equal minima (the first zero)
       mx = fmaxf(mx, x);
     }
     const float zero = mn;
@@ -378,7 +380,7 @@ __global__ void __launch_bounds__(kThreads)
       const float* grp = xs + r * (D + 1) + cg * G;
       float mn = INFINITY, mx = -INFINITY;
       for (uint32_t e = 0; e < G; ++e) {
-        mn = fminf(mn, grp[e]);
+        mn = grp[e] < mn ? grp[e] : mn;  // keeps the first of equal minima (the first zero)
         mx = fmaxf(mx, grp[e]);
       }
       const float scale = scale_of(mx - mn, levels);
@@ -487,6 +489,7 @@ __global__ void __launch_bounds__(kThreads)
         mn = fminf(mn, x[t][j]);
         mx = fmaxf(mx, x[t][j]);
       }
+      if (mn == 0.f) mn = first_zero(rows + CPL * lane + j, D, GG);  // the group's first zero
       sz[j] = make_float2(scale_of(mx - mn, levels), mn);
       inv[j] = quant_inv(sz[j].x);
       sh[j] = code_shift(BITS, (CPL * lane + j) % PPW);
@@ -571,6 +574,12 @@ __global__ void __launch_bounds__(kThreads)
           load_lane<CPL>(row, lane, x[p]);
         }
       }
+      // the row slot p loaded (both load paths above address the same row)
+      auto value_row = [&](uint32_t p) -> const float* {
+        const uint32_t pc = p < p_lo ? p_lo : p > p_hi ? p_hi : p;
+        const uint64_t i = t0 + pc - vq0;
+        return i < n_ring ? source_row(ring, unit, i, R, D) : source_row(in, unit, i - n_ring, R, D);
+      };
       uint32_t word[CPL][WPW];
 #pragma unroll
       for (int j = 0; j < CPL; ++j)
@@ -591,6 +600,7 @@ __global__ void __launch_bounds__(kThreads)
         float mn_r, mx_r;
         row_minmax16(pmn, pmx, mn_r, mx_r);
         const uint32_t r = lane % 16;
+        if (mn_r == 0.f) mn_r = first_zero(value_row(r) + cg * GG, 1, GG);  // row r's first zero
         const float scale_r = scale_of(mx_r - mn_r, levels);
         const float inv_r = quant_inv(scale_r);
         if (t0 + r >= t_lo && t0 + r < t_hi) {
@@ -617,6 +627,7 @@ __global__ void __launch_bounds__(kThreads)
 #pragma unroll
           for (int j = 1; j < CPL; ++j) minmax_with(mn, mx, x[p][j], x[p][j]);
           group_minmax<L>(mn, mx);
+          if (mn == 0.f) mn = first_zero(value_row(p) + cg * GG, 1, GG);  // row p's first zero
           const float scale = scale_of(mx - mn, levels);
           const float inv = quant_inv(scale);
           if (valid) {
@@ -841,7 +852,7 @@ __global__ void __launch_bounds__(kThreads)
     float mn = INFINITY, mx = -INFINITY;
     for (uint32_t t = 0; t < G; ++t) {
       const float x = rows[(uint64_t)t * D + d];
-      mn = fminf(mn, x);
+      mn = x < mn ? x : mn;  // keeps the first of equal minima (the first zero)
       mx = fmaxf(mx, x);
     }
     const float scale = scale_of(mx - mn, levels);
@@ -874,7 +885,7 @@ __global__ void __launch_bounds__(kThreads)
     const float* grp = data + idx * G;  // (unit*tokens + t)*D + cg*G == idx*G
     float mn = INFINITY, mx = -INFINITY;
     for (uint32_t e = 0; e < G; ++e) {
-      mn = fminf(mn, grp[e]);
+      mn = grp[e] < mn ? grp[e] : mn;  // keeps the first of equal minima (the first zero)
       mx = fmaxf(mx, grp[e]);
     }
     const float scale = scale_of(mx - mn, levels);

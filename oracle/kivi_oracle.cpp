@@ -9,7 +9,9 @@
 // Faithfulness rules (they make it bit-identical to the Rust build by construction):
 //  * every loop runs in the reference's order; f32 arithmetic only; `mul_add` is
 //    std::fma (libm fmaf, as Rust lowers it without target-cpu); `/` is IEEE division;
-//    `f32::exp` is expf; `min/max` are fminf/fmaxf (minNum/maxNum, as Rust's);
+//    `f32::exp` is expf; the quantizers' `f32::min/max` are rust_min/rust_max below, the
+//    compare-select x86-64 codegen of Rust's minnum/maxnum (NaN skipped, equal values keep
+//    the running one, so a zero minimum keeps the sign of the group's first zero);
 //  * built with -ffp-contract=off and without -ffast-math (oracle/Makefile);
 //  * error checks in the reference's order, with the reference's Display text.
 // Each function cites the reference lines it restates. The exported C API mirrors
@@ -26,6 +28,15 @@
 #include <vector>
 
 namespace {
+
+// f32::min / f32::max as the reference's x86-64 build runs them (src/quant.rs:303-304,
+// 356-357). rustc lowers them to llvm.minnum / llvm.maxnum, and LLVM's x86 lowering of
+// minnum(a, b) is minss(b, a) plus "a is NaN ? b : that": minss passes its second operand
+// through on ties and NaNs, so minnum(a, b) = b < a ? b : a (a is never NaN here: it starts at
+// +inf and only takes non-NaN values). glibc's fminf instead returns b on a tie of +0 and -0.
+// The two differ only in the sign of a zero minimum; this is the reference's.
+inline float rust_min(float acc, float x) { return x < acc ? x : acc; }
+inline float rust_max(float acc, float x) { return x > acc ? x : acc; }
 
 // ---------------------------------------------------------------- errors
 // KiviError + Display (src/error.rs:5-95).
@@ -169,8 +180,8 @@ void append_key_block(PackedStream& s, const float* data, size_t tokens, size_t 
     for (size_t t = 0; t < group_size; ++t) {
       const float* row = data + base + t * head_dim;
       for (size_t d = 0; d < head_dim; ++d) {
-        mn[d] = std::fmin(mn[d], row[d]);
-        mx[d] = std::fmax(mx[d], row[d]);
+        mn[d] = rust_min(mn[d], row[d]);
+        mx[d] = rust_max(mx[d], row[d]);
       }
     }
     for (size_t d = 0; d < head_dim; ++d) {
@@ -209,8 +220,8 @@ void append_value_block(PackedStream& s, const float* data, size_t tokens, size_
       const float* group = row + cg * group_size;
       float mn = INFINITY, mx = -INFINITY;
       for (size_t i = 0; i < group_size; ++i) {
-        mn = std::fmin(mn, group[i]);
-        mx = std::fmax(mx, group[i]);
+        mn = rust_min(mn, group[i]);
+        mx = rust_max(mx, group[i]);
       }
       const float scale = scale_of(mx - mn, levels);
       s.params.push_back(scale);

@@ -87,6 +87,14 @@ class DeviceArrays:
     def empty(self, n):
         return self.upload(np.zeros(n, np.float32))
 
+    def alloc(self, n):
+        """Device buffer of n floats, contents undefined (no host copy)."""
+        C = self._C
+        p = C.c_void_p()
+        self._ok(self._hip.hipMalloc(C.byref(p), C.c_size_t(max(4 * n, 4))), "hipMalloc")
+        self._ptrs.append(p)
+        return p.value
+
     def download(self, ptr, n):
         C = self._C
         out = np.empty(n, np.float32)
@@ -99,3 +107,25 @@ class DeviceArrays:
         for p in self._ptrs:
             self._hip.hipFree(p)
         self._ptrs = []
+
+
+def reference_minimum(x, axis):
+    """Group minima as the reference's f32::min takes them in element order along ``axis``
+    (src/quant.rs:303, 356): the minimum's value, and for a zero minimum the sign of the
+    first zero (+0 and -0 compare equal, so the running minimum keeps the first)."""
+    x = np.asarray(x, np.float32)
+    mn = x.min(axis=axis)
+    first = np.argmax(x == 0, axis=axis)
+    fz = np.take_along_axis(x, np.expand_dims(first, axis), axis).squeeze(axis)
+    return np.where(mn == 0, fz, mn).astype(np.float32)
+
+
+def signed_zero_rows(rng, shape, p=0.25):
+    """|N(0,1)| with zeros of random sign planted at rate p: nearly every group of 16+
+    elements then has a zero minimum and zeros of both signs."""
+    x = np.abs(rng.standard_normal(shape)).astype(np.float32)
+    z = rng.random(shape) < p
+    neg = rng.random(shape) < 0.5
+    x[z & neg] = np.float32(-0.0)
+    x[z & ~neg] = np.float32(0.0)
+    return x

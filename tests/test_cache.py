@@ -6,7 +6,7 @@ import numpy as np
 import pytest
 
 from kivi import KiviCache, KiviConfig, KiviError, quantize_per_channel, quantize_per_token
-from helpers import fill, slice_tokens
+from helpers import fill, reference_minimum, signed_zero_rows, slice_tokens
 
 
 def config(backend):
@@ -307,3 +307,44 @@ def test_no_config_can_loop_forever(backend):
     for bad in (KiviConfig(2, 0, 32), KiviConfig(3, 32, 32), KiviConfig(2, 32, 0)):
         with pytest.raises(KiviError):
             KiviCache(backend, bad, 1, 1, 32)
+
+
+ZERO_SCHEDULES = {"bulk": [300], "decode": [3] + [1] * 140, "mixed": [37, 1, 64, 1, 1, 130, 7, 1, 1, 60]}
+
+
+@pytest.mark.parametrize("dim,group", [(128, 32), (128, 64), (256, 32), (64, 16), (96, 32)])
+@pytest.mark.parametrize("schedule", list(ZERO_SCHEDULES))
+def test_zero_minima_follow_the_first_zero_on_every_schedule(backend, dim, group, schedule):
+    """Keys and values whose groups have zero minima with zeros of both signs, appended in
+    bulk, token by token (window evictions) and in mixed chunks: every stored zero is the
+    group's first zero in element order (src/quant.rs:303, 356), so the streams are the same
+    bit for bit whatever the schedule (src/cache.rs:182-185). The shapes take each
+    quantize path: lane-register reductions with 1, 2 or 4 channels per lane, 8 to 32 lanes
+    per value group, and the LDS-staged kernels (head_dim 96)."""
+    bits, residual = 2, 2 * group
+    batch, heads = 1, 2
+    chunks = ZERO_SCHEDULES[schedule]
+    total = sum(chunks)
+    rng = np.random.default_rng(dim + group)
+    keys = signed_zero_rows(rng, (batch, heads, total, dim))
+    keys[:, 1, :, 2::5] -= 1.0  # some channels with negative minima
+    values = signed_zero_rows(rng, (batch, heads, total, dim))
+    values[:, 0, ::7, 1] = -2.0  # some tokens with negative minima
+    cache = KiviCache(backend, KiviConfig(bits, group, residual), batch, heads, dim)
+    off = 0
+    for n in chunks:
+        cache.append(np.ascontiguousarray(keys[:, :, off:off + n]), np.ascontiguousarray(values[:, :, off:off + n]), n)
+        off += n
+    kq, vq = cache.quantized_key_tokens(), cache.quantized_value_tokens()
+    assert kq > 0 and vq > 0
+    _, kp, _, vp = cache.export_streams()
+    units = batch * heads
+    want_k = reference_minimum(keys.reshape(units, total, dim)[:, :kq].reshape(units, kq // group, group, dim), axis=2)
+    got_k = kp.reshape(units, kq // group, dim, 2)[..., 1]
+    np.testing.assert_array_equal(got_k.view(np.uint32), want_k.view(np.uint32))
+    want_v = reference_minimum(values.reshape(units, total, dim)[:, :vq].reshape(units, vq, dim // group, group), axis=3)
+    got_v = vp.reshape(units, vq, dim // group, 2)[..., 1]
+    np.testing.assert_array_equal(got_v.view(np.uint32), want_v.view(np.uint32))
+    for want in (want_k, want_v):
+        signs = np.signbit(want[want == 0])
+        assert signs.any() and not signs.all()

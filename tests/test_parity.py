@@ -13,7 +13,7 @@ import pytest
 
 import kivi
 from kivi import KiviCache, KiviConfig, RuntimeKv
-from helpers import DeviceArrays, dense_attend, fill, max_abs
+from helpers import DeviceArrays, dense_attend, fill, max_abs, reference_minimum, signed_zero_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -402,4 +402,40 @@ def test_runtime_decode_device_parity(amd, oracle, bits, residual, gqa):
             assert_same_state(ra.cache(), ro.cache())
             assert_streams_equal(ra.cache(), ro.cache())
             assert_streams_equal(cb, ro.cache())
+    mem.free()
+
+
+@pytest.mark.parametrize("bits", [2, 8])
+def test_decode_device_zero_minima_parity(amd, oracle, bits):
+    """RuntimeKv::decode on device pointers with window rows whose channel groups have zero
+    minima and zeros of both signs: the token each step evicts is quantized inside the
+    attention launch, and its stored zeros must be each group's first zero, as the oracle's
+    decode stores them (src/quant.rs:356)."""
+    heads, dim, residual, gqa = 2, 128, 64, 4
+    prefill, steps = 3 * residual + 17, 2 * residual + 5
+    qh = heads * gqa
+    cfg = KiviConfig(bits, 32, residual)
+    rng = np.random.default_rng(900 + bits)
+    total = prefill + steps
+    keys = rng.standard_normal((1, heads, total, dim)).astype(np.float32)
+    values = signed_zero_rows(rng, (1, heads, total, dim))
+    ra, ro = RuntimeKv(amd, cfg, 1, heads, dim), RuntimeKv(oracle, cfg, 1, heads, dim)
+    for r in (ra, ro):
+        r.prefill(np.ascontiguousarray(keys[:, :, :prefill]), np.ascontiguousarray(values[:, :, :prefill]), prefill)
+    scale = np.float32(1 / np.sqrt(dim))
+    mem = DeviceArrays()
+    n_kv, n_q = heads * dim, qh * dim
+    out = mem.empty(n_q)
+    for step in range(steps):
+        t = prefill + step
+        kk = np.ascontiguousarray(keys[:, :, t]).reshape(-1)
+        vv = np.ascontiguousarray(values[:, :, t]).reshape(-1)
+        q = rng.standard_normal(n_q).astype(np.float32)
+        ra.decode_device(mem.upload(kk), n_kv, mem.upload(vv), n_kv, mem.upload(q), n_q, qh, scale, out, n_q)
+        assert_close(mem.download(out, n_q), ro.decode(kk, vv, q, qh, scale), f"step {step}")
+    assert_streams_equal(ra.cache(), ro.cache())
+    vq = ra.cache().quantized_value_tokens()
+    want = reference_minimum(values.reshape(heads, total, dim)[:, :vq].reshape(heads, vq, dim // 32, 32), axis=3)
+    got = ra.cache().export_streams()[3].reshape(heads, vq, dim // 32, 2)[..., 1]
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
     mem.free()

@@ -9,7 +9,7 @@ import pytest
 
 import kivi
 from kivi import KiviError, quantize_per_channel, quantize_per_token
-from helpers import fill
+from helpers import fill, reference_minimum, signed_zero_rows
 
 
 def pattern_token():
@@ -291,3 +291,29 @@ def test_per_token_codes_match_definition(backend, bits, group):
             for i in range(group):
                 w = int(codes[(t * n_ch + cg) * ipg + i // per])
                 assert (w >> (bits * (i % per))) & mask == int(want[i])
+
+
+@pytest.mark.parametrize("bits,group,dim", [(2, 32, 128), (4, 16, 64), (8, 32, 96), (2, 64, 128)])
+def test_zero_minimum_keeps_the_first_zeros_sign(backend, bits, group, dim):
+    """Groups whose minimum is zero, with +0 and -0 both present: the stored zero is the
+    group's first zero in element order, tokens for keys and channels for values (the
+    reference's f32::min on x86-64 keeps the running minimum on ties). Compared bit for bit,
+    so the sign of every zero counts; the codes still follow the definition."""
+    rng = np.random.default_rng(bits * 100 + group + dim)
+    batch, heads, tokens = 1, 2, 4 * group
+    xk = signed_zero_rows(rng, (batch, heads, tokens, dim))
+    xk[:, 1, :, 1::3] = -np.abs(xk[:, 1, :, 1::3]) - 0.5  # negative minima in some channels
+    qk = quantize_per_channel(backend, xk.reshape(-1), batch, heads, tokens, dim, bits, group)
+    keys = xk.reshape(batch * heads, tokens // group, group, dim)
+    want = reference_minimum(keys, axis=2)  # [units][groups][D]
+    got = qk.scale_zero().reshape(batch * heads, tokens // group, dim, 2)[..., 1]
+    assert (want == 0).sum() > 0 and np.signbit(want[want == 0]).any() and not np.signbit(want[want == 0]).all()
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+    xv = signed_zero_rows(rng, (batch, heads, tokens, dim))
+    xv[:, 1, ::5, 3] = -1.5  # negative minima in some tokens
+    qv = quantize_per_token(backend, xv.reshape(-1), batch, heads, tokens, dim, bits, group)
+    vals = xv.reshape(batch * heads, tokens, dim // group, group)
+    want = reference_minimum(vals, axis=3)  # [units][tokens][D/G]
+    got = qv.scale_zero().reshape(batch * heads, tokens, dim // group, 2)[..., 1]
+    assert np.signbit(want[want == 0]).any() and not np.signbit(want[want == 0]).all()
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
