@@ -174,6 +174,20 @@ kivi_status kivi_cache_attention_device(const kivi_cache* cache, const float* qu
                                         size_t query_len, size_t num_q_heads, float scale,
                                         float* out, size_t out_len, void* stream,
                                         kivi_error* err);
+/* No counterpart in the reference. For callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc): the same attention
+ * as kivi_cache_attention_device, bit for bit, with its split partials in a static workspace
+ * the library holds on each device until the process ends (2,097,152 floats = 8 MiB; the
+ * partials of one call are units * splits * (num_q_heads/num_kv_heads) * (head_dim + 2)
+ * floats, about 1.26 M for batch 16 x 8 KV heads x 32768 tokens with 32 query heads). It calls
+ * no hipMalloc, hipFree or memset (an empty cache's zeros come from a fill kernel) and does not
+ * wait for the device. Larger calls return KIVI_ERR_CAPACITY (a = floats needed, b = the
+ * limit). Every call on one device shares that device's workspace: calls that overlap on the
+ * device race (calls on one stream are ordered). */
+kivi_status kivi_cache_attention_device_noalloc(const kivi_cache* cache, const float* query,
+                                                size_t query_len, size_t num_q_heads, float scale,
+                                                float* out, size_t out_len, void* stream,
+                                                kivi_error* err);
 
 /* KiviCache::dequantize (src/cache.rs:282-325): both outputs hold
  * batch*num_kv_heads*seq*head_dim floats. */

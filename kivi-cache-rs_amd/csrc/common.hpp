@@ -240,6 +240,18 @@ bool attention_fuses_decode(const AttnProblem& p);
 size_t attention_workspace_floats(const AttnProblem& p);
 hipError_t launch_attention(const AttnProblem& p, float* workspace, hipStream_t stream);
 
+// Static attention workspace (kernels_attn.hip): a file-scope device array of
+// kStaticWorkspaceFloats floats (8 MiB) that every device running the library holds until the
+// process ends, for callers that cannot allocate. static_workspace gives its address on the
+// current device, resolved once per device (hipGetSymbolAddress with that device current) and
+// kept. Calls that use it share one array per device: calls that overlap on one device race.
+constexpr size_t kStaticWorkspaceFloats = (size_t)2 << 20;
+hipError_t static_workspace(float** out);
+
+// out[0, n) = 0.f by a kernel (for callers that may capture the stream into a graph, where a
+// memset node is avoided).
+hipError_t launch_fill_zero(float* out, size_t n, hipStream_t stream);
+
 // One session of a batched call: its fp32 suffix ([units][*][D], `stride` floats between
 // units; k / v may be null when len is 0).
 struct SessionDesc {

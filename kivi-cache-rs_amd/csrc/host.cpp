@@ -109,7 +109,10 @@ void format_error(const Status& s, kivi_error* e) {
       std::snprintf(m, n, "%s", s.detail.empty() ? "HIP device error" : s.detail.c_str());
       break;
     case KIVI_ERR_CAPACITY:
-      std::snprintf(m, n, "size %llu exceeds the supported limit %llu", A, B);
+      if (s.name != nullptr)
+        std::snprintf(m, n, "%s %llu exceeds the supported limit %llu", s.name, A, B);
+      else
+        std::snprintf(m, n, "size %llu exceeds the supported limit %llu", A, B);
       break;
     case KIVI_ERR_UNSUPPORTED:
       std::snprintf(m, n, "%s %llu is outside this build's limit %llu", s.name ? s.name : "value", A, B);
@@ -607,22 +610,17 @@ struct AttnSync {
   }
 };
 
-// Attention over `core` plus an optional device suffix, writing `out` on the device.
-// With `tape_only` the cache's tokens are left out: attention over the suffix rows alone
-// (the QualityGuard's fp32 attention over its tape).
-Status attend(const CacheCore& core, AttnSync& sync, const float* suffix_k, const float* suffix_v,
-              uint64_t L, uint64_t suffix_stride, const float* query, size_t qh, float scale,
-              float* out, hipStream_t s, bool tape_only = false) {
+// The attention problem over `core` plus an optional device suffix (tape_only: the suffix
+// rows alone), after the limit check every attention entry point shares.
+Status attention_problem(const CacheCore& core, const float* suffix_k, const float* suffix_v,
+                         uint64_t L, uint64_t suffix_stride, const float* query, size_t qh,
+                         float scale, float* out, bool tape_only, AttnProblem* out_p) {
   const size_t gq = qh / core.heads;
   if (gq * core.head_dim > kMaxGqD)
     return Err(KIVI_ERR_UNSUPPORTED, gq * core.head_dim, kMaxGqD, "(num_q_heads/num_kv_heads)*head_dim");
-  const size_t out_n = core.batch * qh * core.head_dim;
   const uint64_t seq = tape_only ? 0 : core.seq;
-  if (seq + L == 0) {
-    HIP_TRY(hipMemsetAsync(out, 0, out_n * sizeof(float), s), "attention zero output");
-    return Status{};
-  }
-  AttnProblem p{};
+  AttnProblem& p = *out_p;
+  p = AttnProblem{};
   p.cache = core.view();
   p.st = tape_only ? SeqState{} : core.state();
   p.seq = seq;
@@ -636,6 +634,21 @@ Status attend(const CacheCore& core, AttnSync& sync, const float* suffix_k, cons
   p.heads = static_cast<uint32_t>(core.heads);
   p.batch = static_cast<uint32_t>(core.batch);
   p.scale = scale;
+  return Status{};
+}
+
+// Attention over `core` plus an optional device suffix, writing `out` on the device.
+// With `tape_only` the cache's tokens are left out: attention over the suffix rows alone
+// (the QualityGuard's fp32 attention over its tape).
+Status attend(const CacheCore& core, AttnSync& sync, const float* suffix_k, const float* suffix_v,
+              uint64_t L, uint64_t suffix_stride, const float* query, size_t qh, float scale,
+              float* out, hipStream_t s, bool tape_only = false) {
+  AttnProblem p;
+  KIVI_TRY(attention_problem(core, suffix_k, suffix_v, L, suffix_stride, query, qh, scale, out, tape_only, &p));
+  if (p.seq + L == 0) {
+    HIP_TRY(hipMemsetAsync(out, 0, core.batch * qh * core.head_dim * sizeof(float), s), "attention zero output");
+    return Status{};
+  }
   std::lock_guard<std::mutex> lock(sync.mu);
   KIVI_TRY(sync.reserve(attention_workspace_floats(p) * sizeof(float)));
   KIVI_TRY(sync.before(s));
@@ -774,6 +787,34 @@ Status cache_attention(const kivi_cache* c, const float* query, size_t query_len
                   dout.as<float>(), s));
   HIP_TRY(hipMemcpyAsync(out, dout.p, out_len * 4, hipMemcpyDeviceToHost, s), "attention D2H");
   return sync(s, "attention");
+}
+
+// KiviCache::attention on device pointers with the split partials in the library's static
+// per-device workspace: no allocation, no memset (an empty cache's zeros come from a fill
+// kernel), no host-side wait. Checks as cache_attention, then the workspace size. Calls that
+// overlap on one device share the workspace and race; calls on one stream are ordered.
+Status cache_attention_noalloc(const kivi_cache* c, const float* query, size_t query_len,
+                               size_t num_q_heads, float scale, float* out, size_t out_len,
+                               hipStream_t stream) {
+  KIVI_TRY(need(c, "cache"));
+  const CacheCore& core = c->core;
+  KIVI_TRY(check_attention(core.batch, core.heads, core.head_dim, query_len, num_q_heads, out_len));
+  KIVI_TRY(need_slice(query, query_len, "query"));
+  KIVI_TRY(need_slice(out, out_len, "out"));
+  DeviceScope scope(core.device);
+  AttnProblem p;
+  KIVI_TRY(attention_problem(core, nullptr, nullptr, 0, 0, query, num_q_heads, scale, out, false, &p));
+  if (p.seq == 0) {
+    HIP_TRY(launch_fill_zero(out, out_len, stream), "attention zero output");
+    return Status{};
+  }
+  const size_t floats = attention_workspace_floats(p);
+  if (floats > kStaticWorkspaceFloats)
+    return Err(KIVI_ERR_CAPACITY, floats, kStaticWorkspaceFloats, "attention workspace floats");
+  float* ws = nullptr;
+  HIP_TRY(static_workspace(&ws), "static attention workspace");
+  HIP_TRY(launch_attention(p, ws, stream), "attention");
+  return Status{};
 }
 
 // KiviCache::dequantize (src/cache.rs:282-325) into host buffers (staged) or device buffers.
@@ -1408,6 +1449,16 @@ kivi_status kivi_cache_attention_device(const kivi_cache* cache, const float* qu
   return guarded(err, [&] {
     return cache_attention(cache, query, query_len, num_q_heads, scale, out, out_len, true,
                            static_cast<hipStream_t>(stream));
+  });
+}
+
+kivi_status kivi_cache_attention_device_noalloc(const kivi_cache* cache, const float* query,
+                                                size_t query_len, size_t num_q_heads, float scale,
+                                                float* out, size_t out_len, void* stream,
+                                                kivi_error* err) {
+  return guarded(err, [&] {
+    return cache_attention_noalloc(cache, query, query_len, num_q_heads, scale, out, out_len,
+                                   static_cast<hipStream_t>(stream));
   });
 }
 

@@ -1815,6 +1815,47 @@ hipError_t dispatch_generic(const AttnArgs& a, hipStream_t stream) {
 
 }  // namespace
 
+// The static workspace. In host code `scratch` is only a stand-in for the symbol: its device
+// address on each device comes from hipGetSymbolAddress, never from the name.
+static __device__ __align__(256) float scratch[kStaticWorkspaceFloats];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch[kMaxDevices] = {};
+
+__global__ void __launch_bounds__(kThreads) k_fill_zero(float* out, size_t n) {
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+    out[i] = 0.f;
+}
+
+}  // namespace
+
+hipError_t static_workspace(float** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    if (p == nullptr) return hipErrorInvalidSymbol;
+    g_scratch[dev] = static_cast<float*>(p);
+  }
+  *out = g_scratch[dev];
+  return hipSuccess;
+}
+
+hipError_t launch_fill_zero(float* out, size_t n, hipStream_t stream) {
+  if (n == 0) return hipSuccess;
+  const size_t blocks = std::min<size_t>((n + kThreads - 1) / kThreads, 1024);
+  k_fill_zero<<<static_cast<unsigned>(blocks), kThreads, 0, stream>>>(out, n);
+  return hipGetLastError();
+}
+
 bool attention_fuses_decode(const AttnProblem& p) {
   const AttnArgs a = make_args(p, nullptr);
   return a.total > 0 && a.nsplit_gen == 0 && (a.nsplit_fast > 0 || a.nsplit_win > 0);

@@ -136,6 +136,7 @@ class KiviError(Exception):
         self.variant = VARIANTS.get(code, f"Unknown{code}")
         self.name = name
         self.message = message
+        self.a, self.b = a, b  # raw payload fields of the C status
         self.payload = {}
         for field, value in zip(FIELDS.get(self.variant, ()), (a, b)):
             self.payload[field] = value
@@ -271,6 +272,7 @@ _DEVICE_SIGS = {
     "cache_set_stream": (C.c_int, [_P, _P, _ERRP]),
     "cache_append_device": (C.c_int, [_P, _P, _SZ, _P, _SZ, _SZ, _P, _ERRP]),
     "cache_attention_device": (C.c_int, [_P, _P, _SZ, _SZ, C.c_float, _P, _SZ, _P, _ERRP]),
+    "cache_attention_device_noalloc": (C.c_int, [_P, _P, _SZ, _SZ, C.c_float, _P, _SZ, _P, _ERRP]),
     "session_append_device": (C.c_int, [_P, _P, _SZ, _P, _SZ, _SZ, _P, _ERRP]),
     "sessions_attention_device": (
         C.c_int,
@@ -542,6 +544,12 @@ class KiviCache:
 
     def attention_device(self, q_ptr, q_len, num_q_heads, scale, out_ptr, out_len, stream=0):
         self._b.call("cache_attention_device", self._h, C.c_void_p(q_ptr), q_len, num_q_heads,
+                     C.c_float(scale), C.c_void_p(out_ptr), out_len, C.c_void_p(stream))
+
+    def attention_device_noalloc(self, q_ptr, q_len, num_q_heads, scale, out_ptr, out_len, stream=0):
+        """attention_device with the split partials in the library's static per-device
+        workspace (no allocation; see kivi_cache_attention_device_noalloc)."""
+        self._b.call("cache_attention_device_noalloc", self._h, C.c_void_p(q_ptr), q_len, num_q_heads,
                      C.c_float(scale), C.c_void_p(out_ptr), out_len, C.c_void_p(stream))
 
     def dequantize_device(self, k_ptr, k_len, v_ptr, v_len, stream=0):
