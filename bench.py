@@ -1,37 +1,42 @@
 #!/usr/bin/env python3
 """Decode-attention benchmark of the MI355X KIVI path (one JSON line on stdout).
 
-Workload (the north-star target): batch 16, 32 query / 8 KV heads,
-head_dim 128, 32768 cached tokens per sequence, 2-bit G=32 R=128, K ~ N(0,1) with 1% of key
-channels (2 per KV head) scaled x10, V ~ N(0,1), fp32 inputs. A step is one decode attention
+Primary workload (the north-star target): batch 16, 32 query / 8 KV
+heads, head_dim 128, 32768 cached tokens per sequence, 2-bit G=32 R=128, K ~ N(0,1) with 1% of
+key channels (2 per KV head) scaled x10, V ~ N(0,1), fp32 inputs. A step is one decode attention
 over all 16 sequences (the cache and the queries already resident in HBM); value = decode
-tokens/s = 16 * steps / time. The cache build (prefill quantization) is timed once and
-reported as quantize GB/s; the device-side export formats (packed streams in the reference
-order, dense reconstruction) are timed once each after it (`exports`: GB/s and fraction of
-8 TB/s). The CPU baseline is the oracle (C++ restatement of the
-reference CPU path, 1 core) on one of the 16 sequences. Before the prefill and before the W
-warm-up steps the GPU runs ~0.3 s of untimed work (device copies, then the step's own
-kernels) so that its clocks have ramped up; `clock_warmup_calls` counts the second part.
-Workloads whose cache is smaller than three times the 256 MB Infinity Cache (C3, C4) rotate
-over identical cache copies between steps (`cache_copies`), so each step reads its cache from
-HBM rather than from the previous step's cache lines; C0 and C1 are too small for that and
-report `cache_resident: true`.
+tokens/s = 16 * steps / time.
 
-The roofline object is for the dominant kernel (the packed-chunk attention kernel): its
-algorithmic bytes per launch (packed codes + (scale, zero) of the chunks it covers, plus the
-query) over its mean launch duration, both measured live by the library's HIP-event launch
-timing (kivi_timing_*) on the launch stream during the timed region. `traffic` is the HBM
-bytes per launch of that kernel from rocprofv3 FETCH_SIZE + WRITE_SIZE runs, calibrated on a
-plain copy kernel (--copy-calibration), as recorded in profiles/traffic.json; null when no
-record matches this kernel, workload and byte count.
+The default run measures every BASELINE.json workload in the same process and puts the others
+in `configs` (each with its own roofline and CPU baseline): c0 (the reference's CPU-runnable
+case), c1 (streaming decode: a step is RuntimeKv::decode = append one token + attention after
+an 8192-token prefill), c3_4 / c3_8 (4-/8-bit at 131072 tokens, GQA 8), c4 (64 RagSessions over
+one 65536-token prefix, one batched call per step). `--config NAME` measures one workload and
+prints its line alone (the form the rocprof summaries use).
 
-Other workloads (a line each, same contract): --config c0 (the reference's CPU-runnable case),
-c1 (streaming decode: a step is RuntimeKv::decode = append one token + attention, after an
-8192-token prefill; warmup + 2*steps <= 512; its line also times one QualityGuard check,
-`guard`), c3_4 / c3_8 (4-/8-bit at 131072 tokens, GQA 8),
-c4 (64 RagSessions over one 65536-token prefix, one batched call per step).
+Per workload: the cache build (prefill quantization) is timed once (`quantize_gbps`, and per
+kernel); the timed region runs `steps` steps twice, plain (the step time) and with the library's
+per-launch HIP events (kivi_timing_*, per-kernel durations and algorithmic bytes on the launch
+stream). Before the prefill and before the warm-up steps the GPU runs ~0.3 s of untimed work so
+its clocks have ramped up (`clock_warmup_calls`). Caches smaller than three times the 256 MB
+Infinity Cache rotate over identical copies between steps (`cache_copies`), so each step reads
+HBM; C0 and C1 are too small for that and report `cache_resident: true`.
 
-Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--config c2] [--no-cpu]
+`roofline` is for the dominant kernel: the packed-chunk attention kernel (k_attn_mfma, HBM
+bound: algorithmic bytes per launch over its mean launch duration), or for c4 the shared-prefix
+GEMM kernel (k_attn_shared, matrix-core bound: 4*D flops per (session row, prefix token) over
+its mean duration, against the dense f16 MFMA peak). `traffic` is that kernel's HBM bytes per
+launch from rocprofv3 FETCH_SIZE + WRITE_SIZE runs calibrated on a plain copy kernel
+(--copy-calibration), as recorded in profiles/traffic.json; null when no record matches the
+kernel, workload and algorithmic bytes.
+
+The primary line also carries the device exports (packed streams in the reference order, dense
+reconstruction), the standalone codec (quantize_per_channel / per_token of the C2 tensors), and
+one QualityGuard check per R appended tokens on the c1 shape (median over repetitions).
+`cpu_baseline` is the oracle (C++ restatement of the reference CPU path, one thread) on a
+bounded sample of each workload, on this host.
+
+Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--config NAME] [--no-cpu]
                        [--copy-calibration MIB]
 """
 
@@ -39,6 +44,8 @@ import argparse
 import json
 import math
 import os
+import platform
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -67,10 +74,13 @@ CONFIGS = {
            "config 4: one 65536-token 2-bit G=32 R=128 prefix (8 KV heads, head_dim 128) shared by "
            "64 RagSessions with 96-token fp32 suffixes, 32 query heads, batched sessions attention"),
 }
+SECONDARY = ("c0", "c1", "c3_4", "c3_8", "c4")
 # batched-sessions workloads: name -> (sessions, suffix tokens per session)
 SESSIONS = {"c4": (64, 96)}
 # streaming-decode workloads: name -> decode steps the workload allows after the prefill
 DECODE = {"c1": 512}
+# CPU-baseline time per workload (seconds of oracle work, beyond its prefill)
+CPU_SECONDS = {"c2": 12.0, "c0": 3.0, "c1": 5.0, "c3_4": 4.0, "c3_8": 4.0, "c4": 5.0}
 
 
 def log(*a):
@@ -95,62 +105,95 @@ def gpu_inputs(torch, batch, heads, qh, dim, seq, seed):
     return k, v, q
 
 
-def cpu_baseline(kivi, cfg_tuple, target_s=12.0):
-    """Oracle (CPU restatement of the reference, one thread) on one sequence of the workload."""
-    _, heads, qh, dim, seq, bits, G, R, _ = cfg_tuple
-    oracle = kivi.Backend.load(ROOT / "oracle" / "libkivi_oracle.so", "kivi_oracle_", device=False)
-    rng = np.random.default_rng(7)
+# ------------------------------------------------------------------ CPU baselines
+
+
+def host_info():
+    """CPU model and counts of this host (the CPU baselines run on one thread of it)."""
+    info = {"cpu": "unknown", "nproc": os.cpu_count()}
+    try:
+        info["nproc_affinity"] = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        pass
+    try:
+        fields = {}
+        for line in open("/proc/cpuinfo"):
+            if ":" in line:
+                key, val = (x.strip() for x in line.split(":", 1))
+                if key in ("model name", "cpu family", "model", "stepping", "vendor_id") and key not in fields:
+                    fields[key] = val
+            if not line.strip() and fields:
+                break
+        info["cpu"] = fields.get("model name", "unknown")
+        info["cpu_id"] = (f"{fields.get('vendor_id', '?')} family {fields.get('cpu family', '?')} "
+                          f"model {fields.get('model', '?')} stepping {fields.get('stepping', '?')}")
+    except OSError:
+        pass
+    info["machine"] = platform.machine()
+    return info
+
+
+def oracle_backend(kivi):
+    return kivi.Backend.load(ROOT / "oracle" / "libkivi_oracle.so", "kivi_oracle_", device=False)
+
+
+def host_kv(heads, dim, seq, seed):
+    rng = np.random.default_rng(seed)
     k = rng.standard_normal((1, heads, seq, dim), dtype=np.float32)
-    for h, chans in enumerate(outlier_channels(heads, dim, 7)):
+    for h, chans in enumerate(outlier_channels(heads, dim, seed)):
         k[:, h, :, chans] *= 10.0
     v = rng.standard_normal((1, heads, seq, dim), dtype=np.float32)
-    q = rng.standard_normal((1, qh, dim), dtype=np.float32)
-    cache = kivi.KiviCache(oracle, kivi.KiviConfig(bits, G, R), 1, heads, dim)
+    return rng, k, v
+
+
+def cpu_result(per_step, tokens_per_step, sample, **extra):
+    r = {"value": tokens_per_step / per_step, "unit": "tokens/s", "cores": 1, "kind": "port",
+         "sample": sample, "ms_per_step": per_step * 1e3}
+    r.update(extra)
+    r.update(host_info())
+    return r
+
+
+def cpu_baseline(kivi, name):
+    """Oracle (CPU restatement of the reference, one thread) on one sequence of the workload:
+    its prefill, then decode attention steps for about CPU_SECONDS[name]."""
+    _, heads, qh, dim, seq, bits, G, R, _ = CONFIGS[name]
+    rng, k, v = host_kv(heads, dim, seq, 7)
+    cache = kivi.KiviCache(oracle_backend(kivi), kivi.KiviConfig(bits, G, R), 1, heads, dim)
     t0 = time.perf_counter()
     cache.append(k, v, seq)
     t_quant = time.perf_counter() - t0
     quant_bytes = 2 * k.nbytes + cache.memory().compressed_bytes()
     del k, v
+    q = rng.standard_normal((1, qh, dim), dtype=np.float32)
     scale = 1.0 / math.sqrt(dim)
     reps, spent = 0, 0.0
-    while spent < target_s and reps < 5:
+    while spent < CPU_SECONDS[name] and reps < 5:
         t0 = time.perf_counter()
         cache.attention(q, qh, scale)
         spent += time.perf_counter() - t0
         reps += 1
-    per_step = spent / reps
-    return {
-        "value": 1.0 / per_step,
-        "unit": "tokens/s",
-        "cores": 1,
-        "kind": "port",
-        "sample": f"1 of the workload's sequences ({heads} KV / {qh} q heads, {seq} tokens): "
-                  f"{reps} decode attention step(s) of the C++ restatement of the reference "
-                  f"CPU path, single thread; prefill quantize {quant_bytes / t_quant / 1e9:.3f} GB/s",
-        "quantize_gbps": quant_bytes / t_quant / 1e9,
-        "ms_per_step": per_step * 1e3,
-        "cpu": _cpu_model(),
-    }
+    return cpu_result(spent / reps, 1,
+                      f"1 of the workload's sequences ({heads} KV / {qh} q heads, {seq} tokens): "
+                      f"{reps} decode attention step(s) of the C++ restatement of the reference CPU "
+                      f"path, single thread; prefill quantize {quant_bytes / t_quant / 1e9:.3f} GB/s",
+                      quantize_gbps=quant_bytes / t_quant / 1e9)
 
 
-def cpu_baseline_sessions(kivi, cfg_tuple, n_sessions, suffix, target_s=12.0):
+def cpu_baseline_sessions(kivi, name):
     """Oracle on the shared-prefix workload: the prefix once, then sessions one by one (the
     reference's RagSession::attention, src/prefix.rs:223-289), timed per session."""
-    _, heads, qh, dim, seq, bits, G, R, _ = cfg_tuple
-    oracle = kivi.Backend.load(ROOT / "oracle" / "libkivi_oracle.so", "kivi_oracle_", device=False)
-    rng = np.random.default_rng(7)
-    k = rng.standard_normal((1, heads, seq, dim), dtype=np.float32)
-    for h, chans in enumerate(outlier_channels(heads, dim, 7)):
-        k[:, h, :, chans] *= 10.0
-    v = rng.standard_normal((1, heads, seq, dim), dtype=np.float32)
-    cache = kivi.KiviCache(oracle, kivi.KiviConfig(bits, G, R), 1, heads, dim)
+    _, heads, qh, dim, seq, bits, G, R, _ = CONFIGS[name]
+    n_sessions, suffix = SESSIONS[name]
+    rng, k, v = host_kv(heads, dim, seq, 7)
+    cache = kivi.KiviCache(oracle_backend(kivi), kivi.KiviConfig(bits, G, R), 1, heads, dim)
     cache.append(k, v, seq)
     del k, v
     prefix = cache.share_prefix()
     del cache
     scale = 1.0 / math.sqrt(dim)
     reps, spent = 0, 0.0
-    while spent < target_s and reps < min(n_sessions, 5):
+    while spent < CPU_SECONDS[name] and reps < min(n_sessions, 5):
         sess = prefix.session()
         sk = rng.standard_normal((1, heads, suffix, dim), dtype=np.float32)
         sv = rng.standard_normal((1, heads, suffix, dim), dtype=np.float32)
@@ -160,36 +203,23 @@ def cpu_baseline_sessions(kivi, cfg_tuple, n_sessions, suffix, target_s=12.0):
         sess.attention(q, qh, scale)
         spent += time.perf_counter() - t0
         reps += 1
-    per_session = spent / reps
-    return {
-        "value": 1.0 / per_session,
-        "unit": "tokens/s",
-        "cores": 1,
-        "kind": "port",
-        "sample": f"{reps} of the {n_sessions} sessions ({seq}-token prefix + {suffix}-token suffix, "
-                  f"{heads} KV / {qh} q heads): one RagSession decode attention each, C++ "
-                  f"restatement of the reference CPU path, single thread",
-        "ms_per_step": per_session * 1e3,
-        "cpu": _cpu_model(),
-    }
+    return cpu_result(spent / reps, 1,
+                      f"{reps} of the {n_sessions} sessions ({seq}-token prefix + {suffix}-token "
+                      f"suffix, {heads} KV / {qh} q heads): one RagSession decode attention each, "
+                      f"C++ restatement of the reference CPU path, single thread")
 
 
-def cpu_baseline_decode(kivi, cfg_tuple, target_s=10.0):
+def cpu_baseline_decode(kivi, name):
     """Oracle RuntimeKv (src/runtime.rs:12-57): the prefill, then decode steps (append one token
     and attend) timed one by one on one thread."""
-    _, heads, qh, dim, seq, bits, G, R, _ = cfg_tuple
-    oracle = kivi.Backend.load(ROOT / "oracle" / "libkivi_oracle.so", "kivi_oracle_", device=False)
-    rng = np.random.default_rng(7)
-    k = rng.standard_normal((1, heads, seq, dim), dtype=np.float32)
-    for h, chans in enumerate(outlier_channels(heads, dim, 7)):
-        k[:, h, :, chans] *= 10.0
-    v = rng.standard_normal((1, heads, seq, dim), dtype=np.float32)
-    rt = kivi.RuntimeKv(oracle, kivi.KiviConfig(bits, G, R), 1, heads, dim)
+    _, heads, qh, dim, seq, bits, G, R, _ = CONFIGS[name]
+    rng, k, v = host_kv(heads, dim, seq, 7)
+    rt = kivi.RuntimeKv(oracle_backend(kivi), kivi.KiviConfig(bits, G, R), 1, heads, dim)
     rt.prefill(k, v, seq)
     del k, v
     scale = 1.0 / math.sqrt(dim)
     reps, spent = 0, 0.0
-    while spent < target_s and reps < 200:
+    while spent < CPU_SECONDS[name] and reps < 200:
         kk = rng.standard_normal(heads * dim, dtype=np.float32)
         vv = rng.standard_normal(heads * dim, dtype=np.float32)
         q = rng.standard_normal(qh * dim, dtype=np.float32)
@@ -197,65 +227,25 @@ def cpu_baseline_decode(kivi, cfg_tuple, target_s=10.0):
         rt.decode(kk, vv, q, qh, scale)
         spent += time.perf_counter() - t0
         reps += 1
-    per_step = spent / reps
-    return {
-        "value": 1.0 / per_step,
-        "unit": "tokens/s",
-        "cores": 1,
-        "kind": "port",
-        "sample": f"{reps} RuntimeKv::decode steps (append 1 token + attention, {heads} KV / {qh} q "
-                  f"heads) after a {seq}-token prefill, C++ restatement of the reference CPU path, "
-                  f"single thread",
-        "ms_per_step": per_step * 1e3,
-        "cpu": _cpu_model(),
-    }
+    return cpu_result(spent / reps, 1,
+                      f"{reps} RuntimeKv::decode steps (append 1 token + attention, {heads} KV / "
+                      f"{qh} q heads) after a {seq}-token prefill, C++ restatement of the reference "
+                      f"CPU path, single thread")
 
 
-def guard_check(kivi, amd, cfg_tuple):
-    """QualityGuard (src/guard.rs) on the streaming-decode shape: after a guarded prefill of
-    the workload's tokens, one append of R tokens makes exactly one key flush and one check
-    (cache attention and fp32 attention over the whole tape on the GPU, cosine on the host).
-    Timed against the plain cache doing the same append and one attention. Host-pointer API:
-    the times include the PCIe copies of the R new rows, the query and the outputs."""
-    batch, heads, qh, dim, seq, bits, G, R, _ = cfg_tuple
-    rng = np.random.default_rng(11)
-    cfg = kivi.KiviConfig(bits, G, R)
-    keys = rng.standard_normal((batch, heads, seq + 2 * R, dim), dtype=np.float32)
-    values = rng.standard_normal((batch, heads, seq + 2 * R, dim), dtype=np.float32)
-    query = rng.standard_normal((batch, qh, dim), dtype=np.float32)
-    scale = 1.0 / math.sqrt(dim)
-    pre_k, pre_v = np.ascontiguousarray(keys[:, :, :seq]), np.ascontiguousarray(values[:, :, :seq])
-    mid_k, mid_v = np.ascontiguousarray(keys[:, :, seq:seq + R]), np.ascontiguousarray(values[:, :, seq:seq + R])
-    new_k, new_v = np.ascontiguousarray(keys[:, :, seq + R:]), np.ascontiguousarray(values[:, :, seq + R:])
-    guard = kivi.QualityGuard(amd, cfg, batch, heads, dim, 0.0, kivi.QualityPolicy.RaiseBits, 8, R)
-    guard.append(pre_k, pre_v, seq, query, qh, scale)
-    guard.append(mid_k, mid_v, R, query, qh, scale)  # untimed: the tape grows past seq here
-    plain = kivi.KiviCache(amd, cfg, batch, heads, dim)
-    plain.append(pre_k, pre_v, seq)
-    plain.append(mid_k, mid_v, R)
-    t0 = time.perf_counter()
-    checks = guard.append(new_k, new_v, R, query, qh, scale)
-    t_guard = time.perf_counter() - t0
-    t0 = time.perf_counter()
-    plain.append(new_k, new_v, R)
-    plain.attention(query, qh, scale)
-    t_plain = time.perf_counter() - t0
-    log(f"[bench] guarded append of {R} tokens with {len(checks)} check(s): {t_guard * 1e3:.2f} ms "
-        f"(plain append + attention {t_plain * 1e3:.2f} ms)")
-    return {"append_tokens": R, "checks": len(checks), "tape_tokens": seq + 2 * R,
-            "cosine": checks[0].cosine if checks else None,
-            "guarded_ms": t_guard * 1e3, "plain_append_attention_ms": t_plain * 1e3,
-            "note": "host-pointer API, PCIe copies included"}
+def run_cpu_baseline(kivi, name):
+    log(f"[bench] {name}: CPU baseline (oracle, 1 thread) ...")
+    if name in SESSIONS:
+        r = cpu_baseline_sessions(kivi, name)
+    elif name in DECODE:
+        r = cpu_baseline_decode(kivi, name)
+    else:
+        r = cpu_baseline(kivi, name)
+    log(f"[bench] {name}: CPU {r['value']:.3f} tokens/s")
+    return r
 
 
-def _cpu_model():
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
-    except OSError:
-        pass
-    return "unknown"
+# ------------------------------------------------------------------ GPU measurement helpers
 
 
 def recorded_traffic(kernel, workload, bytes_per_launch):
@@ -292,39 +282,42 @@ def clock_warmup(torch, stream, fn, seconds=CLOCK_WARMUP_S, batch=20):
     return n
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
-                    help="after the timed region, copy MIB MiB device-to-device 3 times (a plain "
-                         "copy kernel of known size for calibrating rocprofv3 byte counters)")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus "
-              f"{args.gpus}); the (batch, kv_head) units would shard across GPUs with no "
-              f"communication, each GPU running these kernels on its share",
-              file=sys.stderr)
-        sys.exit(2)
+def timed_once(torch, stream, fn):
+    """Seconds of one call of fn on `stream`, after an untimed call (HIP events)."""
+    fn()
+    stream.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        e0.record(stream)
+        fn()
+        e1.record(stream)
+    stream.synchronize()
+    return e0.elapsed_time(e1) / 1e3
 
-    import torch
-    import kivi
 
-    amd = kivi.Backend.amd()
-    assert amd["device_count"]() >= 1, "no HIP device"
-    batch, heads, qh, dim, seq, bits, G, R, desc = CONFIGS[args.config]
-    torch.cuda.set_device(0)
-    stream = torch.cuda.Stream()
+def kernel_table(kivi, amd, families):
+    out = {}
+    for fam in families:
+        n, ms, by = kivi.timing_read(amd, fam)
+        if n:
+            out[fam] = {"launches": n, "mean_us": ms * 1e3 / n, "bytes_per_launch": by / n,
+                        "gbps": by / (ms / 1e3) / 1e9}
+    return out
+
+
+ATTN_FAMILIES = ("attn_packed", "attn_tail", "attn_merge", "attn_shared", "attn_sessions")
+
+
+def measure(name, args, torch, kivi, amd, stream, with_cpu):
+    """One workload: prefill, timed steps, roofline, CPU baseline. Returns its result dict."""
+    batch, heads, qh, dim, seq, bits, G, R, desc = CONFIGS[name]
     sp = stream.cuda_stream
-
-    log(f"[bench] building inputs {desc}")
+    cfg = kivi.KiviConfig(bits, G, R)
+    log(f"[bench] {name}: building inputs ({desc})")
     k, v, q = gpu_inputs(torch, batch, heads, qh, dim, seq, 2001)
     out = torch.empty((batch, qh, dim), device="cuda", dtype=torch.float32)
     # warm-up: a small cache of the same shape loads the kernels' code objects before timing
-    warm = kivi.KiviCache(amd, kivi.KiviConfig(bits, G, R), 1, heads, dim)
+    warm = kivi.KiviCache(amd, cfg, 1, heads, dim)
     wk = torch.randn((1, heads, 4 * R, dim), device="cuda", dtype=torch.float32)
     warm.append_device(wk.data_ptr(), wk.numel(), wk.data_ptr(), wk.numel(), 4 * R, sp)
     wq = torch.randn((1, qh, dim), device="cuda", dtype=torch.float32)
@@ -337,13 +330,14 @@ def main():
     clock_warmup(torch, stream, lambda: scratch.copy_(k), batch=4)
     del scratch
     torch.cuda.empty_cache()
-    if DECODE.get(args.config):
+    decode_steps = DECODE.get(name)
+    if decode_steps:
         # RuntimeKv (src/runtime.rs:12-57): prefill through its cache, then decode steps
-        runtime = kivi.RuntimeKv(amd, kivi.KiviConfig(bits, G, R), batch, heads, dim)
+        runtime = kivi.RuntimeKv(amd, cfg, batch, heads, dim)
         cache = runtime.cache()
-        cache.reserve(seq + DECODE[args.config])
+        cache.reserve(seq + decode_steps)
     else:
-        cache = kivi.KiviCache(amd, kivi.KiviConfig(bits, G, R), batch, heads, dim)
+        cache = kivi.KiviCache(amd, cfg, batch, heads, dim)
         cache.reserve(seq)
     torch.cuda.synchronize()
     # Prefill quantization, timed once on the library's stream (whole append, and per
@@ -357,69 +351,44 @@ def main():
     stream.synchronize()
     t_quant = e0.elapsed_time(e1) / 1e3
     quant_kernels = {}
-    for fam in ("quant_keys", "quant_values"):
-        n, ms, by = kivi.timing_read(amd, fam)
-        if n:
-            quant_kernels[fam] = {"launches": n, "ms": ms, "gbps": by / (ms / 1e3) / 1e9}
+    for fam, r in kernel_table(kivi, amd, ("quant_keys", "quant_values")).items():
+        quant_kernels[fam] = {"launches": r["launches"], "ms": r["mean_us"] * r["launches"] / 1e3,
+                              "gbps": r["gbps"], "frac": r["gbps"] / HBM_PEAK_GBPS}
     kivi.timing_enable(amd, False)
     mem = cache.memory()
     quant_bytes = 2 * k.numel() * 4 + mem.compressed_bytes()
-    log(f"[bench] prefill quantize {quant_bytes / t_quant / 1e9:.1f} GB/s ({t_quant * 1e3:.2f} ms)")
+    log(f"[bench] {name}: prefill quantize {quant_bytes / t_quant / 1e9:.1f} GB/s ({t_quant * 1e3:.2f} ms)")
 
-    # Export formats into device memory, each timed once after an untimed call: the packed
-    # streams in the reference order (packed bytes read and written) and the dense
-    # reconstruction (packed bytes read, fp32 keys and values written).
-    exports = {}
-    if not DECODE.get(args.config):
-        lens = cache.stream_lengths()
-        bufs = [torch.empty(max(n, 1), device="cuda", dtype=torch.float32) for n in lens]
-        ptrs = [b.data_ptr() if n else 0 for b, n in zip(bufs, lens)]
-        n_el = k.numel()
-        dk, dv = torch.empty_like(k), torch.empty_like(v)
-        jobs = (("export_streams", lambda: cache.export_streams_device(ptrs, lens, sp), 2 * 4 * sum(lens)),
-                ("dequantize", lambda: cache.dequantize_device(dk.data_ptr(), n_el, dv.data_ptr(), n_el, sp),
-                 mem.compressed_bytes() + 2 * n_el * 4))
-        for name, fn, nbytes in jobs:
-            fn()
-            stream.synchronize()
-            with torch.cuda.stream(stream):
-                e0.record(stream)
-                fn()
-                e1.record(stream)
-            stream.synchronize()
-            t = e0.elapsed_time(e1) / 1e3
-            exports[name] = {"ms": t * 1e3, "bytes": nbytes, "gbps": nbytes / t / 1e9,
-                             "frac": nbytes / t / (HBM_PEAK_GBPS * 1e9)}
-            log(f"[bench] {name} {nbytes / t / 1e9:.0f} GB/s ({t * 1e3:.3f} ms)")
-        del bufs, dk, dv
-        torch.cuda.empty_cache()
+    extras = {}
+    if name == "c2":
+        extras.update(primary_extras(torch, kivi, amd, stream, cache, mem, k, v))
 
     # A step whose cache is smaller than the 256 MB Infinity Cache (MALL) could be served
     # from it by the previous step. Such workloads rotate over `copies` identical caches (the
     # same prefill), so consecutive steps touch >= ROTATE_BYTES of distinct data and each step
     # reads its cache from HBM. Decode steps (C1) and caches too small to rotate out of the
     # MALL within MAX_COPIES report `cache_resident`.
-    decode_steps = DECODE.get(args.config)
-    step_bytes = mem.compressed_bytes() + (SESSIONS[args.config][0] * batch * heads *
-                                           SESSIONS[args.config][1] * dim * 8 if args.config in SESSIONS else 0)
+    sessions_cfg = SESSIONS.get(name)
+    step_bytes = mem.compressed_bytes() + (sessions_cfg[0] * batch * heads * sessions_cfg[1] * dim * 8
+                                           if sessions_cfg else 0)
     copies = 1
     if not decode_steps and step_bytes < ROTATE_BYTES:
         copies = min(MAX_COPIES, -(-ROTATE_BYTES // step_bytes))
     cache_resident = copies * step_bytes < ROTATE_BYTES
     caches = [cache]
     for _ in range(copies - 1):
-        c2_ = kivi.KiviCache(amd, kivi.KiviConfig(bits, G, R), batch, heads, dim)
-        c2_.reserve(seq)
-        c2_.append_device(k.data_ptr(), k.numel(), v.data_ptr(), v.numel(), seq, sp)
-        caches.append(c2_)
+        cc = kivi.KiviCache(amd, cfg, batch, heads, dim)
+        cc.reserve(seq)
+        cc.append_device(k.data_ptr(), k.numel(), v.data_ptr(), v.numel(), seq, sp)
+        caches.append(cc)
     stream.synchronize()
     if copies > 1:
-        log(f"[bench] {copies} cache copies rotate between steps ({copies * step_bytes / 1e6:.0f} MB)")
+        log(f"[bench] {name}: {copies} cache copies rotate between steps ({copies * step_bytes / 1e6:.0f} MB)")
     del k, v
     torch.cuda.empty_cache()
 
     scale = 1.0 / math.sqrt(dim)
-    sessions_cfg = SESSIONS.get(args.config)
+    keep = []  # device tensors and handles the steps use
     if sessions_cfg:
         # shared prefix + RagSessions with private fp32 suffixes; a step is one batched
         # attention over all sessions (the prefix streamed once per step)
@@ -437,11 +406,12 @@ def main():
             prefixes.append(prefix)
             all_sessions.append(sessions)
             all_handles.append(kivi.session_handles(sessions))
-        del cache, caches, cc
+        del cache, caches
         torch.cuda.empty_cache()
         stream.synchronize()
         q = torch.randn((n_sess, batch, qh, dim), generator=gs, device="cuda")
         out = torch.empty_like(q)
+        keep += [sks, svs, prefixes, q, out]
         qp, op, n_q = q.data_ptr(), out.data_ptr(), q.numel()
         tokens_per_step = n_sess * batch
         kv_bytes = prefixes[0].prefix_bytes() + n_sess * batch * heads * suffix * dim * 4 * 2
@@ -452,12 +422,13 @@ def main():
             turn[0] += 1
             kivi.sessions_attention_device(amd, all_sessions[i], qp, n_q, qh, scale, op, n_q, sp,
                                            handles=all_handles[i])
+        warm_fn = step
     elif decode_steps:
         # one decode step = append one token (key residual, value window, flush every R) and
         # attend; the plain and the evented timed regions each run `steps` of them
         total = args.warmup + 2 * args.steps
         if total > decode_steps:
-            sys.exit(f"c1 allows {decode_steps} decode steps after the prefill: warmup + 2 * steps = {total}")
+            sys.exit(f"{name} allows {decode_steps} decode steps after the prefill: warmup + 2 * steps = {total}")
         gd = torch.Generator(device="cuda")
         gd.manual_seed(2003)
         kd = torch.randn((total, batch, heads, 1, dim), generator=gd, device="cuda")
@@ -465,6 +436,7 @@ def main():
             kd[:, :, h, :, chans] *= 10.0
         vd = torch.randn((total, batch, heads, 1, dim), generator=gd, device="cuda")
         qd = torch.randn((total, batch, qh, dim), generator=gd, device="cuda")
+        keep += [kd, vd, qd, runtime]
         n_kv, n_q = batch * heads * dim, batch * qh * dim
         op = out.data_ptr()
         counter = [0]
@@ -476,6 +448,10 @@ def main():
             counter[0] += 1
             runtime.decode_device(kd[i].data_ptr(), n_kv, vd[i].data_ptr(), n_kv, qd[i].data_ptr(),
                                   n_q, qh, scale, op, n_q, sp)
+
+        # clocks up on attention over the cache, which leaves the decode state alone
+        def warm_fn():
+            cache.attention_device(qd[0].data_ptr(), n_q, qh, scale, op, n_q, sp)
     else:
         qp, op, n_q = q.data_ptr(), out.data_ptr(), q.numel()
         tokens_per_step = batch
@@ -486,16 +462,15 @@ def main():
             i = turn[0] % copies
             turn[0] += 1
             caches[i].attention_device(qp, n_q, qh, scale, op, n_q, sp)
+        warm_fn = step
 
-    # clocks up on the step's own kernels (C1: attention over the cache, which leaves the
-    # decode state alone), then the W warm-up steps
-    extra_warmup = clock_warmup(torch, stream, step if not decode_steps else
-                                (lambda: cache.attention_device(qd[0].data_ptr(), n_q, qh, scale, op, n_q, sp)))
+    extra_warmup = clock_warmup(torch, stream, warm_fn)
     with torch.cuda.stream(stream):
         for _ in range(args.warmup):
             step()
     stream.synchronize()
     torch.cuda.synchronize()
+
     def timed_steps():
         t_start = torch.cuda.Event(enable_timing=True)
         t_end = torch.cuda.Event(enable_timing=True)
@@ -515,16 +490,11 @@ def main():
     # per-kernel durations (the event records add a few microseconds between launches).
     kivi.timing_enable(amd, True)
     per_step_evented = timed_steps()
-    kernels = {}
-    for fam in ("attn_packed", "attn_tail", "attn_merge"):
-        n, ms, by = kivi.timing_read(amd, fam)
-        if n:
-            kernels[fam] = {"launches": n, "mean_us": ms * 1e3 / n, "bytes_per_launch": by / n,
-                            "gbps": by / (ms / 1e3) / 1e9}
+    kernels = kernel_table(kivi, amd, ATTN_FAMILIES)
     kivi.timing_enable(amd, False)
-    log(f"[bench] timed region with per-launch events: {per_step_evented * 1e6:.1f} us/step")
+    log(f"[bench] {name}: timed region with per-launch events: {per_step_evented * 1e6:.1f} us/step")
     for fam, r in kernels.items():
-        log(f"[bench] {fam}: {r['mean_us']:.1f} us/launch, {r['bytes_per_launch'] / 1e6:.2f} MB, "
+        log(f"[bench] {name}: {fam}: {r['mean_us']:.1f} us/launch, {r['bytes_per_launch'] / 1e6:.2f} MB, "
             f"{r['gbps']:.0f} GB/s")
     if args.copy_calibration > 0:
         n = args.copy_calibration * (1 << 20) // 4
@@ -538,20 +508,24 @@ def main():
     algo_bytes = kv_bytes + 2 * out.numel() * 4  # KV bytes + query + output
     eff_gbps = algo_bytes / per_step / 1e9
     tokens_per_s = tokens_per_step / per_step
-    log(f"[bench] attention {per_step * 1e6:.1f} us/step, {eff_gbps:.0f} GB/s effective")
+    log(f"[bench] {name}: attention {per_step * 1e6:.1f} us/step, {eff_gbps:.0f} GB/s effective")
 
-    dom = kernels.get("attn_packed") or kernels.get("attn_tail")
-    # the sessions workload (64 sessions x 4 heads = 256 rows per unit) runs the GEMM form
-    dom_name = ("k_attn_shared" if sessions_cfg else "k_attn_mfma") if "attn_packed" in kernels \
-        else "k_attn_generic"
-    achieved = dom["gbps"] if dom else eff_gbps
-    rec = recorded_traffic(dom_name, args.config, dom["bytes_per_launch"]) if dom else None
+    if sessions_cfg and "attn_shared" in kernels:
+        dom_fam, dom_name = "attn_shared", "k_attn_shared"
+    elif "attn_packed" in kernels:
+        dom_fam, dom_name = "attn_packed", "k_attn_mfma"
+    elif "attn_sessions" in kernels:
+        dom_fam, dom_name = "attn_sessions", "k_attn_sessions"
+    else:
+        dom_fam, dom_name = "attn_tail", "k_attn_generic"
+    dom = kernels.get(dom_fam)
+    rec = recorded_traffic(dom_name, name, dom["bytes_per_launch"]) if dom else None
     roofline = {
         "bound": "hbm",
-        "achieved": achieved,
+        "achieved": dom["gbps"] if dom else eff_gbps,
         "peak": HBM_PEAK_GBPS,
         "unit": "GB/s",
-        "frac": achieved / HBM_PEAK_GBPS,
+        "frac": (dom["gbps"] if dom else eff_gbps) / HBM_PEAK_GBPS,
         "traffic": rec["hbm_bytes_per_launch"] if rec else None,
         "kernel": dom_name,
         "algorithmic_bytes_per_launch": dom["bytes_per_launch"] if dom else algo_bytes,
@@ -560,20 +534,20 @@ def main():
                   "region of the same steps",
         "traffic_source": rec["source"] if rec else None,
     }
-    if sessions_cfg and dom:
-        # The batched-sessions GEMM form is bound by the matrix cores: algorithmic flops of the
-        # launch (q.k and p.v over every session row and token, 4*D flops per row-token) over
-        # its mean duration, against the dense f16 MFMA peak it runs on. Each product executes
-        # as three f16 MFMA products (hi/lo operand splits), reported beside it.
-        n_sess, suffix = sessions_cfg
+    if dom_fam == "attn_shared":
+        # The shared-prefix GEMM form is bound by the matrix cores: algorithmic flops of the
+        # launch (q.k and p.v over every session row and prefix token, 4*D flops per
+        # row-token; the suffixes run in the per-session kernel) over its mean duration,
+        # against the dense f16 MFMA peak it runs on. Each product executes as three f16 MFMA
+        # products (hi/lo operand splits), reported beside it.
+        n_sess, _ = sessions_cfg
         rows = n_sess * (qh // heads)
-        flops = 4.0 * dim * rows * (seq + suffix) * batch * heads
+        flops = 4.0 * dim * rows * seq * batch * heads
         tflops = flops / (dom["mean_us"] * 1e-6) / 1e12
         roofline.update({
             "bound": "mfma", "achieved": tflops, "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
             "frac": tflops / MFMA_F16_PEAK_TFLOPS, "algorithmic_flops_per_launch": flops,
-            "executed_f16_tflops": 3.0 * tflops,
-            "hbm_gbps": dom["gbps"],
+            "executed_f16_tflops": 3.0 * tflops, "hbm_gbps": dom["gbps"],
         })
     result = {
         "metric": METRIC,
@@ -586,6 +560,7 @@ def main():
         "cache_copies": copies,
         "cache_resident": cache_resident,
         "ms_per_step": per_step * 1e3,
+        "ms_per_step_evented": per_step_evented * 1e3,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -602,19 +577,171 @@ def main():
         "roofline": roofline,
         "kernels": kernels,
         "quantize_kernels": quant_kernels,
-        "exports": exports,
     }
+    result.update(extras)
+    del keep, step, warm_fn
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
     if decode_steps:
-        result["guard"] = guard_check(kivi, amd, CONFIGS[args.config])
-    if not args.no_cpu:
-        log("[bench] CPU baseline (oracle, 1 thread) ...")
-        if sessions_cfg:
-            result["cpu_baseline"] = cpu_baseline_sessions(kivi, CONFIGS[args.config], *sessions_cfg)
-        elif decode_steps:
-            result["cpu_baseline"] = cpu_baseline_decode(kivi, CONFIGS[args.config])
+        result["guard"] = guard_check(kivi, amd, CONFIGS[name])
+    if with_cpu:
+        result["cpu_baseline"] = run_cpu_baseline(kivi, name)
+    return result
+
+
+def primary_extras(torch, kivi, amd, stream, cache, mem, k, v):
+    """Device exports of the primary cache and the standalone codec on its tensors."""
+    sp = stream.cuda_stream
+    _, heads, _, dim, seq, bits, G, _, _ = CONFIGS["c2"]
+    batch = k.shape[0]
+    exports = {}
+    # Export formats into device memory, each timed once after an untimed call: the packed
+    # streams in the reference order (packed bytes read and written) and the dense
+    # reconstruction (packed bytes read, fp32 keys and values written).
+    lens = cache.stream_lengths()
+    bufs = [torch.empty(max(n, 1), device="cuda", dtype=torch.float32) for n in lens]
+    ptrs = [b.data_ptr() if n else 0 for b, n in zip(bufs, lens)]
+    n_el = k.numel()
+    dk, dv = torch.empty_like(k), torch.empty_like(v)
+    jobs = (("export_streams", lambda: cache.export_streams_device(ptrs, lens, sp), 2 * 4 * sum(lens)),
+            ("dequantize", lambda: cache.dequantize_device(dk.data_ptr(), n_el, dv.data_ptr(), n_el, sp),
+             mem.compressed_bytes() + 2 * n_el * 4))
+    for name, fn, nbytes in jobs:
+        t = timed_once(torch, stream, fn)
+        exports[name] = {"ms": t * 1e3, "bytes": nbytes, "gbps": nbytes / t / 1e9,
+                         "frac": nbytes / t / (HBM_PEAK_GBPS * 1e9)}
+        log(f"[bench] {name} {nbytes / t / 1e9:.0f} GB/s ({t * 1e3:.3f} ms)")
+    del bufs, dk, dv
+    torch.cuda.empty_cache()
+    # The standalone codec (quantize_per_channel / quantize_per_token, src/quant.rs:153-233) on
+    # the C2 keys and values: device input, reference-order codes and (scale, zero) out. The
+    # kernel is timed by the library's launch events (the call also allocates its outputs).
+    codec = {}
+    import ctypes as C
+    for name, fam, t in (("quantize_per_channel", "codec_keys", k), ("quantize_per_token", "codec_values", v)):
+        handles = []
+
+        def call():
+            h = C.c_void_p()
+            amd.call(name + "_device", C.c_void_p(t.data_ptr()), t.numel(), batch, heads, seq, dim,
+                     bits, G, C.c_void_p(sp), C.byref(h))
+            handles.append(h)
+        call()
+        stream.synchronize()
+        kivi.timing_enable(amd, True)
+        call()
+        r = kernel_table(kivi, amd, (fam,)).get(fam)
+        kivi.timing_enable(amd, False)
+        for h in handles:
+            amd["quantized_free"](h)
+        if r:
+            codec[name] = {"kernel_us": r["mean_us"], "bytes": r["bytes_per_launch"], "gbps": r["gbps"],
+                           "frac": r["gbps"] / HBM_PEAK_GBPS}
+            log(f"[bench] {name}: {r['gbps']:.0f} GB/s ({r['mean_us']:.1f} us)")
+    torch.cuda.empty_cache()
+    return {"exports": exports, "codec": codec}
+
+
+def guard_check(kivi, amd, cfg_tuple, reps=5):
+    """QualityGuard (src/guard.rs) on the streaming-decode shape: after a guarded prefill of
+    the workload's tokens, each append of R tokens makes exactly one key flush and one check
+    (cache attention and fp32 attention over the whole tape on the GPU, cosine on the host).
+    Timed against the plain cache doing the same append and one attention, alternating which
+    runs first, after one untimed repetition; medians and ranges over `reps`. Host-pointer API:
+    the times include the PCIe copies of the R new rows, the query and the outputs."""
+    batch, heads, qh, dim, seq, bits, G, R, _ = cfg_tuple
+    rng = np.random.default_rng(11)
+    cfg = kivi.KiviConfig(bits, G, R)
+    total = seq + (reps + 1) * R
+    keys = rng.standard_normal((batch, heads, total, dim), dtype=np.float32)
+    values = rng.standard_normal((batch, heads, total, dim), dtype=np.float32)
+    query = rng.standard_normal((batch, qh, dim), dtype=np.float32)
+    scale = 1.0 / math.sqrt(dim)
+    pre_k, pre_v = np.ascontiguousarray(keys[:, :, :seq]), np.ascontiguousarray(values[:, :, :seq])
+    guard = kivi.QualityGuard(amd, cfg, batch, heads, dim, 0.0, kivi.QualityPolicy.RaiseBits, 8, R)
+    guard.append(pre_k, pre_v, seq, query, qh, scale)
+    plain = kivi.KiviCache(amd, cfg, batch, heads, dim)
+    plain.append(pre_k, pre_v, seq)
+    t_guard, t_plain, checks = [], [], None
+    for i in range(reps + 1):
+        lo = seq + i * R
+        nk, nv = np.ascontiguousarray(keys[:, :, lo:lo + R]), np.ascontiguousarray(values[:, :, lo:lo + R])
+
+        def guarded():
+            t0 = time.perf_counter()
+            c = guard.append(nk, nv, R, query, qh, scale)
+            return time.perf_counter() - t0, c
+
+        def unguarded():
+            t0 = time.perf_counter()
+            plain.append(nk, nv, R)
+            plain.attention(query, qh, scale)
+            return time.perf_counter() - t0
+
+        if i % 2 == 0:
+            tg, checks = guarded()
+            tp = unguarded()
         else:
-            result["cpu_baseline"] = cpu_baseline(kivi, CONFIGS[args.config])
-        log(f"[bench] CPU {result['cpu_baseline']['value']:.3f} tokens/s")
+            tp = unguarded()
+            tg, checks = guarded()
+        if i > 0:
+            t_guard.append(tg)
+            t_plain.append(tp)
+    g_ms = [x * 1e3 for x in t_guard]
+    p_ms = [x * 1e3 for x in t_plain]
+    log(f"[bench] guarded append of {R} tokens with {len(checks)} check(s): median "
+        f"{statistics.median(g_ms):.2f} ms (plain append + attention {statistics.median(p_ms):.2f} ms)")
+    return {"append_tokens": R, "checks_per_append": len(checks), "repetitions": reps,
+            "tape_tokens_first": seq + R, "tape_tokens_last": total,
+            "cosine": checks[0].cosine if checks else None,
+            "guarded_ms_median": statistics.median(g_ms), "guarded_ms_range": [min(g_ms), max(g_ms)],
+            "plain_append_attention_ms_median": statistics.median(p_ms),
+            "plain_append_attention_ms_range": [min(p_ms), max(p_ms)],
+            "note": "host-pointer API, PCIe copies included; one untimed repetition first, order "
+                    "alternating"}
+
+
+SUMMARY_KEYS = ("value", "unit", "ms_per_step", "ms_per_step_evented", "effective_hbm_gbps",
+                "hbm_fraction", "quantize_gbps", "cache_copies", "cache_resident", "clock_warmup_calls",
+                "config", "roofline", "kernels", "quantize_kernels", "guard", "cpu_baseline")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default=None, choices=sorted(CONFIGS),
+                    help="measure only this workload (default: c2 as the primary line, the others "
+                         "in `configs`)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="after each timed region, copy MIB MiB device-to-device 3 times (a plain "
+                         "copy kernel of known size for calibrating rocprofv3 byte counters)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus "
+              f"{args.gpus}); the (batch, kv_head) units would shard across GPUs with no "
+              f"communication, each GPU running these kernels on its share",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import kivi
+
+    amd = kivi.Backend.amd()
+    assert amd["device_count"]() >= 1, "no HIP device"
+    torch.cuda.set_device(0)
+    stream = torch.cuda.Stream()
+    with_cpu = not args.no_cpu
+    if args.config is not None:
+        print(json.dumps(measure(args.config, args, torch, kivi, amd, stream, with_cpu)), flush=True)
+        return
+    result = measure("c2", args, torch, kivi, amd, stream, with_cpu)
+    result["configs"] = {}
+    for name in SECONDARY:
+        sub = measure(name, args, torch, kivi, amd, stream, with_cpu)
+        result["configs"][name] = {key: sub[key] for key in SUMMARY_KEYS if key in sub}
     print(json.dumps(result), flush=True)
 
 

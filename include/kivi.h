@@ -455,7 +455,11 @@ typedef enum kivi_kernel_family {
   KIVI_KERNEL_ATTN_MERGE = 2,   /* log-sum-exp merge of the split partials */
   KIVI_KERNEL_QUANT_KEYS = 3,   /* per-channel key quantization into the cache */
   KIVI_KERNEL_QUANT_VALUES = 4, /* per-token value quantization into the cache */
-  KIVI_KERNEL_FAMILIES = 5
+  KIVI_KERNEL_ATTN_SHARED = 5,  /* batched sessions: the shared prefix as a GEMM operand */
+  KIVI_KERNEL_ATTN_SESSIONS = 6,/* batched sessions: per-session suffix chunks (or whole sessions) */
+  KIVI_KERNEL_CODEC_KEYS = 7,   /* standalone quantize_per_channel */
+  KIVI_KERNEL_CODEC_VALUES = 8, /* standalone quantize_per_token */
+  KIVI_KERNEL_FAMILIES = 9
 } kivi_kernel_family;
 
 typedef struct kivi_kernel_timing {

@@ -1974,24 +1974,34 @@ AttnArgs make_shared_args(const SessionsProblem& sp, uint32_t nsess, uint64_t ma
   return a;
 }
 
+// Algorithmic bytes of one launch group: the prefix's packed and fp32 rows, the sessions'
+// suffix rows, and the queries.
+struct GroupBytes {
+  double prefix, suffixes, queries;
+};
+
 template <int BITS, int NRS>
-hipError_t launch_sessions(const AttnArgs& a, const SessionTable& t, hipStream_t stream) {
+hipError_t launch_sessions(const AttnArgs& a, const SessionTable& t, const GroupBytes& by,
+                           hipStream_t stream) {
   constexpr int NH = 4 * NRS;
   const size_t logits = (size_t)4 * NH * ((a.nsplit_fast > 0 ? kSessCpw : 1) * 64 + kRowPad);
   const size_t combine = (size_t)4 * NH * (128 + 2);
   const size_t lds = std::max(logits, combine) * sizeof(float);
   const uint32_t grid = a.nsess * a.units * a.nsplit_win + a.units * a.nsplit_fast;
+  TimedLaunch timed(KIVI_KERNEL_ATTN_SESSIONS, stream, by.prefix + by.suffixes + by.queries);
   k_attn_sessions<BITS, NRS><<<grid, kThreads, lds, stream>>>(a, t);
   return hipGetLastError();
 }
 
 template <int BITS, int NRS>
-hipError_t launch_shared(const AttnArgs& a, const SessionTable& t, hipStream_t stream) {
+hipError_t launch_shared(const AttnArgs& a, const SessionTable& t, const GroupBytes& by,
+                         hipStream_t stream) {
   // window / suffix chunks per session: the window workgroups of the per-session kernel
   const uint32_t nwin = a.nsess * a.units * a.nsplit_win;
   if (nwin > 0) {
     constexpr int NH = 4 * NRS;
     const size_t lds = (size_t)4 * NH * (128 + 2) * sizeof(float);
+    TimedLaunch timed(KIVI_KERNEL_ATTN_SESSIONS, stream, by.suffixes + by.queries);
     k_attn_sessions<BITS, NRS><<<nwin, kThreads, lds, stream>>>(a, t);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -2006,6 +2016,7 @@ hipError_t launch_shared(const AttnArgs& a, const SessionTable& t, hipStream_t s
   });
   if (configured != hipSuccess) return configured;
   const uint32_t rblocks = (a.nsess * a.gq + kShRows - 1) / kShRows;
+  TimedLaunch timed(KIVI_KERNEL_ATTN_SHARED, stream, by.prefix + by.queries);
   k_attn_shared<BITS><<<a.units * rblocks * a.nsplit_fast, kShThreads, kShLdsBytes, stream>>>(a);
   return hipGetLastError();
 }
@@ -2054,27 +2065,23 @@ hipError_t launch_sessions_attention(const SessionsProblem& p, float* workspace,
     }
     bool shared;
     const AttnArgs a = group_args(p, first, count, workspace, &shared);
+    // algorithmic bytes: the prefix once, every session's suffix, the queries
+    const double key_tok = g.D * g.bits / 8.0 + g.D * 8.0 / g.G;
+    const double val_tok = g.D * g.bits / 8.0 + g.ncg() * 8.0;
+    const double row = g.D * 4.0;
+    const double fp32_rows = (double)(p.seq - p.st.kq) + (double)(p.seq - p.st.vq);
+    const GroupBytes by{g.units * ((double)p.st.kq * key_tok + (double)p.st.vq * val_tok + fp32_rows * row),
+                        g.units * suffix_rows * row, count * (double)a.q_sess_stride * 4.0};
     hipError_t e = hipSuccess;
-    {
-      // algorithmic bytes: the prefix once, every session's suffix, queries and outputs
-      const double key_tok = g.D * g.bits / 8.0 + g.D * 8.0 / g.G;
-      const double val_tok = g.D * g.bits / 8.0 + g.ncg() * 8.0;
-      const double row = g.D * 4.0;
-      const double fp32_rows = (double)(p.seq - p.st.kq) + (double)(p.seq - p.st.vq);
-      const double bytes =
-          g.units * ((double)p.st.kq * key_tok + (double)p.st.vq * val_tok + (fp32_rows + suffix_rows) * row) +
-          2.0 * count * (double)a.q_sess_stride * 4.0;
-      TimedLaunch timed(KIVI_KERNEL_ATTN_PACKED, stream, bytes);
-      const int nrs = a.gq <= 4 ? 1 : 2;
-      switch (g.bits * 10 + nrs) {
-        case 21: e = shared ? launch_shared<2, 1>(a, t, stream) : launch_sessions<2, 1>(a, t, stream); break;
-        case 22: e = shared ? launch_shared<2, 2>(a, t, stream) : launch_sessions<2, 2>(a, t, stream); break;
-        case 41: e = shared ? launch_shared<4, 1>(a, t, stream) : launch_sessions<4, 1>(a, t, stream); break;
-        case 42: e = shared ? launch_shared<4, 2>(a, t, stream) : launch_sessions<4, 2>(a, t, stream); break;
-        case 81: e = shared ? launch_shared<8, 1>(a, t, stream) : launch_sessions<8, 1>(a, t, stream); break;
-        case 82: e = shared ? launch_shared<8, 2>(a, t, stream) : launch_sessions<8, 2>(a, t, stream); break;
-        default: e = hipErrorInvalidValue; break;
-      }
+    const int nrs = a.gq <= 4 ? 1 : 2;
+    switch (g.bits * 10 + nrs) {
+      case 21: e = shared ? launch_shared<2, 1>(a, t, by, stream) : launch_sessions<2, 1>(a, t, by, stream); break;
+      case 22: e = shared ? launch_shared<2, 2>(a, t, by, stream) : launch_sessions<2, 2>(a, t, by, stream); break;
+      case 41: e = shared ? launch_shared<4, 1>(a, t, by, stream) : launch_sessions<4, 1>(a, t, by, stream); break;
+      case 42: e = shared ? launch_shared<4, 2>(a, t, by, stream) : launch_sessions<4, 2>(a, t, by, stream); break;
+      case 81: e = shared ? launch_shared<8, 1>(a, t, by, stream) : launch_sessions<8, 1>(a, t, by, stream); break;
+      case 82: e = shared ? launch_shared<8, 2>(a, t, by, stream) : launch_sessions<8, 2>(a, t, by, stream); break;
+      default: e = hipErrorInvalidValue; break;
     }
     if (e != hipSuccess) return e;
     const double bytes = (double)count * g.units * a.gq * ((double)a.nsplit_total * (g.D + 2) + g.D) * 4.0;

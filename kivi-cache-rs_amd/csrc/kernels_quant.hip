@@ -4,8 +4,9 @@
 // Bit-exactness with the reference (src/quant.rs:453-485): scale = span/levels and
 // code = clamp(rint((x - zero)/scale), 0, levels) use IEEE-correct f32 division (hipcc's
 // default; -ffast-math and reciprocal-multiply are never used) and v_rndne (round half to
-// even, equal to the reference's floor-based rounding for every finite input). min/max are
-// order independent, so the reduction order is free.
+// even, equal to the reference's floor-based rounding for every finite input). The value of
+// a min/max does not depend on the reduction order; the sign of a zero minimum does, and
+// follows the first-zero rule of common.hpp in every kernel here.
 #include "common.hpp"
 #include "kivi.h"
 
@@ -481,6 +482,8 @@ __global__ void __launch_bounds__(kThreads)
     float2 sz[CPL];
     float inv[CPL];
     uint32_t sh[CPL];
+    float mns[CPL], mxs[CPL];
+    bool zero_min = false;
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
       float mn = INFINITY, mx = -INFINITY;
@@ -489,7 +492,18 @@ __global__ void __launch_bounds__(kThreads)
         mn = fminf(mn, x[t][j]);
         mx = fmaxf(mx, x[t][j]);
       }
-      if (mn == 0.f) mn = first_zero(rows + CPL * lane + j, D, GG);  // the group's first zero
+      mns[j] = mn;
+      mxs[j] = mx;
+      zero_min |= mn == 0.f;
+    }
+    if (__ballot(zero_min)) {  // rare, and wave-uniform: a zero minimum takes its first zero's sign
+#pragma unroll
+      for (int j = 0; j < CPL; ++j)
+        if (mns[j] == 0.f) mns[j] = first_zero(rows + CPL * lane + j, D, GG);
+    }
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const float mn = mns[j], mx = mxs[j];
       sz[j] = make_float2(scale_of(mx - mn, levels), mn);
       inv[j] = quant_inv(sz[j].x);
       sh[j] = code_shift(BITS, (CPL * lane + j) % PPW);
@@ -574,12 +588,6 @@ __global__ void __launch_bounds__(kThreads)
           load_lane<CPL>(row, lane, x[p]);
         }
       }
-      // the row slot p loaded (both load paths above address the same row)
-      auto value_row = [&](uint32_t p) -> const float* {
-        const uint32_t pc = p < p_lo ? p_lo : p > p_hi ? p_hi : p;
-        const uint64_t i = t0 + pc - vq0;
-        return i < n_ring ? source_row(ring, unit, i, R, D) : source_row(in, unit, i - n_ring, R, D);
-      };
       uint32_t word[CPL][WPW];
 #pragma unroll
       for (int j = 0; j < CPL; ++j)
@@ -600,7 +608,13 @@ __global__ void __launch_bounds__(kThreads)
         float mn_r, mx_r;
         row_minmax16(pmn, pmx, mn_r, mx_r);
         const uint32_t r = lane % 16;
-        if (mn_r == 0.f) mn_r = first_zero(value_row(r) + cg * GG, 1, GG);  // row r's first zero
+        if (__ballot(mn_r == 0.f)) {  // rare, and wave-uniform: row r's first zero gives the sign
+          if (mn_r == 0.f) {
+            const uint64_t i = t0 + (r < p_lo ? p_lo : r > p_hi ? p_hi : r) - vq0;
+            const float* row = i < n_ring ? source_row(ring, unit, i, R, D) : source_row(in, unit, i - n_ring, R, D);
+            mn_r = first_zero(row + cg * GG, 1, GG);
+          }
+        }
         const float scale_r = scale_of(mx_r - mn_r, levels);
         const float inv_r = quant_inv(scale_r);
         if (t0 + r >= t_lo && t0 + r < t_hi) {
@@ -627,7 +641,11 @@ __global__ void __launch_bounds__(kThreads)
 #pragma unroll
           for (int j = 1; j < CPL; ++j) minmax_with(mn, mx, x[p][j], x[p][j]);
           group_minmax<L>(mn, mx);
-          if (mn == 0.f) mn = first_zero(value_row(p) + cg * GG, 1, GG);  // row p's first zero
+          if (__ballot(mn == 0.f)) {  // rare, and wave-uniform: row p's first zero gives the sign
+            const uint64_t i = t0 + ((uint32_t)p < p_lo ? p_lo : (uint32_t)p > p_hi ? p_hi : (uint32_t)p) - vq0;
+            const float* row = i < n_ring ? source_row(ring, unit, i, R, D) : source_row(in, unit, i - n_ring, R, D);
+            if (mn == 0.f) mn = first_zero(row + cg * GG, 1, GG);
+          }
           const float scale = scale_of(mx - mn, levels);
           const float inv = quant_inv(scale);
           if (valid) {
@@ -835,6 +853,172 @@ __global__ void __launch_bounds__(kThreads)
 }
 
 // ------------------------------------------------------------------ standalone codec (reference order)
+// The wave forms (head_dim = 64*CPL, CPL = 1, 2, 4): a lane holds channels CPL*lane .. +CPL-1
+// of each row in registers, as the cache's quantizers do, and the codes are packed straight
+// into the reference order. Units are contiguous in both the input and the output, so the
+// kernels index groups (keys) and rows (values) over all units at once.
+
+template <int N>
+__device__ __forceinline__ void store_words(uint32_t* p, const uint32_t (&w)[N]) {
+  typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+  typedef uint32_t u2v __attribute__((ext_vector_type(2)));
+  if constexpr (N % 4 == 0) {
+#pragma unroll
+    for (int i = 0; i < N; i += 4) *reinterpret_cast<u4v*>(p + i) = u4v{w[i], w[i + 1], w[i + 2], w[i + 3]};
+  } else if constexpr (N % 2 == 0) {
+#pragma unroll
+    for (int i = 0; i < N; i += 2) *reinterpret_cast<u2v*>(p + i) = u2v{w[i], w[i + 1]};
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; ++i) p[i] = w[i];
+  }
+}
+
+// quantize_per_channel (src/quant.rs:153-191 -> append_key_block :275-328): wave per group
+// (grid-stride over all units' groups). Word (q*D + d)*ipc + w of group q holds tokens
+// w*ppw .. w*ppw+ppw-1 of channel d, first token in the low bits: all of them are the lane's
+// own codes, so a lane packs its CPL*ipc consecutive words and stores them in one go.
+template <int BITS, int CPL, int GG>
+__global__ void __launch_bounds__(kThreads)
+    k_codec_keys_wave(const float* data, uint64_t groups, uint32_t* codes, float* params) {
+  constexpr uint32_t D = 64 * CPL, PPW = 32 / BITS, IPC = GG / PPW;
+  constexpr uint32_t kLevels = (1u << BITS) - 1u;
+  constexpr float levels = static_cast<float>(kLevels);
+  const uint32_t lane = threadIdx.x % 64;
+  for (uint64_t q = (uint64_t)blockIdx.x * 4 + threadIdx.x / 64; q < groups; q += (uint64_t)gridDim.x * 4) {
+    const float* rows = data + q * GG * D;
+    float x[GG][CPL];
+#pragma unroll
+    for (int t = 0; t < GG; ++t) load_lane<CPL>(rows + (uint64_t)t * D, lane, x[t]);
+    float2* pp = reinterpret_cast<float2*>(params) + q * D + CPL * lane;
+    uint32_t w[CPL * IPC];
+    float mns[CPL], mxs[CPL];
+    bool zero_min = false;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      float mn = INFINITY, mx = -INFINITY;
+#pragma unroll
+      for (int t = 0; t < GG; ++t) {
+        mn = fminf(mn, x[t][j]);
+        mx = fmaxf(mx, x[t][j]);
+      }
+      mns[j] = mn;
+      mxs[j] = mx;
+      zero_min |= mn == 0.f;
+    }
+    if (__ballot(zero_min)) {  // rare, and wave-uniform: a zero minimum takes its first zero's sign
+#pragma unroll
+      for (int j = 0; j < CPL; ++j)
+        if (mns[j] == 0.f) mns[j] = first_zero(rows + CPL * lane + j, D, GG);
+    }
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const float mn = mns[j];
+      const float scale = scale_of(mxs[j] - mn, levels), inv = quant_inv(scale);
+      pp[j] = make_float2(scale, mn);
+#pragma unroll
+      for (int k = 0; k < (int)IPC; ++k) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int i = 0; i < (int)PPW; ++i)
+          word |= quant_code_fast(x[k * PPW + i][j], mn, scale, inv, kLevels) << (BITS * i);
+        w[j * IPC + k] = word;
+      }
+    }
+    store_words<CPL * IPC>(codes + (q * D + CPL * lane) * IPC, w);
+  }
+}
+
+// quantize_per_token (src/quant.rs:193-233 -> append_value_block :330-377): wave per 16
+// consecutive rows (grid-stride over all units' rows). Group min/max as the cache's value
+// quantizer takes them (the 16-lane butterfly when a channel group is a DPP row). Word
+// r*(D/ppw) + j of row r holds channels j*ppw .. j*ppw+ppw-1, first channel in the low bits:
+// the LPW lanes of a word OR their parts (DPP), lane m keeps rows p = m (mod LPW), and every
+// store writes 64 consecutive words; (scale, zero) of (row r, group cg) at r*(D/G) + cg.
+template <int BITS, int CPL, int GG>
+__global__ void __launch_bounds__(kThreads)
+    k_codec_values_wave(const float* data, uint64_t rows, uint32_t* codes, float* params) {
+  constexpr uint32_t D = 64 * CPL, PPW = 32 / BITS, NCG = D / GG;
+  constexpr uint32_t LPW = PPW / CPL;  // lanes per code word
+  constexpr uint32_t KW = D / PPW;     // words per row (= 64 / LPW)
+  constexpr uint32_t NS = 16 / LPW;    // words kept per lane
+  constexpr uint32_t L = GG / CPL;     // lanes per channel group
+  constexpr uint32_t kLevels = (1u << BITS) - 1u;
+  constexpr float levels = static_cast<float>(kLevels);
+  const uint32_t lane = threadIdx.x % 64;
+  const uint32_t cg = CPL * lane / GG;
+  const uint32_t m = lane % LPW;
+  const uint64_t slabs = (rows + 15) / 16;
+  for (uint64_t sl = (uint64_t)blockIdx.x * 4 + threadIdx.x / 64; sl < slabs; sl += (uint64_t)gridDim.x * 4) {
+    const uint64_t r0 = sl * 16;
+    const uint32_t nvalid = static_cast<uint32_t>(rows - r0 < 16 ? rows - r0 : 16);
+    float x[16][CPL];
+#pragma unroll
+    for (int p = 0; p < 16; ++p) {
+      const uint32_t pc = (uint32_t)p < nvalid ? (uint32_t)p : nvalid - 1;  // rows past the end: the last
+      load_lane<CPL>(data + (r0 + pc) * D, lane, x[p]);
+    }
+    uint32_t keep[NS];
+#pragma unroll
+    for (int k = 0; k < (int)NS; ++k) keep[k] = 0;
+    float2* pp = reinterpret_cast<float2*>(params);
+    if constexpr (L == 16) {
+      float pmn[16], pmx[16];
+#pragma unroll
+      for (int p = 0; p < 16; ++p) {
+        pmn[p] = pmx[p] = x[p][0];
+#pragma unroll
+        for (int j = 1; j < CPL; ++j) minmax_with(pmn[p], pmx[p], x[p][j], x[p][j]);
+      }
+      float mn_r, mx_r;
+      row_minmax16(pmn, pmx, mn_r, mx_r);
+      const uint32_t r = lane % 16;
+      if (__ballot(mn_r == 0.f)) {  // rare, and wave-uniform: row r's first zero gives the sign
+        if (mn_r == 0.f && r < nvalid) mn_r = first_zero(data + (r0 + r) * D + cg * GG, 1, GG);
+      }
+      const float scale_r = scale_of(mx_r - mn_r, levels);
+      const float inv_r = quant_inv(scale_r);
+      if (r < nvalid) pp[(r0 + r) * NCG + cg] = make_float2(scale_r, mn_r);
+#pragma unroll
+      for (int p = 0; p < 16; ++p) {
+        const float scale = row_bcast(scale_r, p), inv = row_bcast(inv_r, p), zero = row_bcast(mn_r, p);
+        uint32_t part = 0;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j)
+          part |= quant_code_fast(x[p][j], zero, scale, inv, kLevels) << (BITS * ((CPL * lane + j) % PPW));
+        part = group_or<LPW>(part);
+        if (m == (uint32_t)p % LPW) keep[p / LPW] = part;
+      }
+    } else {
+#pragma unroll
+      for (int p = 0; p < 16; ++p) {
+        float mn = x[p][0], mx = x[p][0];
+#pragma unroll
+        for (int j = 1; j < CPL; ++j) minmax_with(mn, mx, x[p][j], x[p][j]);
+        group_minmax<L>(mn, mx);
+        if (__ballot(mn == 0.f)) {  // rare, and wave-uniform: row p's first zero gives the sign
+          if (mn == 0.f && (uint32_t)p < nvalid) mn = first_zero(data + (r0 + p) * D + cg * GG, 1, GG);
+        }
+        const float scale = scale_of(mx - mn, levels), inv = quant_inv(scale);
+        if (lane % L == 0 && (uint32_t)p < nvalid) pp[(r0 + p) * NCG + cg] = make_float2(scale, mn);
+        uint32_t part = 0;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j)
+          part |= quant_code_fast(x[p][j], mn, scale, inv, kLevels) << (BITS * ((CPL * lane + j) % PPW));
+        part = group_or<LPW>(part);
+        if (m == (uint32_t)p % LPW) keep[p / LPW] = part;
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < (int)NS; ++k) {
+      const uint32_t p = k * LPW + m;
+      if (p < nvalid) codes[(r0 + p) * KW + lane / LPW] = keep[k];
+    }
+  }
+}
+
+// The general forms (any head_dim and group): one workgroup per (unit, group) for keys, one
+// thread per (row, channel group) for values.
 
 // quantize_per_channel (src/quant.rs:153-191 -> append_key_block :275-328), one workgroup per
 // (unit, group), words (g*D + d)*ipc + w.
@@ -1168,11 +1352,63 @@ hipError_t copy_units(void* dst, size_t dst_pitch, const void* src, size_t src_p
                           stream);
 }
 
+// Wave-form instantiations of the standalone codec: channels per lane 1, 2, 4 and the groups
+// the cache's quantizers take (false: the general kernel runs).
+#define KIVI_CODEC_CASES(X) X(1, 16) X(1, 32) X(1, 64) X(2, 16) X(2, 32) X(2, 64) X(4, 16) X(4, 32)
+template <int BITS>
+bool codec_keys_bits(uint32_t cpl, uint32_t G, unsigned grid, hipStream_t stream, const float* data,
+                     uint64_t groups, uint32_t* codes, float* params) {
+#define KIVI_CK(C, GG)                                                                     \
+  case C * 1000 + GG:                                                                      \
+    k_codec_keys_wave<BITS, C, GG><<<grid, kThreads, 0, stream>>>(data, groups, codes, params); \
+    return true;
+  switch (cpl * 1000 + G) {
+    KIVI_CODEC_CASES(KIVI_CK)
+    default: return false;
+  }
+#undef KIVI_CK
+}
+template <int BITS>
+bool codec_values_bits(uint32_t cpl, uint32_t G, unsigned grid, hipStream_t stream, const float* data,
+                       uint64_t rows, uint32_t* codes, float* params) {
+#define KIVI_CV(C, GG)                                                                        \
+  case C * 1000 + GG:                                                                         \
+    k_codec_values_wave<BITS, C, GG><<<grid, kThreads, 0, stream>>>(data, rows, codes, params); \
+    return true;
+  switch (cpl * 1000 + G) {
+    KIVI_CODEC_CASES(KIVI_CV)
+    default: return false;
+  }
+#undef KIVI_CV
+}
+#undef KIVI_CODEC_CASES
+
+// Channels per lane of the wave forms for head_dim D (0: none) given the input's alignment.
+uint32_t codec_cpl(const float* data, uint32_t D) {
+  const uint32_t cpl = D / 64;
+  if (D % 64 != 0 || !(cpl == 1 || cpl == 2 || cpl == 4)) return 0;
+  return reinterpret_cast<uintptr_t>(data) % (4 * cpl) == 0 ? cpl : 0;
+}
+
 hipError_t launch_quant_ref_keys(const float* data, uint32_t units, uint64_t tokens, uint32_t D,
                                  uint32_t bits, uint32_t G, uint32_t* codes, float* params,
                                  hipStream_t stream) {
   const uint64_t blocks = (uint64_t)units * (tokens / G);
   if (blocks == 0) return hipSuccess;
+  const double elems = (double)units * tokens * D;
+  TimedLaunch timed(KIVI_KERNEL_CODEC_KEYS, stream, elems * (4.0 + bits / 8.0) + (double)blocks * D * 8.0);
+  const uint32_t cpl = codec_cpl(data, D);
+  if (cpl != 0) {
+    const unsigned grid = static_cast<unsigned>(std::min<uint64_t>((blocks + 3) / 4, 1u << 20));
+    bool done = false;
+    switch (bits) {
+      case 2: done = codec_keys_bits<2>(cpl, G, grid, stream, data, blocks, codes, params); break;
+      case 4: done = codec_keys_bits<4>(cpl, G, grid, stream, data, blocks, codes, params); break;
+      case 8: done = codec_keys_bits<8>(cpl, G, grid, stream, data, blocks, codes, params); break;
+      default: break;
+    }
+    if (done) return hipGetLastError();
+  }
   k_quant_ref_keys<<<static_cast<unsigned>(blocks), kThreads, (size_t)G * D, stream>>>(
       data, tokens, D, bits, G, codes, params);
   return hipGetLastError();
@@ -1183,6 +1419,21 @@ hipError_t launch_quant_ref_values(const float* data, uint32_t units, uint64_t t
                                    hipStream_t stream) {
   const uint64_t work = (uint64_t)units * tokens * (D / G);
   if (work == 0) return hipSuccess;
+  const uint64_t rows = (uint64_t)units * tokens;
+  TimedLaunch timed(KIVI_KERNEL_CODEC_VALUES, stream,
+                    (double)rows * (D * (4.0 + bits / 8.0) + (double)(D / G) * 8.0));
+  const uint32_t cpl = codec_cpl(data, D);
+  if (cpl != 0 && G % cpl == 0) {
+    const unsigned grid = static_cast<unsigned>(std::min<uint64_t>(((rows + 15) / 16 + 3) / 4, 1u << 20));
+    bool done = false;
+    switch (bits) {
+      case 2: done = codec_values_bits<2>(cpl, G, grid, stream, data, rows, codes, params); break;
+      case 4: done = codec_values_bits<4>(cpl, G, grid, stream, data, rows, codes, params); break;
+      case 8: done = codec_values_bits<8>(cpl, G, grid, stream, data, rows, codes, params); break;
+      default: break;
+    }
+    if (done) return hipGetLastError();
+  }
   k_quant_ref_values<<<grid_for(work), kThreads, 0, stream>>>(data, units, tokens, D, bits, G, codes, params);
   return hipGetLastError();
 }

@@ -661,7 +661,8 @@ class RagSession:
 
 # kivi_kernel_family (include/kivi.h)
 KERNEL_FAMILIES = {"attn_packed": 0, "attn_tail": 1, "attn_merge": 2, "quant_keys": 3,
-                   "quant_values": 4}
+                   "quant_values": 4, "attn_shared": 5, "attn_sessions": 6, "codec_keys": 7,
+                   "codec_values": 8}
 
 
 def timing_enable(backend, on=True):

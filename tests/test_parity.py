@@ -439,3 +439,27 @@ def test_decode_device_zero_minima_parity(amd, oracle, bits):
     got = ra.cache().export_streams()[3].reshape(heads, vq, dim // 32, 2)[..., 1]
     np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
     mem.free()
+
+
+@pytest.mark.parametrize("bits", [2, 4, 8])
+@pytest.mark.parametrize("dim,group", [(64, 16), (64, 32), (64, 64), (128, 16), (128, 64),
+                                       (256, 16), (256, 32), (256, 64), (96, 32)])
+def test_standalone_codec_lane_layouts_parity(amd, oracle, bits, dim, group):
+    """quantize_per_channel / quantize_per_token on the wave forms (head_dim 64/128/256: 1, 2
+    or 4 channels per lane) and the general kernels (head_dim 96, 4 channels per lane with
+    G=64): several units, many groups, and for values a row count that leaves a partial
+    16-row slab. Codes, (scale, zero), pytorch order and dequantize bit-exact."""
+    if group * bits % 32:
+        pytest.skip("invalid group for bits")
+    rng = np.random.default_rng(dim * 7 + group + bits)
+    batch, heads = 2, 3
+    for fn, tokens in ((kivi.quantize_per_channel, 9 * group), (kivi.quantize_per_token, 37)):
+        data = rng.standard_normal((batch, heads, tokens, dim)).astype(np.float32)
+        data[:, :, :, 5] *= np.float32(10.0)
+        flat = data.reshape(-1)
+        qa = fn(amd, flat, batch, heads, tokens, dim, bits, group)
+        qo = fn(oracle, flat, batch, heads, tokens, dim, bits, group)
+        assert np.array_equal(qa.codes(), qo.codes()), fn.__name__
+        assert np.array_equal(qa.scale_zero().view(np.uint32), qo.scale_zero().view(np.uint32)), fn.__name__
+        assert np.array_equal(qa.pytorch_codes(), qo.pytorch_codes()), fn.__name__
+        assert np.array_equal(qa.dequantize().view(np.uint32), qo.dequantize().view(np.uint32)), fn.__name__
