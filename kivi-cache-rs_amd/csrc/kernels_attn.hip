@@ -1225,6 +1225,8 @@ constexpr uint32_t kShBufHalves = 2 * 64 * kShKRow + 2 * 128 * kShVRow;  // khi,
 constexpr uint32_t kShParamFloats = 1024;  // keys [2 groups][128][2], values [4 groups][64][2]
 constexpr size_t kShLdsBytes = 2 * (size_t)kShBufHalves * sizeof(_Float16) + 2 * kShParamFloats * sizeof(float);
 constexpr float kShPScale = 16384.f;   // P operands are p * 2^14 (p <= 1)
+constexpr uint32_t kShOutRow = 128 + 4;  // partial row (acc[128], m, l) in LDS, 16 B aligned
+static_assert((size_t)kShRows * kShOutRow * sizeof(float) <= kShLdsBytes, "partials fit the chunk buffers");
 
 typedef uint32_t ux4 __attribute__((ext_vector_type(4)));
 
@@ -1683,21 +1685,32 @@ __device__ __forceinline__ void shared_split(const AttnArgs& a, uint32_t unit, u
     __syncthreads();  // the buffer is rewritten by the next chunk
   }
   l += __shfl_xor(l, 32);
-  if (!live) return;
-  float* part = a.ws + (uint64_t)sess * a.ws_sess_stride +
-                (((uint64_t)unit * a.nsplit_total + split) * gq + head) * (D + 2);
+  // Partials through LDS, so that the global stores are whole rows of consecutive lanes:
+  // (acc[128], m, l) of the wave's row r at LDS row r of its block (stride kShOutRow floats).
+  float* ob = reinterpret_cast<float*>(lds) + (size_t)wave * 32 * kShOutRow;
+  __syncthreads();  // every wave is done with the chunk buffers
   // O^T value v of tile mt is channel 32mt + 8(v/4) + 4h + v%4
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4) {
-      const float4 v = make_float4(o[mt][4 * q4] * o_unscale, o[mt][4 * q4 + 1] * o_unscale,
-                                   o[mt][4 * q4 + 2] * o_unscale, o[mt][4 * q4 + 3] * o_unscale);
-      *reinterpret_cast<float4*>(part + 32 * mt + 8 * q4 + 4 * h) = v;
-    }
+    for (int q4 = 0; q4 < 4; ++q4)
+      *reinterpret_cast<float4*>(ob + r * kShOutRow + 32 * mt + 8 * q4 + 4 * h) =
+          make_float4(o[mt][4 * q4] * o_unscale, o[mt][4 * q4 + 1] * o_unscale, o[mt][4 * q4 + 2] * o_unscale,
+                      o[mt][4 * q4 + 3] * o_unscale);
   if (h == 0) {
-    part[D] = c1 > c0 ? m : -INFINITY;
-    part[D + 1] = c1 > c0 ? l / kShPScale : 0.f;
+    ob[r * kShOutRow + D] = c1 > c0 ? m : -INFINITY;
+    ob[r * kShOutRow + D + 1] = c1 > c0 ? l / kShPScale : 0.f;
+  }
+  __syncthreads();
+  // row rr of the wave, float2 f of its 65: the partial of (session, head) at its workspace row
+  const uint32_t row0 = rblk * kShRows + wave * 32;
+  for (uint32_t i = lane; i < 32 * 65; i += 64) {
+    const uint32_t rr = i / 65, f = i % 65;
+    const uint32_t rg = row0 + rr, se = rg / gq, hd = rg % gq;
+    if (se < a.nsess) {
+      float* part = a.ws + (uint64_t)se * a.ws_sess_stride + (((uint64_t)unit * a.nsplit_total + split) * gq + hd) * (D + 2);
+      *reinterpret_cast<float2*>(part + 2 * f) = *reinterpret_cast<const float2*>(ob + rr * kShOutRow + 2 * f);
+    }
   }
 }
 
