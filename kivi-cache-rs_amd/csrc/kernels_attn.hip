@@ -1094,13 +1094,13 @@ __global__ void __launch_bounds__(kThreads) k_attn_sessions(AttnArgs a, SessionT
   }
 }
 
-// Log-sum-exp merge of the split partials: one workgroup per (session, unit, head) of
-// `parts` groups of dt = ceil(D/64)*64 threads. Thread (part, d) reads splits part, part +
-// parts, ... (kMergeBatch per round of independent loads, each split's (m, l) with its channel
-// d) and keeps a running (max, sum, channel sum) of its own; the parts meet in LDS. A merge is
-// one round of load latency for up to parts * kMergeBatch splits.
-constexpr uint32_t kMergeBatch = 16;
-constexpr uint32_t kMergeThreads = 1024;
+// Log-sum-exp merge of the split partials. One wave per output row (session, unit, head), or
+// `parts` waves (2 or 4) that take every parts-th split and meet in LDS. Lane l owns channels
+// l, l + 64, ... (CPL of them); the splits' (m, l) are wave-uniform loads, so each weight
+// exp2(m - max) is computed once per wave, not once per channel. Loads go out in rounds of
+// kMergeBatch / CPL splits, all independent.
+constexpr uint32_t kMergeThreads = 256;  // 4 waves
+constexpr uint32_t kMergeBatch = 32;     // loads per lane in flight per round
 
 // Rows of a decode token the attention launch consumed from its inputs, written to the key
 // residual and the value window once that launch is over (null k: nothing to write).
@@ -1112,89 +1112,122 @@ struct PendRows {
   uint32_t kslot, vslot, R;
 };
 
+template <int CPL>
 __global__ void __launch_bounds__(kMergeThreads)
-    k_attn_merge(const float* ws, uint32_t nsplit, uint32_t gq, uint32_t D, uint32_t heads,
-                 uint32_t qh, float* out, uint32_t units, uint64_t ws_sess_stride,
+    k_attn_merge(const float* ws, uint32_t nsplit, uint32_t parts, uint32_t gq, uint32_t D, uint32_t heads,
+                 uint32_t qh, float* out, uint32_t units, uint32_t rows, uint64_t ws_sess_stride,
                  uint64_t out_sess_stride, PendRows pend) {
-  __shared__ float red[kMergeThreads];
-  __shared__ float red_m[kMergeThreads / 64], red_l[kMergeThreads / 64];
-  const uint32_t sess = blockIdx.x / (units * gq);
-  const uint32_t unit = (blockIdx.x / gq) % units, h = blockIdx.x % gq;
-  const uint32_t b = unit / heads, kvh = unit % heads;
-  const uint32_t dt = std::min(kMergeThreads, (D + 63) / 64 * 64);
-  const uint32_t parts = blockDim.x / dt, part = threadIdx.x / dt, dl = threadIdx.x % dt;
-  const uint64_t stride = (uint64_t)gq * (D + 2);
-  const float* base = ws + sess * ws_sess_stride + (uint64_t)unit * nsplit * stride + h * (D + 2);
-  float* o = out + sess * out_sess_stride + ((uint64_t)b * qh + kvh * gq + h) * D;
-  if (pend.k != nullptr && sess == 0 && h == 0) {
-    for (uint32_t d = threadIdx.x; d < D; d += blockDim.x) {
-      pend.kres[((uint64_t)unit * pend.R + pend.kslot) * D + d] = pend.k[(uint64_t)unit * D + d];
-      pend.vring[((uint64_t)unit * pend.R + pend.vslot) * D + d] = pend.v[(uint64_t)unit * D + d];
-    }
-  }
-  for (uint32_t d0 = 0; d0 < D; d0 += dt) {
-    const uint32_t d = d0 + dl, dr = d < D ? d : D - 1;
-    float mp = -INFINITY, lp = 0.f, acc = 0.f;  // this part's running max, sum, channel sum
-    for (uint32_t s0 = part; s0 < nsplit; s0 += parts * kMergeBatch) {
-      float v[kMergeBatch], ms[kMergeBatch], ls[kMergeBatch];
+  constexpr uint32_t SB = kMergeBatch / CPL;
+  __shared__ float xch[4][2 + 64 * CPL];  // per wave: (m, l), then the channel sums
+  const uint32_t lane = threadIdx.x % 64;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+  const uint32_t row = blockIdx.x * (4 / parts) + wave / parts, part = wave % parts;
+  const bool live = row < rows;
+  float mp = -INFINITY, lp = 0.f, acc[CPL];
 #pragma unroll
-      for (uint32_t j = 0; j < kMergeBatch; ++j) {
+  for (int i = 0; i < CPL; ++i) acc[i] = 0.f;
+  uint32_t sess = 0, unit = 0, h = 0;
+  if (live) {
+    sess = row / (units * gq);
+    unit = (row / gq) % units;
+    h = row % gq;
+    const uint64_t stride = (uint64_t)gq * (D + 2);
+    const float* base = ws + sess * ws_sess_stride + (uint64_t)unit * nsplit * stride + h * (D + 2);
+    for (uint32_t s0 = part; s0 < nsplit; s0 += parts * SB) {
+      float v[SB][CPL], ms[SB], ls[SB];
+#pragma unroll
+      for (uint32_t j = 0; j < SB; ++j) {
         const uint32_t s = s0 + j * parts;
-        const float* ps = base + (uint64_t)(s < nsplit ? s : 0u) * stride;
-        v[j] = ps[dr];
+        const float* ps = base + (uint64_t)(s < nsplit ? s : part) * stride;
         ms[j] = s < nsplit ? ps[D] : -INFINITY;
         ls[j] = ps[D + 1];
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+          const uint32_t c = lane + 64 * i;
+          v[j][i] = ps[c < D ? c : 0];
+        }
       }
       float bm = mp;
 #pragma unroll
-      for (uint32_t j = 0; j < kMergeBatch; ++j) bm = fmaxf(bm, ms[j]);
+      for (uint32_t j = 0; j < SB; ++j) bm = fmaxf(bm, ms[j]);
       if (bm != -INFINITY) {
         const float r = __builtin_amdgcn_exp2f(mp - bm);  // 0 while mp is -inf
-        acc *= r;
         lp *= r;
 #pragma unroll
-        for (uint32_t j = 0; j < kMergeBatch; ++j) {
+        for (int i = 0; i < CPL; ++i) acc[i] *= r;
+#pragma unroll
+        for (uint32_t j = 0; j < SB; ++j) {
           const float f = ms[j] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms[j] - bm);
-          acc = fmaf(v[j], f, acc);
           lp = fmaf(ls[j], f, lp);
+#pragma unroll
+          for (int i = 0; i < CPL; ++i) acc[i] = fmaf(v[j][i], f, acc[i]);
         }
         mp = bm;
       }
     }
-    if (parts > 1) {
-      red[threadIdx.x] = acc;
-      if (dl == 0) {
-        red_m[part] = mp;
-        red_l[part] = lp;
-      }
-      __syncthreads();
-      if (part == 0) {
-        float M = -INFINITY;
-        for (uint32_t q = 0; q < parts; ++q) M = fmaxf(M, red_m[q]);
-        acc = 0.f;
-        lp = 0.f;
-        for (uint32_t q = 0; q < parts; ++q) {
-          const float f = red_m[q] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(red_m[q] - M);
-          acc = fmaf(red[q * dt + dl], f, acc);
-          lp = fmaf(red_l[q], f, lp);
-        }
-      }
-      __syncthreads();
+  }
+  if (parts > 1) {
+    if (lane == 0) {
+      xch[wave][0] = mp;
+      xch[wave][1] = lp;
     }
-    if (part == 0 && d < D) o[d] = acc / lp;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) xch[wave][2 + lane + 64 * i] = acc[i];
+    __syncthreads();
+    if (part == 0 && live) {
+      float M = -INFINITY;
+      for (uint32_t q = 0; q < parts; ++q) M = fmaxf(M, xch[wave + q][0]);
+      lp = 0.f;
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) acc[i] = 0.f;
+      for (uint32_t q = 0; q < parts; ++q) {
+        const float mq = xch[wave + q][0];
+        const float f = mq == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mq - M);
+        lp = fmaf(xch[wave + q][1], f, lp);
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) acc[i] = fmaf(xch[wave + q][2 + lane + 64 * i], f, acc[i]);
+      }
+    }
+  }
+  if (part != 0 || !live) return;
+  const uint32_t b = unit / heads, kvh = unit % heads;
+  float* o = out + sess * out_sess_stride + ((uint64_t)b * qh + kvh * gq + h) * D;
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    const uint32_t c = lane + 64 * i;
+    if (c < D) o[c] = acc[i] / lp;
+  }
+  if (pend.k != nullptr && sess == 0 && h == 0) {
+    for (uint32_t d = lane; d < D; d += 64) {
+      pend.kres[((uint64_t)unit * pend.R + pend.kslot) * D + d] = pend.k[(uint64_t)unit * D + d];
+      pend.vring[((uint64_t)unit * pend.R + pend.vslot) * D + d] = pend.v[(uint64_t)unit * D + d];
+    }
   }
 }
 
-// Merge launch for `count` sessions of `units` units: split parts sized so each thread sums
-// about kMergeBatch splits.
+// Merge launch for `count` sessions of `units` units: parts per row so that a wave takes about
+// one round of loads.
 hipError_t launch_merge(const float* ws, uint32_t nsplit, uint32_t gq, uint32_t D, uint32_t heads,
                         uint32_t qh, float* out, uint32_t units, uint32_t count,
                         uint64_t ws_sess_stride, uint64_t out_sess_stride, hipStream_t stream,
                         PendRows pend = PendRows{}) {
-  const uint32_t dt = std::min(kMergeThreads, (D + 63) / 64 * 64);
-  const uint32_t parts = std::max(1u, std::min(kMergeThreads / dt, (nsplit + kMergeBatch - 1) / kMergeBatch));
-  k_attn_merge<<<count * units * gq, parts * dt, 0, stream>>>(ws, nsplit, gq, D, heads, qh, out, units,
-                                                              ws_sess_stride, out_sess_stride, pend);
+  const uint32_t cpl = D <= 64 ? 1 : D <= 128 ? 2 : D <= 256 ? 4 : D <= 512 ? 8 : 16;
+  const uint32_t sb = kMergeBatch / cpl;
+  const uint32_t want = (nsplit + sb - 1) / sb;
+  const uint32_t parts = want <= 1 ? 1 : want <= 2 ? 2 : 4;
+  const uint32_t rows = count * units * gq;
+  const uint32_t grid = (rows * parts + 3) / 4;
+#define KIVI_MERGE(C)                                                                                        \
+  k_attn_merge<C><<<grid, kMergeThreads, 0, stream>>>(ws, nsplit, parts, gq, D, heads, qh, out, units, rows, \
+                                                      ws_sess_stride, out_sess_stride, pend)
+  switch (cpl) {
+    case 1: KIVI_MERGE(1); break;
+    case 2: KIVI_MERGE(2); break;
+    case 4: KIVI_MERGE(4); break;
+    case 8: KIVI_MERGE(8); break;
+    default: KIVI_MERGE(16); break;
+  }
+#undef KIVI_MERGE
   return hipGetLastError();
 }
 
