@@ -67,10 +67,8 @@ struct AttnArgs {
   // batched sessions (0 otherwise): session count and the strides between consecutive
   // sessions' queries, partials and outputs
   uint32_t nsess;
-  // window / suffix workgroups mask tokens below t_min (0, or the prefix length when the
-  // shared-prefix GEMM covers the prefix's own fp32 band); the GEMM covers prefix chunks
-  // [0, gemm_end)
-  uint64_t t_min;
+  // the shared-prefix GEMM covers prefix chunks [0, gemm_end); k_attn_suffix takes the
+  // suffixes in nsplit_win runs per session
   uint32_t gemm_end;
   uint64_t q_sess_stride, ws_sess_stride;
   float* out;              // [batch][QH][D]
@@ -857,7 +855,7 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
         load_key_rows(a, unit, t0, quarter, lane, kr);
         key_fp32<NRS>(a, t0, quarter, lane, qv, kr, kUnit, lg);
       }
-      const bool live = !MIXED || (t0 + lane < total && t0 + lane >= a.t_min && lane / 16 == quarter);
+      const bool live = !MIXED || (t0 + lane < total && lane / 16 == quarter);
 #pragma unroll
       for (int rs = 0; rs < NRS; ++rs)
 #pragma unroll
@@ -1090,6 +1088,139 @@ __global__ void __launch_bounds__(kThreads) k_attn_sessions(AttnArgs a, SessionT
       as.ws = a.ws + s * a.ws_sess_stride;
       mfma_split<BITS, NRS, kSessCpw, false>(as, unit, split, lds);
       __syncthreads();  // the next session reuses the LDS
+    }
+  }
+}
+
+// Session suffixes of the shared-prefix form (fp32 rows, head_dim 128, GQA <= 8): one
+// workgroup per (session, unit, run of kSufTokens suffix tokens) writes one partial per head
+// into split nsplit_fast + run (runs past a session's suffix write empty partials). Keys: lane
+// pair (l, l + 32) of wave w owns token 32w + l%32, 64 channels each; values: lane l owns
+// channels 2l, 2l+1 of wave w's 32 tokens, and the four waves' sums meet in LDS. Every key and
+// value load of a workgroup is issued before the softmax.
+constexpr uint32_t kSufTokens = 128;
+constexpr uint32_t kSufMaxHeads = 8;
+
+__global__ void __launch_bounds__(kThreads) k_attn_suffix(AttnArgs a, SessionTable t) {
+  constexpr uint32_t D = 128;
+  __shared__ float qs[kSufMaxHeads][D];
+  __shared__ float sp[kSufMaxHeads][kSufTokens];
+  __shared__ float ml[kSufMaxHeads][2];
+  __shared__ float red[4][kSufMaxHeads][D];
+  const uint32_t lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+  const uint32_t gq = a.gq;
+  const uint32_t per_sess = a.units * a.nsplit_win;
+  const uint32_t sess = blockIdx.x / per_sess, rem = blockIdx.x % per_sess;
+  const uint32_t unit = rem / a.nsplit_win, run = rem % a.nsplit_win;
+  const SessionDesc d = t.d[sess];
+  const uint64_t t0 = (uint64_t)run * kSufTokens;
+  const uint32_t n = d.len > t0 ? static_cast<uint32_t>(std::min<uint64_t>(kSufTokens, d.len - t0)) : 0u;
+  const uint32_t b = unit / a.heads, kvh = unit % a.heads;
+  if (n == 0) {
+    // no token of this session in the run (its suffix arrays may be absent): empty partials
+    for (uint32_t h = wave; h < gq; h += 4) {
+      float* part = a.ws + (uint64_t)sess * a.ws_sess_stride +
+                    (((uint64_t)unit * a.nsplit_total + a.nsplit_fast + run) * gq + h) * (D + 2);
+      *reinterpret_cast<float2*>(part + 2 * lane) = make_float2(0.f, 0.f);
+      if (lane == 0) {
+        part[D] = -INFINITY;
+        part[D + 1] = 0.f;
+      }
+    }
+    return;
+  }
+  // queries in base-2 logit units
+  const float* qp = a.query + (uint64_t)sess * a.q_sess_stride + ((uint64_t)b * a.qh + kvh * gq) * D;
+  for (uint32_t i = threadIdx.x; i < gq * D; i += blockDim.x) qs[i / D][i % D] = qp[i] * a.scale2;
+  // this wave's tokens: keys (half a row per lane) and values (two channels per lane)
+  const uint32_t tk = 32 * wave + lane % 32, hh = lane / 32;
+  const float* krow = d.k + unit * d.stride + (t0 + (tk < n ? tk : 0)) * D + 64 * hh;
+  float4 kv[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) kv[i] = reinterpret_cast<const float4*>(krow)[i];
+  float2 vv[32];
+  const float* vbase = d.v + unit * d.stride + t0 * D + 2 * lane;
+#pragma unroll
+  for (int j = 0; j < 32; ++j) {
+    const uint32_t tv = 32 * wave + j;
+    vv[j] = *reinterpret_cast<const float2*>(vbase + (uint64_t)(tv < n ? tv : 0) * D);
+  }
+  __syncthreads();  // queries in LDS
+  float dot[kSufMaxHeads];
+#pragma unroll
+  for (uint32_t h = 0; h < kSufMaxHeads; ++h) {
+    float acc = 0.f;
+    if (h < gq) {
+      const float4* q4 = reinterpret_cast<const float4*>(&qs[h][64 * hh]);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float4 q = q4[i];
+        acc = fmaf(q.x, kv[i].x, acc);
+        acc = fmaf(q.y, kv[i].y, acc);
+        acc = fmaf(q.z, kv[i].z, acc);
+        acc = fmaf(q.w, kv[i].w, acc);
+      }
+    }
+    dot[h] = acc + __shfl_xor(acc, 32);
+  }
+  if (hh == 0) {
+#pragma unroll
+    for (uint32_t h = 0; h < kSufMaxHeads; ++h)
+      if (h < gq) sp[h][tk] = tk < n ? dot[h] : -INFINITY;
+  }
+  __syncthreads();
+  // softmax per head over the run's tokens (waves take heads w, w + 4)
+  for (uint32_t h = wave; h < gq; h += 4) {
+    const float s0 = sp[h][lane], s1 = sp[h][lane + 64];
+    float m = fmaxf(s0, s1);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    const float p0 = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s0 - m);
+    const float p1 = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s1 - m);
+    float l = p0 + p1;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) l += __shfl_xor(l, o);
+    sp[h][lane] = p0;
+    sp[h][lane + 64] = p1;
+    if (lane == 0) {
+      ml[h][0] = m;
+      ml[h][1] = l;
+    }
+  }
+  __syncthreads();
+  // value sums of this wave's tokens
+  float2 acc[kSufMaxHeads];
+#pragma unroll
+  for (uint32_t h = 0; h < kSufMaxHeads; ++h) acc[h] = make_float2(0.f, 0.f);
+#pragma unroll
+  for (int j = 0; j < 32; ++j) {
+#pragma unroll
+    for (uint32_t h = 0; h < kSufMaxHeads; ++h) {
+      if (h < gq) {
+        const float p = sp[h][32 * wave + j];  // 0 for tokens past n
+        acc[h].x = fmaf(p, vv[j].x, acc[h].x);
+        acc[h].y = fmaf(p, vv[j].y, acc[h].y);
+      }
+    }
+  }
+#pragma unroll
+  for (uint32_t h = 0; h < kSufMaxHeads; ++h)
+    if (h < gq) *reinterpret_cast<float2*>(&red[wave][h][2 * lane]) = acc[h];
+  __syncthreads();
+  for (uint32_t h = wave; h < gq; h += 4) {
+    float2 o = make_float2(0.f, 0.f);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float2 x = *reinterpret_cast<const float2*>(&red[w][h][2 * lane]);
+      o.x += x.x;
+      o.y += x.y;
+    }
+    float* part = a.ws + (uint64_t)sess * a.ws_sess_stride +
+                  (((uint64_t)unit * a.nsplit_total + a.nsplit_fast + run) * gq + h) * (D + 2);
+    *reinterpret_cast<float2*>(part + 2 * lane) = o;
+    if (lane == 0) {
+      part[D] = ml[h][0];
+      part[D + 1] = ml[h][1];
     }
   }
 }
@@ -1823,7 +1954,6 @@ AttnArgs make_args(const AttnProblem& p, float* ws) {
   a.out = p.out;
   a.units = p.cache.geo.units;
   a.nsess = 0;
-  a.t_min = 0;
   a.gemm_end = 0;
   a.q_sess_stride = a.ws_sess_stride = 0;
   return a;
@@ -2001,8 +2131,8 @@ bool use_shared(const SessionsProblem& sp, uint32_t nsess) {
 // multiple of 8 (the XCD count) where the chunks allow, so about kSharedTargetGroups
 // workgroups cover units x row blocks x splits.
 // The GEMM form covers every prefix chunk, [0, ceil(seq/64)) (the fp32 band of the prefix
-// too, as the prefix's smax covers those rows); the per-session window workgroups cover the
-// suffix only: chunks from floor(seq/64), tokens below seq masked.
+// too, as the prefix's smax covers those rows); k_attn_suffix covers each session's suffix
+// [seq, seq + len) in runs of kSufTokens.
 AttnArgs make_shared_args(const SessionsProblem& sp, uint32_t nsess, uint64_t max_suffix, float* ws) {
   AttnArgs a = make_session_args(sp, nsess, max_suffix, ws);
   const uint32_t rblocks = (nsess * a.gq + kShRows - 1) / kShRows;
@@ -2011,10 +2141,8 @@ AttnArgs make_shared_args(const SessionsProblem& sp, uint32_t nsess, uint64_t ma
   ns = (ns + 7) / 8 * 8;
   a.gemm_end = static_cast<uint32_t>((sp.seq + 63) / 64);
   a.nsplit_fast = a.gemm_end == 0 ? 0 : std::max(1u, std::min(ns, a.gemm_end));
-  a.t_min = sp.seq;
-  a.win_begin = static_cast<uint32_t>(sp.seq / 64);
-  a.win_end = static_cast<uint32_t>((sp.seq + max_suffix + 63) / 64);
-  a.nsplit_win = max_suffix > 0 ? a.win_end - a.win_begin : 0;
+  // suffixes: runs of kSufTokens tokens (k_attn_suffix)
+  a.nsplit_win = static_cast<uint32_t>((max_suffix + kSufTokens - 1) / kSufTokens);
   a.nsplit_total = a.nsplit_fast + a.nsplit_win + a.nsplit_gen;
   a.ws_sess_stride = (uint64_t)sp.cache.geo.units * a.nsplit_total * a.gq * (sp.cache.geo.D + 2);
   return a;
@@ -2045,10 +2173,8 @@ hipError_t launch_shared(const AttnArgs& a, const SessionTable& t, const GroupBy
   // window / suffix chunks per session: the window workgroups of the per-session kernel
   const uint32_t nwin = a.nsess * a.units * a.nsplit_win;
   if (nwin > 0) {
-    constexpr int NH = 4 * NRS;
-    const size_t lds = (size_t)4 * NH * (128 + 2) * sizeof(float);
     TimedLaunch timed(KIVI_KERNEL_ATTN_SESSIONS, stream, by.suffixes + by.queries);
-    k_attn_sessions<BITS, NRS><<<nwin, kThreads, lds, stream>>>(a, t);
+    k_attn_suffix<<<nwin, kThreads, 0, stream>>>(a, t);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
