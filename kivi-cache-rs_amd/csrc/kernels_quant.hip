@@ -757,58 +757,71 @@ __global__ void __launch_bounds__(kThreads)
 // ------------------------------------------------------------------ dense reconstruction
 
 // KiviCache::dequantize (src/cache.rs:282-325): packed tokens as fma(code, scale, zero)
-// (src/quant.rs:406, 443), residual tokens copied. Grid (row slices, units); a thread writes
-// four consecutive channels of a token (D % 4 == 0).
+// (src/quant.rs:406, 443), residual tokens copied. A workgroup takes one 64-token block of a
+// unit at a time: the block's value words are staged in LDS as [word][channel] (so the four
+// channels of a float4 are one 16-byte read) with their (scale, zero) pairs, and a thread
+// writes float4 runs of consecutive channels (D % 4 == 0) of keys and values.
 __global__ void __launch_bounds__(kThreads)
     k_dequant_cache(CacheView c, SeqState s, uint64_t seq, float* keys, float* values) {
+  extern __shared__ uint32_t stage[];  // [vw][D] words, then [ncg][64] (scale, zero)
   const Geometry& geo = c.geo;
   const uint32_t D = geo.D, G = geo.G, R = geo.R, bits = geo.bits, ppw = geo.ppw();
   const uint32_t kw = geo.kwords_per_token(), vw = geo.vwords_per_channel(), ncg = geo.ncg();
   const uint32_t mask = geo.levels();
   const uint32_t q4 = D / 4;
-  const uint64_t per_unit = seq * q4;
-  for (uint32_t unit = blockIdx.y; unit < geo.units; unit += gridDim.y)
-  for (uint64_t r = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; r < per_unit;
-       r += (uint64_t)gridDim.x * blockDim.x) {
+  float2* sprm = reinterpret_cast<float2*>(stage + vw * D);
+  const uint64_t nblk = (seq + kValueBlock - 1) / kValueBlock;
+  const uint64_t total = nblk * geo.units;
+  for (uint64_t job = blockIdx.x; job < total; job += gridDim.x) {
+    const uint32_t unit = static_cast<uint32_t>(job / nblk);
+    const uint64_t tb = job % nblk;
+    const uint64_t t0 = tb * kValueBlock;
+    const uint32_t ntok = static_cast<uint32_t>(std::min<uint64_t>(kValueBlock, seq - t0));
     const uint32_t* kc = c.kcodes + unit * geo.kcodes_unit();
     const float2* kp = reinterpret_cast<const float2*>(c.kparams + unit * geo.kparams_unit());
-    const uint32_t* vc = c.vcodes + unit * geo.vcodes_unit();
-    const float2* vp = reinterpret_cast<const float2*>(c.vparams + unit * geo.vparams_unit());
-    const uint64_t t = r / q4;
-    const uint32_t d0 = static_cast<uint32_t>(r - t * q4) * 4;
-    float k[4], v[4];
-    if (t < s.kq) {
-      // one code word holds the four channels (ppw >= 4); their (scale, zero) pairs are 32
-      // contiguous bytes
-      const uint32_t word = kc[t * kw + d0 / ppw];
-      const float4* pp = reinterpret_cast<const float4*>(kp + (t / G) * D + d0);
-      const float4 p01 = pp[0], p23 = pp[1];
-      const float sc[4] = {p01.x, p01.z, p23.x, p23.z}, zr[4] = {p01.y, p01.w, p23.y, p23.w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        k[e] = fmaf(static_cast<float>((word >> code_shift(bits, (d0 + e) % ppw)) & mask), sc[e], zr[e]);
-    } else {
-      const float4 x = *reinterpret_cast<const float4*>(c.kres + ((uint64_t)unit * R + (t - s.kq)) * D + d0);
-      k[0] = x.x; k[1] = x.y; k[2] = x.z; k[3] = x.w;
+    const bool packed_v = t0 < s.vq;
+    if (packed_v) {
+      const uint32_t* vc = c.vcodes + unit * geo.vcodes_unit() + tb * D * vw;
+      for (uint32_t i = threadIdx.x; i < D * vw; i += blockDim.x) stage[(i % vw) * D + i / vw] = vc[i];
+      const float2* vp = reinterpret_cast<const float2*>(c.vparams + unit * geo.vparams_unit()) + tb * ncg * kValueBlock;
+      for (uint32_t i = threadIdx.x; i < ncg * kValueBlock; i += blockDim.x) sprm[i] = vp[i];
     }
-    if (t < s.vq) {
-      const uint64_t tb = t / kValueBlock;
-      const uint32_t tt = static_cast<uint32_t>(t % kValueBlock);
-      const uint32_t sh = code_shift(bits, tt % ppw);
-      const float2 sz = vp[(tb * ncg + d0 / G) * kValueBlock + tt];  // one group holds the four (G % 4 == 0)
+    __syncthreads();
+    for (uint32_t r = threadIdx.x; r < ntok * q4; r += blockDim.x) {
+      const uint32_t tt = r / q4, d0 = (r % q4) * 4;
+      const uint64_t t = t0 + tt;
+      float k[4], v[4];
+      if (t < s.kq) {
+        // one code word holds the four channels (ppw >= 4); their (scale, zero) pairs are 32
+        // contiguous bytes
+        const uint32_t word = kc[t * kw + d0 / ppw];
+        const float4* pp = reinterpret_cast<const float4*>(kp + (t / G) * D + d0);
+        const float4 p01 = pp[0], p23 = pp[1];
+        const float sc[4] = {p01.x, p01.z, p23.x, p23.z}, zr[4] = {p01.y, p01.w, p23.y, p23.w};
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t word = vc[(tb * D + d0 + e) * vw + tt / ppw];
-        v[e] = fmaf(static_cast<float>((word >> sh) & mask), sz.x, sz.y);
+        for (int e = 0; e < 4; ++e)
+          k[e] = fmaf(static_cast<float>((word >> code_shift(bits, (d0 + e) % ppw)) & mask), sc[e], zr[e]);
+      } else {
+        const float4 x = *reinterpret_cast<const float4*>(c.kres + ((uint64_t)unit * R + (t - s.kq)) * D + d0);
+        k[0] = x.x; k[1] = x.y; k[2] = x.z; k[3] = x.w;
       }
-    } else {
-      const float4 x = *reinterpret_cast<const float4*>(
-          c.vring + ((uint64_t)unit * R + (s.vhead + (t - s.vq)) % R) * D + d0);
-      v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
+      if (t < s.vq) {
+        const uint32_t sh = code_shift(bits, tt % ppw);
+        const float2 sz = sprm[(d0 / G) * kValueBlock + tt];  // one group holds the four (G % 4 == 0)
+        const uint4 w = *reinterpret_cast<const uint4*>(stage + (tt / ppw) * D + d0);
+        const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = fmaf(static_cast<float>((ws[e] >> sh) & mask), sz.x, sz.y);
+      } else {
+        const float4 x = *reinterpret_cast<const float4*>(
+            c.vring + ((uint64_t)unit * R + (s.vhead + (t - s.vq)) % R) * D + d0);
+        v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
+      }
+      const uint64_t o = ((uint64_t)unit * seq + t) * D + d0;
+      *reinterpret_cast<float4*>(keys + o) = make_float4(k[0], k[1], k[2], k[3]);
+      *reinterpret_cast<float4*>(values + o) = make_float4(v[0], v[1], v[2], v[3]);
     }
-    const uint64_t o = ((uint64_t)unit * seq + t) * D + d0;
-    *reinterpret_cast<float4*>(keys + o) = make_float4(k[0], k[1], k[2], k[3]);
-    *reinterpret_cast<float4*>(values + o) = make_float4(v[0], v[1], v[2], v[3]);
+    __syncthreads();  // the staging buffer is refilled for the next block
   }
 }
 
@@ -1336,12 +1349,17 @@ hipError_t launch_dequant_cache(const CacheView& c, const SeqState& s, float* ke
   const uint64_t seq = s.kq + s.kres;
   const uint64_t work = seq * (c.geo.D / 4);
   if (work == 0) return hipSuccess;
-  if (reinterpret_cast<uintptr_t>(keys) % 16 != 0 || reinterpret_cast<uintptr_t>(values) % 16 != 0) {
+  const size_t lds = ((size_t)c.geo.vwords_per_channel() * c.geo.D + 2 * c.geo.ncg() * kValueBlock) * sizeof(uint32_t);
+  // unaligned outputs, and blocks whose staging would not fit the default 64 KB of LDS (wide
+  // heads with small groups): one element per thread
+  if (reinterpret_cast<uintptr_t>(keys) % 16 != 0 || reinterpret_cast<uintptr_t>(values) % 16 != 0 ||
+      lds > 65536) {
     k_dequant_cache_elem<<<grid_for(work * 4 * c.geo.units), kThreads, 0, stream>>>(c, s, seq, keys, values);
     return hipGetLastError();
   }
-  const unsigned slices = static_cast<unsigned>(std::min<uint64_t>((work + kThreads - 1) / kThreads, 4096));
-  k_dequant_cache<<<dim3(slices, std::min(c.geo.units, 65535u)), kThreads, 0, stream>>>(c, s, seq, keys, values);
+  const uint64_t blocks = (seq + kValueBlock - 1) / kValueBlock * c.geo.units;
+  k_dequant_cache<<<static_cast<unsigned>(std::min<uint64_t>(blocks, 8192)), kThreads, lds, stream>>>(
+      c, s, seq, keys, values);
   return hipGetLastError();
 }
 
