@@ -685,72 +685,96 @@ __global__ void __launch_bounds__(kThreads)
 // ------------------------------------------------------------------ export to reference order
 
 // Key words (g*D + d)*ipc + w hold tokens g*G + w*ppw + i of channel d (src/quant.rs:312-323).
-// Grid (group slices, units): a workgroup stages a group's token-major words in LDS (one
-// coalesced read), then writes the group's channel-major words (one coalesced write).
-constexpr uint32_t kExportGroups = 8;  // groups per workgroup
+// Grid (group slices, units): a workgroup stages its `per` groups' words in LDS at once
+// (coalesced reads, one barrier), then writes their channel-major words (coalesced writes);
+// the ppw codes of an output word are gathered with the shifts unrolled.
+constexpr uint32_t kExportGroups = 8;        // groups per workgroup, at most
+constexpr uint32_t kExportLdsWords = 16384;  // staging words per workgroup, at most (64 KB)
+template <int BITS>
 __global__ void __launch_bounds__(kThreads)
-    k_export_keys(CacheView c, uint64_t kq, uint32_t* out) {
-  extern __shared__ uint32_t words[];  // [G * D / ppw]
+    k_export_keys(CacheView c, uint64_t kq, uint32_t per, uint32_t* out) {
+  constexpr uint32_t PPW = 32 / BITS, MASK = (1u << BITS) - 1u;
+  // [per][kw][G + 4]: native word (token t, channel word k) at k * (G + 4) + t, so that the
+  // PPW tokens of an output word are 16-byte reads (rows 16-byte aligned, 4 words apart in
+  // banks between rows)
+  extern __shared__ uint32_t words[];
   const Geometry& geo = c.geo;
-  const uint32_t G = geo.G, bits = geo.bits, ppw = geo.ppw(), kw = geo.kwords_per_token();
-  const uint32_t ipc = G / ppw, n = G * kw;  // words per group, both orders
-  const uint32_t mask = geo.levels();
+  const uint32_t G = geo.G, kw = geo.kwords_per_token(), row = G + 4;
+  const uint32_t ipc = G / PPW, n = G * kw, np = kw * row;  // words per group, both orders
   const uint64_t ngroups = kq / G;
-  const uint64_t g_end = std::min<uint64_t>(ngroups, (uint64_t)(blockIdx.x + 1) * kExportGroups);
-  for (uint32_t unit = blockIdx.y; unit < geo.units; unit += gridDim.y)
-  for (uint64_t g = (uint64_t)blockIdx.x * kExportGroups; g < g_end; ++g) {
-    const uint32_t* src = c.kcodes + unit * geo.kcodes_unit();
-    uint32_t* dst = out + (uint64_t)unit * ngroups * n;
-    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) words[i] = src[g * n + i];
-    __syncthreads();
-    for (uint32_t o = threadIdx.x; o < n; o += blockDim.x) {
-      const uint32_t w = o % ipc, d = o / ipc;
-      const uint32_t sh = code_shift(bits, d % ppw);
-      uint32_t word = 0;
-      for (uint32_t i = 0; i < ppw; ++i)
-        word |= ((words[(w * ppw + i) * kw + d / ppw] >> sh) & mask) << (bits * i);
-      dst[g * n + o] = word;
+  const uint64_t g0 = (uint64_t)blockIdx.x * per;
+  const uint32_t ng = static_cast<uint32_t>(std::min<uint64_t>(per, ngroups - g0));
+  for (uint32_t unit = blockIdx.y; unit < geo.units; unit += gridDim.y) {
+    const uint32_t* src = c.kcodes + unit * geo.kcodes_unit() + g0 * n;
+    uint32_t* dst = out + (uint64_t)unit * ngroups * n + g0 * n;
+    for (uint32_t i = threadIdx.x; i < ng * n; i += blockDim.x) {
+      const uint32_t gg = i / n, r = i % n;
+      words[gg * np + (r % kw) * row + r / kw] = src[i];
     }
-    __syncthreads();  // the staging buffer is refilled for the next group
+    __syncthreads();
+    for (uint32_t o = threadIdx.x; o < ng * n; o += blockDim.x) {
+      const uint32_t gg = o / n, r = o % n, w = r % ipc, d = r / ipc;
+      const uint32_t sh = code_shift(BITS, d % PPW);
+      const uint4* tw = reinterpret_cast<const uint4*>(words + gg * np + (d / PPW) * row + w * PPW);
+      uint32_t word = 0;
+#pragma unroll
+      for (uint32_t q = 0; q < PPW / 4; ++q) {
+        const uint4 x = tw[q];
+        const uint32_t xs[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+        for (uint32_t e = 0; e < 4; ++e) word |= ((xs[e] >> sh) & MASK) << (BITS * (4 * q + e));
+      }
+      dst[o] = word;
+    }
+    __syncthreads();  // the staging buffer is refilled for the next unit
   }
 }
 
 // Value words (t*(D/G) + cg)*ipg + w = t*(D/ppw) + j hold channels j*ppw + i of token t
 // (src/quant.rs:362-372); params (t*(D/G) + cg)*2 (src/quant.rs:360-361). Grid (block slices,
-// units): a workgroup stages a 64-token block's channel-major words in LDS (one coalesced read)
-// and writes the block's token-major words and (scale, zero) pairs.
-constexpr uint32_t kExportBlocks = 4;  // 64-token blocks per workgroup
+// units): a workgroup stages its `per` 64-token blocks' channel-major words in LDS at once and
+// writes their token-major words and (scale, zero) pairs.
+constexpr uint32_t kExportBlocks = 4;  // 64-token blocks per workgroup, at most
+template <int BITS>
 __global__ void __launch_bounds__(kThreads)
-    k_export_values(CacheView c, uint64_t vq, uint32_t* out_codes, float* out_params) {
-  extern __shared__ uint32_t words[];  // [D * 64 / ppw]
+    k_export_values(CacheView c, uint64_t vq, uint32_t per, uint32_t* out_codes, float* out_params) {
+  constexpr uint32_t PPW = 32 / BITS, MASK = (1u << BITS) - 1u, VW = kValueBlock / PPW;
+  // [per][D * VW + D / PPW]: native word (channel c, w) at c * VW + w + c / PPW, so that the
+  // lanes gathering one output word each (channel runs PPW apart) hit distinct banks
+  extern __shared__ uint32_t words[];
   const Geometry& geo = c.geo;
-  const uint32_t D = geo.D, bits = geo.bits, ppw = geo.ppw(), vw = geo.vwords_per_channel();
-  const uint32_t ncg = geo.ncg(), wpt = D / ppw, n = D * vw;
-  const uint32_t mask = geo.levels();
+  const uint32_t D = geo.D, ncg = geo.ncg(), wpt = D / PPW, n = D * VW, np = n + D / PPW;
   const uint64_t nblk = (vq + kValueBlock - 1) / kValueBlock;
-  const uint64_t b_end = std::min<uint64_t>(nblk, (uint64_t)(blockIdx.x + 1) * kExportBlocks);
-  for (uint32_t unit = blockIdx.y; unit < geo.units; unit += gridDim.y)
-  for (uint64_t tb = (uint64_t)blockIdx.x * kExportBlocks; tb < b_end; ++tb) {
-    const uint32_t* src = c.vcodes + unit * geo.vcodes_unit();
-    const float2* prm = reinterpret_cast<const float2*>(c.vparams + unit * geo.vparams_unit());
-    uint32_t* dst = out_codes + (uint64_t)unit * vq * wpt;
-    float2* dpar = out_params ? reinterpret_cast<float2*>(out_params) + (uint64_t)unit * vq * ncg : nullptr;
-    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) words[i] = src[tb * n + i];
-    __syncthreads();
-    const uint32_t ntok = static_cast<uint32_t>(std::min<uint64_t>(kValueBlock, vq - tb * kValueBlock));
-    for (uint32_t o = threadIdx.x; o < ntok * wpt; o += blockDim.x) {
-      const uint32_t tt = o / wpt, j = o % wpt;
-      const uint32_t sh = code_shift(bits, tt % ppw);
-      uint32_t word = 0;
-      for (uint32_t i = 0; i < ppw; ++i) word |= ((words[(j * ppw + i) * vw + tt / ppw] >> sh) & mask) << (bits * i);
-      dst[tb * kValueBlock * wpt + o] = word;
+  const uint64_t b0 = (uint64_t)blockIdx.x * per;
+  const uint32_t nb = static_cast<uint32_t>(std::min<uint64_t>(per, nblk - b0));
+  // tokens of this workgroup's blocks (the last block of the stream may be partial)
+  const uint32_t ntok = static_cast<uint32_t>(std::min<uint64_t>((uint64_t)nb * kValueBlock, vq - b0 * kValueBlock));
+  for (uint32_t unit = blockIdx.y; unit < geo.units; unit += gridDim.y) {
+    const uint32_t* src = c.vcodes + unit * geo.vcodes_unit() + b0 * n;
+    const float2* prm = reinterpret_cast<const float2*>(c.vparams + unit * geo.vparams_unit()) + b0 * ncg * kValueBlock;
+    uint32_t* dst = out_codes + (uint64_t)unit * vq * wpt + b0 * kValueBlock * wpt;
+    for (uint32_t i = threadIdx.x; i < nb * n; i += blockDim.x) {
+      const uint32_t bb = i / n, r = i % n;
+      words[bb * np + r + r / (PPW * VW)] = src[i];
     }
-    if (dpar != nullptr)
-      for (uint32_t o = threadIdx.x; o < ntok * ncg; o += blockDim.x) {
-        const uint32_t tt = o / ncg, cg = o % ncg;
-        dpar[(tb * kValueBlock + tt) * ncg + cg] = prm[(tb * ncg + cg) * kValueBlock + tt];
-      }
     __syncthreads();
+    for (uint32_t o = threadIdx.x; o < ntok * wpt; o += blockDim.x) {
+      const uint32_t tk = o / wpt, j = o % wpt, bb = tk / kValueBlock, tt = tk % kValueBlock;
+      const uint32_t sh = code_shift(BITS, tt % PPW);
+      const uint32_t* cw = words + bb * np + (j * PPW) * VW + j + tt / PPW;
+      uint32_t word = 0;
+#pragma unroll
+      for (uint32_t i = 0; i < PPW; ++i) word |= ((cw[i * VW] >> sh) & MASK) << (BITS * i);
+      dst[o] = word;
+    }
+    if (out_params != nullptr) {
+      float2* dpar = reinterpret_cast<float2*>(out_params) + ((uint64_t)unit * vq + b0 * kValueBlock) * ncg;
+      for (uint32_t o = threadIdx.x; o < ntok * ncg; o += blockDim.x) {
+        const uint32_t tk = o / ncg, cg = o % ncg, bb = tk / kValueBlock, tt = tk % kValueBlock;
+        dpar[o] = prm[((uint64_t)bb * ncg + cg) * kValueBlock + tt];
+      }
+    }
+    __syncthreads();  // the staging buffer is refilled for the next unit
   }
 }
 
@@ -1305,11 +1329,24 @@ hipError_t launch_export_keys(const CacheView& c, uint64_t kq, uint32_t* codes, 
   const Geometry& g = c.geo;
   if (kq == 0) return hipSuccess;
   if (codes != nullptr) {
-    const uint64_t slices = (kq / g.G + kExportGroups - 1) / kExportGroups;
-    const size_t lds = (size_t)g.G * g.kwords_per_token() * sizeof(uint32_t);
-    k_export_keys<<<dim3(static_cast<unsigned>(std::min<uint64_t>(slices, 1u << 30)), std::min(g.units, 65535u)),
-                    kThreads, lds, stream>>>(c, kq, codes);
-    hipError_t e = hipGetLastError();
+    // staged words per group: kw rows of G + 4 tokens
+    const uint32_t np = g.kwords_per_token() * (g.G + 4);
+    const uint32_t per = std::max(1u, std::min(kExportGroups, kExportLdsWords / np));
+    const uint64_t slices = (kq / g.G + per - 1) / per;
+    const size_t lds = (size_t)per * np * sizeof(uint32_t);
+    const dim3 grid(static_cast<unsigned>(std::min<uint64_t>(slices, 1u << 30)), std::min(g.units, 65535u));
+    hipError_t e = hipSuccess;
+    if (lds > 65536) {
+      const void* f = g.bits == 2 ? reinterpret_cast<const void*>(&k_export_keys<2>)
+                      : g.bits == 4 ? reinterpret_cast<const void*>(&k_export_keys<4>)
+                                    : reinterpret_cast<const void*>(&k_export_keys<8>);
+      e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+      if (e != hipSuccess) return e;
+    }
+    if (g.bits == 2) k_export_keys<2><<<grid, kThreads, lds, stream>>>(c, kq, per, codes);
+    else if (g.bits == 4) k_export_keys<4><<<grid, kThreads, lds, stream>>>(c, kq, per, codes);
+    else k_export_keys<8><<<grid, kThreads, lds, stream>>>(c, kq, per, codes);
+    e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
   if (params != nullptr) {
@@ -1332,11 +1369,25 @@ hipError_t launch_export_values(const CacheView& c, uint64_t vq, uint32_t* codes
     codes = tmp;
   }
   const uint64_t nblk = (vq + kValueBlock - 1) / kValueBlock;
-  const uint64_t slices = (nblk + kExportBlocks - 1) / kExportBlocks;
-  const size_t lds = (size_t)g.D * g.vwords_per_channel() * sizeof(uint32_t);
-  k_export_values<<<dim3(static_cast<unsigned>(std::min<uint64_t>(slices, 1u << 30)), std::min(g.units, 65535u)),
-                     kThreads, lds, stream>>>(c, vq, codes, params);
-  hipError_t e = hipGetLastError();
+  // staged words per block, padded by one word per run of ppw channels; a block of the widest
+  // heads (D = 1024, 8-bit) stages 16640 words (65 KB)
+  const uint32_t np = g.D * g.vwords_per_channel() + g.D / g.ppw();
+  const uint32_t per = std::max(1u, std::min(kExportBlocks, kExportLdsWords / np));
+  const uint64_t slices = (nblk + per - 1) / per;
+  const size_t lds = (size_t)per * np * sizeof(uint32_t);
+  const dim3 grid(static_cast<unsigned>(std::min<uint64_t>(slices, 1u << 30)), std::min(g.units, 65535u));
+  hipError_t e = hipSuccess;
+  if (g.bits == 2) {
+    k_export_values<2><<<grid, kThreads, lds, stream>>>(c, vq, per, codes, params);
+  } else if (g.bits == 4) {
+    k_export_values<4><<<grid, kThreads, lds, stream>>>(c, vq, per, codes, params);
+  } else {
+    if (lds > 65536)
+      e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_export_values<8>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    if (e == hipSuccess) k_export_values<8><<<grid, kThreads, lds, stream>>>(c, vq, per, codes, params);
+  }
+  if (e == hipSuccess) e = hipGetLastError();
   if (tmp != nullptr) {
     hipError_t f = hipFreeAsync(tmp, stream);
     if (e == hipSuccess) e = f;
