@@ -73,6 +73,11 @@ CONFIGS = {
     "c4": (1, 8, 32, 128, 65536, 2, 32, 128,
            "config 4: one 65536-token 2-bit G=32 R=128 prefix (8 KV heads, head_dim 128) shared by "
            "64 RagSessions with 96-token fp32 suffixes, 32 query heads, batched sessions attention"),
+    # shapes outside the matrix-core path (k_attn_generic), timed on request only
+    "g_d64": (16, 8, 32, 64, 32768, 2, 32, 128, "generic path: batch 16, 32q/8kv heads, head_dim 64, 32768 tokens, 2-bit"),
+    "g_d256": (4, 8, 32, 256, 32768, 2, 32, 128, "generic path: batch 4, 32q/8kv heads, head_dim 256, 32768 tokens, 2-bit"),
+    "g_gqa16": (4, 4, 64, 128, 32768, 2, 32, 128, "generic path: batch 4, 64q/4kv heads (GQA 16), head_dim 128, 32768 tokens, 2-bit"),
+    "g_g64": (16, 8, 32, 128, 32768, 2, 64, 128, "generic path: batch 16, 32q/8kv heads, head_dim 128, 32768 tokens, 2-bit G=64"),
 }
 SECONDARY = ("c0", "c1", "c3_4", "c3_8", "c4")
 # batched-sessions workloads: name -> (sessions, suffix tokens per session)
@@ -80,7 +85,8 @@ SESSIONS = {"c4": (64, 96)}
 # streaming-decode workloads: name -> decode steps the workload allows after the prefill
 DECODE = {"c1": 512}
 # CPU-baseline time per workload (seconds of oracle work, beyond its prefill)
-CPU_SECONDS = {"c2": 12.0, "c0": 3.0, "c1": 5.0, "c3_4": 4.0, "c3_8": 4.0, "c4": 5.0}
+CPU_SECONDS = {"c2": 12.0, "c0": 3.0, "c1": 5.0, "c3_4": 4.0, "c3_8": 4.0, "c4": 5.0,
+               "g_d64": 3.0, "g_d256": 3.0, "g_gqa16": 3.0, "g_g64": 3.0}
 
 
 def log(*a):
@@ -537,7 +543,7 @@ def measure(name, args, torch, kivi, amd, stream, with_cpu):
     if dom_fam == "attn_shared":
         # The shared-prefix GEMM form is bound by the matrix cores: algorithmic flops of the
         # launch (q.k and p.v over every session row and prefix token, 4*D flops per
-        # row-token; the suffixes run in the per-session kernel) over its mean duration,
+        # row-token; the suffixes run in k_attn_suffix) over its mean duration,
         # against the dense f16 MFMA peak it runs on. Each product executes as three f16 MFMA
         # products (hi/lo operand splits), reported beside it.
         n_sess, _ = sessions_cfg
