@@ -63,6 +63,9 @@ struct AttnArgs {
   uint32_t win_begin, win_end;
   uint32_t nsplit_win;
   uint32_t nsplit_total;   // splits per unit in the workspace
+  // shapes outside the matrix-core path: k_attn_vpack takes 64-token blocks [0, chunk_end)
+  // (keys and values packed) in splits 0 .. nsplit_fast-1, the generic splits the rest
+  uint32_t vpack;
   float* ws;               // [units][nsplit_total][gq][D+2]
   // batched sessions (0 otherwise): session count and the strides between consecutive
   // sessions' queries, partials and outputs
@@ -260,6 +263,136 @@ __global__ void __launch_bounds__(kThreads) k_attn_generic(AttnArgs a) {
   extern __shared__ float lds[];
   const uint32_t unit = blockIdx.x / a.nsplit_gen;
   generic_split<BITS, DD, GG>(a, unit, blockIdx.x % a.nsplit_gen, lds);
+}
+
+// ------------------------------------------------------------------ packed blocks, other shapes
+// Shapes outside the matrix-core path with D % 64 == 0, D <= 256 and G 32 or a multiple of 64:
+// one wave per (unit, split) over 64-token blocks whose keys and values are all packed, with a
+// running maximum and rescaled sums across the blocks. The wave-uniform operands sit in LDS
+// and are read as broadcasts: the pass's queries ([channel][head]) and each block's key and
+// value (scale, zero). Keys: lane = token, a code becomes fma(code, scale, zero), then one fma
+// per head. Values: lane = channels c = lane + 64j, with the block's probabilities from LDS.
+// With G = 32 a block holds two key groups (lanes 0-31 and 32-63) and a 64-channel slot two
+// value groups. Heads go in passes of HP (the last pass's extra heads read the last head's
+// query and are dropped).
+template <int BITS, bool G32, int HP>
+__global__ void __launch_bounds__(64) k_attn_vpack(AttnArgs a) {
+  constexpr uint32_t PPW = 32 / BITS, MASK = (1u << BITS) - 1u, VW = 64 / PPW;
+  __shared__ float qs[256][HP];     // the pass's queries [channel][head]
+  __shared__ float2 kps[2][256];    // the block's key (scale, zero) [group][channel]
+  __shared__ float2 vps[8][64];     // the block's value (scale, zero) [channel group][token]
+  __shared__ float pl[64][HP];      // the block's probabilities [token][head]
+  const Geometry& g = a.c.geo;
+  // KW = D / PPW is a multiple of 4 (D % 64 == 0, PPW <= 16): a token row is whole uint4 words
+  const uint32_t D = g.D, G = g.G, gq = a.gq, ncg = D / G, KW = D / PPW, DC = D / 64;
+  const uint32_t lane = threadIdx.x;
+  const uint32_t unit = blockIdx.x / a.nsplit_fast, split = blockIdx.x % a.nsplit_fast;
+  const uint32_t nblk = a.chunk_end;
+  const uint32_t bps = (nblk + a.nsplit_fast - 1) / a.nsplit_fast;
+  const uint32_t b0 = std::min(nblk, split * bps), b1 = std::min(nblk, b0 + bps);
+  const uint32_t bb = unit / a.heads, kvh = unit % a.heads;
+  const float* qbase = a.query + ((uint64_t)bb * a.qh + kvh * gq) * D;
+  const uint32_t* kc = a.c.kcodes + unit * g.kcodes_unit();
+  const float2* kp = reinterpret_cast<const float2*>(a.c.kparams + unit * g.kparams_unit());
+  const uint32_t* vc = a.c.vcodes + unit * g.vcodes_unit();
+  const float2* vp = reinterpret_cast<const float2*>(a.c.vparams + unit * g.vparams_unit());
+  const uint32_t hk = G32 && lane >= 32 ? 1 : 0;  // the lane's key group within a block
+  for (uint32_t h0 = 0; h0 < gq; h0 += HP) {
+    __syncthreads();  // the previous pass is done with the queries
+    for (uint32_t d = lane; d < D; d += 64)
+#pragma unroll
+      for (int h = 0; h < HP; ++h) qs[d][h] = qbase[(uint64_t)std::min<uint32_t>(h0 + h, gq - 1) * D + d];
+    float m[HP], ls[HP], o[HP][4];
+#pragma unroll
+    for (int h = 0; h < HP; ++h) {
+      m[h] = -INFINITY;
+      ls[h] = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[h][j] = 0.f;
+    }
+    for (uint32_t blk = b0; blk < b1; ++blk) {
+      // the block's (scale, zero): key groups blk*64/G (+1 when G = 32), value groups of all
+      // channels for its 64 tokens
+      {
+        const float2* kpg = kp + (uint64_t)((uint64_t)blk * 64 / G) * D;
+        for (uint32_t i = lane; i < (G32 ? 2 : 1) * D; i += 64) kps[i / D][i % D] = kpg[i];
+        const float2* vpg = vp + (uint64_t)blk * ncg * 64;
+        for (uint32_t i = lane; i < ncg * 64; i += 64) vps[i / 64][i % 64] = vpg[i];
+      }
+      __syncthreads();
+      // logits, lane = token blk*64 + lane (base-2 units after the scale)
+      float acc[HP];
+#pragma unroll
+      for (int h = 0; h < HP; ++h) acc[h] = 0.f;
+      const uint4* kw = reinterpret_cast<const uint4*>(kc + ((uint64_t)blk * 64 + lane) * KW);
+      for (uint32_t w4 = 0; w4 < KW / 4; ++w4) {
+        const uint4 x = kw[w4];
+        const uint32_t words[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+        for (uint32_t i = 0; i < 4 * PPW; ++i) {
+          const uint32_t d = (w4 * 4 + i / PPW) * PPW + i % PPW;
+          const float2 sz = kps[hk][d];
+          const float r = fmaf(static_cast<float>((words[i / PPW] >> code_shift(BITS, i % PPW)) & MASK), sz.x, sz.y);
+#pragma unroll
+          for (int h = 0; h < HP; ++h) acc[h] = fmaf(r, qs[d][h], acc[h]);
+        }
+      }
+      // running maxima, rescaled sums, the block's probabilities into LDS
+#pragma unroll
+      for (int h = 0; h < HP; ++h) {
+        const float lg = acc[h] * a.scale2;
+        float bm = lg;
+#pragma unroll
+        for (int sft = 32; sft >= 1; sft >>= 1) bm = fmaxf(bm, __shfl_xor(bm, sft));
+        const float mnew = fmaxf(m[h], bm);
+        const float alpha = m[h] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m[h] - mnew);
+        const float pr = __builtin_amdgcn_exp2f(lg - mnew);
+        ls[h] = fmaf(ls[h], alpha, pr);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[h][j] *= alpha;
+        m[h] = mnew;
+        pl[lane][h] = pr;
+      }
+      __syncthreads();
+      // values, lane = channels lane + 64j
+#pragma unroll
+      for (uint32_t j = 0; j < 4; ++j) {
+        if (j >= DC) break;
+        const uint32_t c = lane + 64 * j;
+        uint32_t words[VW];
+        const uint32_t* cw = vc + ((uint64_t)blk * D + c) * VW;
+#pragma unroll
+        for (uint32_t q = 0; q < VW; q += 4) {
+          const uint4 x = *reinterpret_cast<const uint4*>(cw + q);
+          words[q] = x.x; words[q + 1] = x.y; words[q + 2] = x.z; words[q + 3] = x.w;
+        }
+        const float2* vg = vps[c / G];
+        for (uint32_t tt = 0; tt < 64; ++tt) {
+          const float2 sz = vg[tt];
+          const float r = fmaf(static_cast<float>((words[tt / PPW] >> code_shift(BITS, tt % PPW)) & MASK), sz.x, sz.y);
+#pragma unroll
+          for (int h = 0; h < HP; ++h) o[h][j] = fmaf(pl[tt][h], r, o[h][j]);
+        }
+      }
+      __syncthreads();  // the block's operands are rewritten by the next block
+    }
+    // partials of the pass's heads
+#pragma unroll
+    for (int h = 0; h < HP; ++h) {
+      float l = ls[h];
+#pragma unroll
+      for (int sft = 32; sft >= 1; sft >>= 1) l += __shfl_xor(l, sft);
+      if (h0 + h >= gq) continue;
+      float* part = a.ws + (((uint64_t)unit * a.nsplit_total + split) * gq + h0 + h) * (D + 2);
+#pragma unroll
+      for (uint32_t j = 0; j < 4; ++j)
+        if (j < DC) part[lane + 64 * j] = o[h][j];
+      if (lane == 0) {
+        part[D] = b1 > b0 ? m[h] : -INFINITY;
+        part[D + 1] = b1 > b0 ? l : 0.f;
+      }
+    }
+  }
 }
 
 // ------------------------------------------------------------------ MFMA splits
@@ -1906,6 +2039,14 @@ bool fast_eligible(const AttnProblem& p) {
          gq <= 8;
 }
 
+// Shapes k_attn_vpack takes (outside the matrix-core path): D a multiple of 64 up to 256, G 32
+// or a multiple of 64, bits 2/4/8.
+bool vpack_eligible(const AttnProblem& p) {
+  const Geometry& g = p.cache.geo;
+  return !fast_eligible(p) && g.D % 64 == 0 && g.D <= 256 && (g.G == 32 || g.G % 64 == 0) &&
+         (g.bits == 2 || g.bits == 4 || g.bits == 8);
+}
+
 // MFMA chunks: [0, floor(vq/64)) (keys and values packed; vq <= kq). Everything after
 // (value window, its band of packed keys, session suffix) goes to the generic kernel.
 AttnArgs make_args(const AttnProblem& p, float* ws) {
@@ -1948,6 +2089,27 @@ AttnArgs make_args(const AttnProblem& p, float* ws) {
   }
   a.nsplit_win = a.win_end - a.win_begin;  // one chunk per workgroup, a quarter per wave
   a.t_begin = fast ? a.total : 0;
+  a.vpack = 0;
+  if (!fast && vpack_eligible(p)) {
+    // packed 64-token blocks [0, floor(min(kq, vq)/64)) to k_attn_vpack, in splits of at least
+    // max(4, gq/2) blocks (partials stay small against the blocks) and ~2048 waves when the
+    // blocks allow; the generic splits take the rest
+    const uint32_t nblk = static_cast<uint32_t>(std::min(p.st.kq, p.st.vq) / 64);
+    if (nblk > 0) {
+      const uint32_t units = p.cache.geo.units;
+      const uint32_t minb = std::max(4u, a.gq / 2);
+      const uint32_t most = std::max(1u, nblk / minb);
+      a.vpack = 1;
+      a.chunk_end = nblk;
+      a.nsplit_fast = std::max(1u, std::min(most, (2048 + units - 1) / units));
+      a.t_begin = (uint64_t)nblk * 64;
+      // the rest is short (the fp32 residual and window, a suffix): shorter splits, down to 16
+      // tokens while the rest would fill fewer than ~1024 workgroups
+      a.S = std::max(32u, a.S / 4);
+      const uint64_t rest = a.total - a.t_begin;
+      while (a.S > 16 && (uint64_t)units * ((rest + a.S - 1) / a.S) < 1024) a.S >>= 1;
+    }
+  }
   a.nsplit_gen = static_cast<uint32_t>((a.total - a.t_begin + a.S - 1) / a.S);
   a.nsplit_total = a.nsplit_fast + a.nsplit_win + a.nsplit_gen;
   a.ws = ws;
@@ -1987,6 +2149,27 @@ hipError_t dispatch_generic(const AttnArgs& a, hipStream_t stream) {
   const size_t lds = ((size_t)a.gq * a.c.geo.D + (size_t)a.gq * a.S) * sizeof(float);
   k_attn_generic<0, 0, 0><<<a.units * a.nsplit_gen, kThreads, lds, stream>>>(a);
   return hipGetLastError();
+}
+
+template <int BITS, bool G32>
+hipError_t launch_vpack(const AttnArgs& a, hipStream_t stream) {
+  const unsigned grid = a.units * a.nsplit_fast;
+  switch (a.gq <= 1 ? 1 : a.gq <= 2 ? 2 : a.gq <= 4 ? 4 : 8) {
+    case 1: k_attn_vpack<BITS, G32, 1><<<grid, 64, 0, stream>>>(a); break;
+    case 2: k_attn_vpack<BITS, G32, 2><<<grid, 64, 0, stream>>>(a); break;
+    case 4: k_attn_vpack<BITS, G32, 4><<<grid, 64, 0, stream>>>(a); break;
+    default: k_attn_vpack<BITS, G32, 8><<<grid, 64, 0, stream>>>(a); break;
+  }
+  return hipGetLastError();
+}
+
+hipError_t dispatch_vpack(const AttnArgs& a, hipStream_t stream) {
+  const bool g32 = a.c.geo.G == 32;
+  switch (a.c.geo.bits) {
+    case 2: return g32 ? launch_vpack<2, true>(a, stream) : launch_vpack<2, false>(a, stream);
+    case 4: return g32 ? launch_vpack<4, true>(a, stream) : launch_vpack<4, false>(a, stream);
+    default: return g32 ? launch_vpack<8, true>(a, stream) : launch_vpack<8, false>(a, stream);
+  }
 }
 
 }  // namespace
@@ -2034,7 +2217,7 @@ hipError_t launch_fill_zero(float* out, size_t n, hipStream_t stream) {
 
 bool attention_fuses_decode(const AttnProblem& p) {
   const AttnArgs a = make_args(p, nullptr);
-  return a.total > 0 && a.nsplit_gen == 0 && (a.nsplit_fast > 0 || a.nsplit_win > 0);
+  return a.total > 0 && !a.vpack && a.nsplit_gen == 0 && (a.nsplit_fast > 0 || a.nsplit_win > 0);
 }
 
 size_t attention_workspace_floats(const AttnProblem& p) {
@@ -2056,7 +2239,20 @@ hipError_t launch_attention(const AttnProblem& p, float* workspace, hipStream_t 
   const double kp = kq > t0 ? (double)(kq - t0) : 0.0, vp = vq > t0 ? (double)(vq - t0) : 0.0;
   const double kd = (double)(p.seq - std::max(kq, t0)), vd = (double)(p.seq - std::max(vq, t0));
   const double tail_bytes = units * (kp * key_tok + vp * val_tok + (kd + vd + 2.0 * p.suffix_len) * row);
-  if (a.nsplit_fast > 0 || a.nsplit_win > 0) {
+  if (a.vpack) {
+    // packed blocks on k_attn_vpack, then the generic splits over the rest
+    const double pk = (double)a.chunk_end * 64;
+    {
+      TimedLaunch timed(KIVI_KERNEL_ATTN_PACKED, stream, units * pk * (key_tok + val_tok) + q_bytes);
+      hipError_t e = dispatch_vpack(a, stream);
+      if (e != hipSuccess) return e;
+    }
+    if (a.nsplit_gen > 0) {
+      TimedLaunch timed(KIVI_KERNEL_ATTN_TAIL, stream, tail_bytes + q_bytes);
+      hipError_t e = dispatch_generic(a, stream);
+      if (e != hipSuccess) return e;
+    }
+  } else if (a.nsplit_fast > 0 || a.nsplit_win > 0) {
     // one launch over every chunk: packed tokens at packed cost, the rest as fp32 rows
     const double kpt = (double)std::min<uint64_t>(kq, p.seq), vpt = (double)vq;
     const double fp32_rows = (double)(p.seq - kq) + (double)(p.seq - vq) + 2.0 * p.suffix_len;

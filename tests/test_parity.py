@@ -93,6 +93,34 @@ def test_streaming_cache_parity(amd, oracle, bits, group, residual, dim, schedul
     assert np.array_equal(va.view(np.uint32), vo.view(np.uint32))
 
 
+@pytest.mark.parametrize("dim,group,gqa,bits", [
+    (64, 32, 4, 2), (64, 64, 1, 4), (64, 32, 2, 8), (192, 64, 3, 2), (256, 32, 4, 4), (256, 128, 2, 8),
+    (128, 64, 4, 2), (128, 32, 16, 2), (128, 128, 12, 4), (96, 32, 4, 2)])
+def test_other_shapes_attention_parity(amd, oracle, dim, group, gqa, bits):
+    """Shapes outside the matrix-core path: the packed 64-token blocks go to the wave-per-split
+    kernel (head_dim a multiple of 64 up to 256, G = 32 or a multiple of 64, heads in passes
+    of up to 8, the extra heads of a last pass dropped) and the rest to the generic splits;
+    head_dim 96 stays on the generic splits alone. Many splits, against the oracle and f64
+    dense attention on the dequantized cache."""
+    batch, heads = 2, 2
+    seq = 2500 + 13 * bits
+    rng = np.random.default_rng(dim + group + gqa + bits)
+    k = rng.standard_normal(batch * heads * seq * dim).astype(np.float32)
+    k.reshape(batch, heads, seq, dim)[:, :, :, 2] *= np.float32(10.0)
+    v = rng.standard_normal(batch * heads * seq * dim).astype(np.float32)
+    cfg = KiviConfig(bits, group, 2 * group if group >= 64 else 128)
+    a = KiviCache(amd, cfg, batch, heads, dim)
+    o = KiviCache(oracle, cfg, batch, heads, dim)
+    a.append(k, v, seq)
+    o.append(k, v, seq)
+    q = rng.standard_normal(batch * heads * gqa * dim).astype(np.float32)
+    scale = np.float32(1 / np.sqrt(dim))
+    got = a.attention(q, heads * gqa, scale)
+    assert_close(got, o.attention(q, heads * gqa, scale))
+    kh, vh = a.dequantize()
+    assert max_abs(got, dense_attend(kh, vh, q, batch, heads, heads * gqa, seq, dim, scale)) < 1e-4
+
+
 @pytest.mark.parametrize("bits", [2, 4, 8])
 @pytest.mark.parametrize("gqa", [1, 4, 8])
 def test_attention_parity_long(amd, oracle, bits, gqa):
