@@ -66,6 +66,10 @@ struct AttnArgs {
   // shapes outside the matrix-core path: k_attn_vpack takes 64-token blocks [0, chunk_end)
   // (keys and values packed) in splits 0 .. nsplit_fast-1, the generic splits the rest
   uint32_t vpack;
+  // query heads in groups of up to 8 (GQA > 8 on the matrix-core path): one workgroup per
+  // (unit, head group, split), each writing its group's partial rows
+  uint32_t hgroups;
+  uint32_t gshift;         // log2(G) on the matrix-core path (G = 32, 64 or 128 there)
   float* ws;               // [units][nsplit_total][gq][D+2]
   // batched sessions (0 otherwise): session count and the strides between consecutive
   // sessions' queries, partials and outputs
@@ -520,8 +524,9 @@ __device__ __forceinline__ void load_words(const uint32_t* p, uint32_t* w) {
 }
 
 // One chunk's key data for the lane's token: its code words, and the (scale, zero) pairs of
-// its group (half lc) for channels 16*la + 4*li .. +3 (the quad's four lanes hold the block's
-// 16 channels between them; quad_bcast shares them).
+// its half's key group (tokens 32*lc .. +31 of the chunk; the same group for both halves when
+// G >= 64) for channels 16*la + 4*li .. +3 (the quad's four lanes hold the block's 16 channels
+// between them; quad_bcast shares them).
 template <int BITS>
 struct KeyWords {
   uint32_t w[128 * BITS / 32];
@@ -530,7 +535,8 @@ struct KeyParams {
   float4 sz[2];
 };
 // One chunk's value data: the code words of channels lane and 64+lane, and (scale, zero) of
-// tokens 8*la + 2*li, +1 for channel groups lc and lc+2 (the quad holds tokens 8*la .. +7).
+// tokens 8*la + 2*li, +1 for the channel groups of channels 32*lc and 64+32*lc (value_group;
+// the quad holds tokens 8*la .. +7).
 template <int BITS>
 struct ValueWords {
   uint32_t w[2][64 * BITS / 32];
@@ -558,8 +564,10 @@ __device__ __forceinline__ void load_key_words(const AttnArgs& a, uint32_t unit,
 }
 __device__ __forceinline__ void load_key_params(const AttnArgs& a, uint32_t unit, uint32_t ch,
                                                 uint32_t la, uint32_t lc, uint32_t li, KeyParams& kp) {
+  // the key group of the half's tokens 64*ch + 32*lc .. +31 (G a multiple of 32)
+  const uint32_t grp = (64 * ch + 32 * lc) >> a.gshift;
   const float4* pp = reinterpret_cast<const float4*>(
-      a.c.kparams + unit * a.c.geo.kparams_unit() + ((uint64_t)(2 * ch + lc) * 128 + 16 * la + 4 * li) * 2);
+      a.c.kparams + unit * a.c.geo.kparams_unit() + ((uint64_t)grp * 128 + 16 * la + 4 * li) * 2);
   kp.sz[0] = pp[0];
   kp.sz[1] = pp[1];
 }
@@ -572,12 +580,18 @@ __device__ __forceinline__ void load_value_words(const AttnArgs& a, uint32_t uni
     load_words<VW>(a.c.vcodes + unit * a.c.geo.vcodes_unit() + ((uint64_t)tb * 128 + lane + 64 * hv) * VW,
                    vw.w[hv]);
 }
+// channel group of channels 32*lc + 64*hv .. +31 (the lane's channels lane + 64*hv)
+__device__ __forceinline__ uint32_t value_group(const AttnArgs& a, uint32_t lc, uint32_t hv) {
+  return (32 * lc + 64 * hv) >> a.gshift;
+}
 __device__ __forceinline__ void load_value_params(const AttnArgs& a, uint32_t unit, uint32_t tb,
                                                   uint32_t la, uint32_t lc, uint32_t li, ValueParams& vp) {
+  const uint32_t ncg = 128 >> a.gshift;
 #pragma unroll
   for (int hv = 0; hv < 2; ++hv)
     vp.sz[hv] = *reinterpret_cast<const float4*>(
-        a.c.vparams + unit * a.c.geo.vparams_unit() + (((uint64_t)tb * 4 + lc + 2 * hv) * 64 + 8 * la + 2 * li) * 2);
+        a.c.vparams + unit * a.c.geo.vparams_unit() +
+        (((uint64_t)tb * ncg + value_group(a, lc, hv)) * 64 + 8 * la + 2 * li) * 2);
 }
 
 // Key-side A operands of one chunk: q * scale (already times 2^e) per (head, channel) of the
@@ -867,7 +881,7 @@ __device__ __forceinline__ void evict_groups(EvictRow& e, float levels, float& s
 // double-buffered).
 template <int BITS, int NRS, int CPW, bool MIXED>
 __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uint32_t split,
-                                           float* lds) {
+                                           uint32_t hg, float* lds) {
   constexpr int D = 128;
   constexpr int ROW = CPW * 64 + kRowPad;  // logits row stride (floats)
   constexpr int NH = 4 * NRS;              // padded heads per unit
@@ -920,7 +934,7 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
   float qmax = 0.f;
 #pragma unroll
   for (int rs = 0; rs < NRS; ++rs) {
-    const uint32_t h = rs * 4 + li;
+    const uint32_t h = hg * 8 + rs * 4 + li;  // query head within the unit (head group hg)
     const float* qp = a.query + ((uint64_t)b * a.qh + kvh * gq + min(h, gq - 1)) * D + 16 * la;
     const float s = h < gq ? a.scale2 : 0.f;
 #pragma unroll
@@ -1067,6 +1081,7 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
               vp.sz[hv].z = er.sc[hv];
               vp.sz[hv].w = er.mn[hv];
             }
+            // (G = 32 here: the decode is fused into the launch only for G = 32)
             *reinterpret_cast<float2*>(a.c.vparams + unit * a.c.geo.vparams_unit() +
                                        (((uint64_t)tb * 4 + lc + 2 * hv) * 64 + tt) * 2) =
                 make_float2(er.sc[hv], er.mn[hv]);
@@ -1139,8 +1154,10 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
     }
   }
   __syncthreads();
-  float* part = a.ws + ((uint64_t)unit * a.nsplit_total + split_base + split) * gq * (D + 2);
-  for (uint32_t idx = threadIdx.x; idx < gq * (D + 2); idx += blockDim.x) {
+  // the head group's rows hg*8 .. (the unit's heads gq; NH = 8 whenever hg > 0)
+  const uint32_t hrows = std::min<uint32_t>(NH, gq - hg * 8);
+  float* part = a.ws + (((uint64_t)unit * a.nsplit_total + split_base + split) * gq + hg * 8) * (D + 2);
+  for (uint32_t idx = threadIdx.x; idx < hrows * (D + 2); idx += blockDim.x) {
     const uint32_t h = idx / (D + 2), d = idx % (D + 2);
     float M = -INFINITY;
 #pragma unroll
@@ -1171,12 +1188,14 @@ template <int BITS, int NRS>
 __global__ void __launch_bounds__(kThreads, (NRS == 1 && BITS <= 4) ? 4 : (BITS == 8 && NRS == 2) ? 2 : 3)
     k_attn_mfma(AttnArgs a) {
   extern __shared__ float lds[];
-  const uint32_t nwin = a.units * a.nsplit_win;
+  // workgroups of (unit, head group) pairs: vu = unit * hgroups + hg
+  const uint32_t nwin = a.units * a.hgroups * a.nsplit_win;
   if (blockIdx.x < nwin) {
-    mfma_split<BITS, NRS, 1, true>(a, blockIdx.x / a.nsplit_win, blockIdx.x % a.nsplit_win, lds);
+    const uint32_t vu = blockIdx.x / a.nsplit_win;
+    mfma_split<BITS, NRS, 1, true>(a, vu / a.hgroups, blockIdx.x % a.nsplit_win, vu % a.hgroups, lds);
   } else {
-    const uint32_t blk = blockIdx.x - nwin;
-    mfma_split<BITS, NRS, fast_cpw(BITS, NRS), false>(a, blk / a.nsplit_fast, blk % a.nsplit_fast, lds);
+    const uint32_t blk = blockIdx.x - nwin, vu = blk / a.nsplit_fast;
+    mfma_split<BITS, NRS, fast_cpw(BITS, NRS), false>(a, vu / a.hgroups, blk % a.nsplit_fast, vu % a.hgroups, lds);
   }
 }
 
@@ -1211,7 +1230,7 @@ __global__ void __launch_bounds__(kThreads) k_attn_sessions(AttnArgs a, SessionT
   if (blockIdx.x < nwin) {
     const uint32_t s = blockIdx.x / per_sess, r = blockIdx.x % per_sess;
     const AttnArgs as = session_args(a, t, s);
-    mfma_split<BITS, NRS, 1, true>(as, r / a.nsplit_win, r % a.nsplit_win, lds);
+    mfma_split<BITS, NRS, 1, true>(as, r / a.nsplit_win, r % a.nsplit_win, 0, lds);
   } else {
     const uint32_t blk = blockIdx.x - nwin;
     const uint32_t unit = blk / a.nsplit_fast, split = blk % a.nsplit_fast;
@@ -1219,7 +1238,7 @@ __global__ void __launch_bounds__(kThreads) k_attn_sessions(AttnArgs a, SessionT
       AttnArgs as = a;
       as.query = a.query + s * a.q_sess_stride;
       as.ws = a.ws + s * a.ws_sess_stride;
-      mfma_split<BITS, NRS, kSessCpw, false>(as, unit, split, lds);
+      mfma_split<BITS, NRS, kSessCpw, false>(as, unit, split, 0, lds);
       __syncthreads();  // the next session reuses the LDS
     }
   }
@@ -2032,12 +2051,15 @@ uint32_t split_tokens(uint32_t gq) {
   return s;
 }
 
+// Shapes of the matrix-core path: D = 128, G = 32 or a multiple of 64 (a chunk's half-waves
+// then read one key group), any GQA up to 32 (above 8 in head groups of 8).
 bool fast_eligible(const AttnProblem& p) {
   const Geometry& g = p.cache.geo;
   const uint32_t gq = p.qh / p.heads;
-  return g.D == 128 && g.G == 32 && (g.bits == 2 || g.bits == 4 || g.bits == 8) && gq >= 1 &&
-         gq <= 8;
+  return g.D == 128 && (g.G == 32 || g.G % 64 == 0) && (g.bits == 2 || g.bits == 4 || g.bits == 8) &&
+         gq >= 1 && gq <= 32;
 }
+uint32_t head_groups(uint32_t gq) { return gq <= 8 ? 1u : (gq + 7) / 8; }
 
 // Shapes k_attn_vpack takes (outside the matrix-core path): D a multiple of 64 up to 256, G 32
 // or a multiple of 64, bits 2/4/8.
@@ -2078,10 +2100,12 @@ AttnArgs make_args(const AttnProblem& p, float* ws) {
   a.chunk_end = fast ? static_cast<uint32_t>(p.st.vq / 64) : 0;
   a.win_begin = a.chunk_end;
   a.win_end = fast ? static_cast<uint32_t>((a.total + 63) / 64) : 0;
+  a.hgroups = fast ? head_groups(a.gq) : 1u;
+  a.gshift = fast ? static_cast<uint32_t>(__builtin_ctz(p.cache.geo.G)) : 5u;
   // packed splits per unit: at most kFastCpw chunks per wave, at least one, and at least
-  // kFastGroups workgroups when the chunks allow
+  // kFastGroups workgroups (over units and head groups) when the chunks allow
   {
-    const uint32_t units = p.cache.geo.units;
+    const uint32_t units = p.cache.geo.units * a.hgroups;
     const uint32_t cpw = static_cast<uint32_t>(fast_cpw(static_cast<int>(p.cache.geo.bits), a.gq <= 4 ? 1 : 2));
     const uint32_t fewest = (a.chunk_end + 4 * cpw - 1) / (4 * cpw);
     const uint32_t most = (a.chunk_end + 3) / 4;
@@ -2128,7 +2152,7 @@ hipError_t launch_fast(const AttnArgs& a, double bytes, hipStream_t stream) {
   const size_t combine = (size_t)4 * NH * (128 + 2);
   const size_t lds = std::max(logits, combine) * sizeof(float);
   TimedLaunch timed(KIVI_KERNEL_ATTN_PACKED, stream, bytes);
-  k_attn_mfma<BITS, NRS><<<a.units * (a.nsplit_win + a.nsplit_fast), kThreads, lds, stream>>>(a);
+  k_attn_mfma<BITS, NRS><<<a.units * a.hgroups * (a.nsplit_win + a.nsplit_fast), kThreads, lds, stream>>>(a);
   return hipGetLastError();
 }
 
@@ -2215,9 +2239,12 @@ hipError_t launch_fill_zero(float* out, size_t n, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// The decode fused into the attention launch quantizes the evicted window token with the
+// 32-channel value groups of one half-wave, once per chunk workgroup: G = 32, one head group.
 bool attention_fuses_decode(const AttnProblem& p) {
   const AttnArgs a = make_args(p, nullptr);
-  return a.total > 0 && !a.vpack && a.nsplit_gen == 0 && (a.nsplit_fast > 0 || a.nsplit_win > 0);
+  return a.total > 0 && !a.vpack && a.nsplit_gen == 0 && (a.nsplit_fast > 0 || a.nsplit_win > 0) &&
+         p.cache.geo.G == 32 && a.hgroups == 1;
 }
 
 size_t attention_workspace_floats(const AttnProblem& p) {
@@ -2304,7 +2331,8 @@ bool sessions_supported(const SessionsProblem& sp) {
   p.st = sp.st;
   p.qh = sp.qh;
   p.heads = sp.heads;
-  return sp.n > 0 && fast_eligible(p) && sp.st.kq > 0;
+  // the batched-sessions kernels take G = 32 and GQA <= 8
+  return sp.n > 0 && fast_eligible(p) && sp.st.kq > 0 && sp.cache.geo.G == 32 && sp.qh / sp.heads <= 8;
 }
 
 uint64_t longest_suffix(const SessionsProblem& sp, uint32_t first, uint32_t count) {
