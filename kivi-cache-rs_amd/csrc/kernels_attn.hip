@@ -523,26 +523,40 @@ __device__ __forceinline__ void load_words(const uint32_t* p, uint32_t* w) {
   }
 }
 
+// Channel geometry of the matrix-core path for head_dim D (64, 128 or 256): keys in sets of
+// 128 channels (KS of them), each set's channel blocks of 16 (KB per set: 4 for D = 64, else
+// 8) held by blocks 0..KB-1 of each half-wave for the broadcast; values D/64 channels per lane
+// (channels lane + 64*hv).
+template <int D>
+struct Chan {
+  static constexpr int KS = D > 128 ? D / 128 : 1;
+  static constexpr int KB = D >= 128 ? 8 : D / 16;
+  static constexpr int HV = D / 64;
+};
+
 // One chunk's key data for the lane's token: its code words, and the (scale, zero) pairs of
 // its half's key group (tokens 32*lc .. +31 of the chunk; the same group for both halves when
-// G >= 64) for channels 16*la + 4*li .. +3 (the quad's four lanes hold the block's 16 channels
-// between them; quad_bcast shares them).
-template <int BITS>
+// G >= 64) for channels 128*s + 16*la + 4*li .. +3 of each set s (the quad's four lanes hold
+// the block's 16 channels between them; quad_bcast shares them; for D = 64 the blocks la >= 4
+// repeat blocks la - 4, whose operands are never broadcast).
+template <int BITS, int D>
 struct KeyWords {
-  uint32_t w[128 * BITS / 32];
+  uint32_t w[D * BITS / 32];
 };
+template <int D>
 struct KeyParams {
-  float4 sz[2];
+  float4 sz[Chan<D>::KS][2];
 };
-// One chunk's value data: the code words of channels lane and 64+lane, and (scale, zero) of
-// tokens 8*la + 2*li, +1 for the channel groups of channels 32*lc and 64+32*lc (value_group;
-// the quad holds tokens 8*la .. +7).
-template <int BITS>
+// One chunk's value data: the code words of channels lane + 64*hv, and (scale, zero) of
+// tokens 8*la + 2*li, +1 for the channel group of channels 32*lc + 64*hv (value_group; the
+// quad holds tokens 8*la .. +7).
+template <int BITS, int D>
 struct ValueWords {
-  uint32_t w[2][64 * BITS / 32];
+  uint32_t w[Chan<D>::HV][64 * BITS / 32];
 };
+template <int D>
 struct ValueParams {
-  float4 sz[2];
+  float4 sz[Chan<D>::HV];
 };
 
 // v as held by lane q of each quad (DPP quad_perm broadcast; every lane is active here).
@@ -556,80 +570,90 @@ __device__ __forceinline__ float quad_bcast(float v, int q) {
   }
 }
 
-template <int BITS>
+template <int BITS, int D>
 __device__ __forceinline__ void load_key_words(const AttnArgs& a, uint32_t unit, uint32_t ch,
-                                               uint32_t lane, KeyWords<BITS>& kw) {
-  constexpr int KW = 128 * BITS / 32;
+                                               uint32_t lane, KeyWords<BITS, D>& kw) {
+  constexpr int KW = D * BITS / 32;
   load_words<KW>(a.c.kcodes + unit * a.c.geo.kcodes_unit() + ((uint64_t)ch * 64 + lane) * KW, kw.w);
 }
+template <int D>
 __device__ __forceinline__ void load_key_params(const AttnArgs& a, uint32_t unit, uint32_t ch,
-                                                uint32_t la, uint32_t lc, uint32_t li, KeyParams& kp) {
+                                                uint32_t la, uint32_t lc, uint32_t li, KeyParams<D>& kp) {
   // the key group of the half's tokens 64*ch + 32*lc .. +31 (G a multiple of 32)
   const uint32_t grp = (64 * ch + 32 * lc) >> a.gshift;
-  const float4* pp = reinterpret_cast<const float4*>(
-      a.c.kparams + unit * a.c.geo.kparams_unit() + ((uint64_t)grp * 128 + 16 * la + 4 * li) * 2);
-  kp.sz[0] = pp[0];
-  kp.sz[1] = pp[1];
+  const uint32_t blk = la % Chan<D>::KB;
+#pragma unroll
+  for (int ks = 0; ks < Chan<D>::KS; ++ks) {
+    const float4* pp = reinterpret_cast<const float4*>(
+        a.c.kparams + unit * a.c.geo.kparams_unit() + ((uint64_t)grp * D + 128 * ks + 16 * blk + 4 * li) * 2);
+    kp.sz[ks][0] = pp[0];
+    kp.sz[ks][1] = pp[1];
+  }
 }
-template <int BITS>
+template <int BITS, int D>
 __device__ __forceinline__ void load_value_words(const AttnArgs& a, uint32_t unit, uint32_t tb,
-                                                 uint32_t lane, ValueWords<BITS>& vw) {
+                                                 uint32_t lane, ValueWords<BITS, D>& vw) {
   constexpr int VW = 64 * BITS / 32;
 #pragma unroll
-  for (int hv = 0; hv < 2; ++hv)
-    load_words<VW>(a.c.vcodes + unit * a.c.geo.vcodes_unit() + ((uint64_t)tb * 128 + lane + 64 * hv) * VW,
+  for (int hv = 0; hv < Chan<D>::HV; ++hv)
+    load_words<VW>(a.c.vcodes + unit * a.c.geo.vcodes_unit() + ((uint64_t)tb * D + lane + 64 * hv) * VW,
                    vw.w[hv]);
 }
 // channel group of channels 32*lc + 64*hv .. +31 (the lane's channels lane + 64*hv)
 __device__ __forceinline__ uint32_t value_group(const AttnArgs& a, uint32_t lc, uint32_t hv) {
   return (32 * lc + 64 * hv) >> a.gshift;
 }
+template <int D>
 __device__ __forceinline__ void load_value_params(const AttnArgs& a, uint32_t unit, uint32_t tb,
-                                                  uint32_t la, uint32_t lc, uint32_t li, ValueParams& vp) {
-  const uint32_t ncg = 128 >> a.gshift;
+                                                  uint32_t la, uint32_t lc, uint32_t li, ValueParams<D>& vp) {
+  const uint32_t ncg = D >> a.gshift;
 #pragma unroll
-  for (int hv = 0; hv < 2; ++hv)
+  for (int hv = 0; hv < Chan<D>::HV; ++hv)
     vp.sz[hv] = *reinterpret_cast<const float4*>(
         a.c.vparams + unit * a.c.geo.vparams_unit() +
         (((uint64_t)tb * ncg + value_group(a, lc, hv)) * 64 + 8 * la + 2 * li) * 2);
 }
 
 // Key-side A operands of one chunk: q * scale (already times 2^e) per (head, channel) of the
-// lane's group, split hi/lo, for K-groups of channels 16*la + 4k .. +3; bias[h] = sum_d q*zero
-// summed over the 8 blocks of the half, times 2^kExp (it enters through an f32 MFMA).
-template <int NRS>
+// lane's group, split hi/lo, for K-groups of channels 128*s + 16*la + 4k .. +3; bias[h] =
+// sum_d q*zero summed over the blocks of the half (the repeated blocks of D = 64 add 0), times
+// 2^kExp (it enters through an f32 MFMA).
+template <int NRS, int D>
 struct KeyA {
-  h4 hi[NRS][4], lo[NRS][4];
+  h4 hi[NRS][Chan<D>::KS][4], lo[NRS][Chan<D>::KS][4];
   float bias[NRS];
 };
 
-template <int BITS, int NRS>
-__device__ __forceinline__ void key_operands(const KeyParams& kp, const float (&qv)[NRS][16],
-                                             KeyA<NRS>& A) {
+template <int BITS, int NRS, int D>
+__device__ __forceinline__ void key_operands(const KeyParams<D>& kp, const float (&qv)[NRS][Chan<D>::KS][16],
+                                             bool live_block, KeyA<NRS, D>& A) {
   constexpr float kUnit = CodeUnit<BITS>::kExp == 0 ? 1.0f : CodeUnit<BITS>::kExp == -1 ? 0.5f : 0.001953125f;
 #pragma unroll
   for (int rs = 0; rs < NRS; ++rs) {
-    float p[16];
     float bias = 0.f;
 #pragma unroll
-    for (int c = 0; c < 16; ++c) {
-      const float4 sz = kp.sz[(c % 4) / 2];  // channel c lives in quad lane c / 4
-      const float sc = quad_bcast(c % 2 ? sz.z : sz.x, c / 4);
-      const float zc = quad_bcast(c % 2 ? sz.w : sz.y, c / 4);
-      p[c] = qv[rs][c] * sc;
-      bias = fmaf(qv[rs][c], zc, bias);
-    }
+    for (int ks = 0; ks < Chan<D>::KS; ++ks) {
+      float p[16];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) split4(p + 4 * k, A.hi[rs][k], A.lo[rs][k]);
-    A.bias[rs] = sum_over_blocks(bias) * kUnit;
+      for (int c = 0; c < 16; ++c) {
+        const float4 sz = kp.sz[ks][(c % 4) / 2];  // channel c lives in quad lane c / 4
+        const float sc = quad_bcast(c % 2 ? sz.z : sz.x, c / 4);
+        const float zc = quad_bcast(c % 2 ? sz.w : sz.y, c / 4);
+        p[c] = qv[rs][ks][c] * sc;
+        bias = fmaf(qv[rs][ks][c], zc, bias);
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) split4(p + 4 * k, A.hi[rs][ks][k], A.lo[rs][ks][k]);
+    }
+    A.bias[rs] = sum_over_blocks(live_block ? bias : 0.f) * kUnit;
   }
 }
 
 // Logits of one chunk for the lane's token (lane = token within the chunk), scaled by
-// 2^(e + kExp). Block a2's lanes hold A for channels 16*a2 .. +15, so ABID = a2 broadcasts it
-// to the 8 token blocks of each half; B = the lane token's codes (exact).
-template <int BITS, int NRS>
-__device__ __forceinline__ void key_mfma(const KeyWords<BITS>& kw, const KeyA<NRS>& A,
+// 2^(e + kExp). Block a2's lanes hold A for channels 128*s + 16*a2 .. +15, so ABID = a2
+// broadcasts it to the 8 token blocks of each half; B = the lane token's codes (exact).
+template <int BITS, int NRS, int D>
+__device__ __forceinline__ void key_mfma(const KeyWords<BITS, D>& kw, const KeyA<NRS, D>& A,
                                          float (&lg)[NRS][4]) {
   constexpr int PPW = 32 / BITS;
   v4f acc[NRS][2];
@@ -639,15 +663,18 @@ __device__ __forceinline__ void key_mfma(const KeyWords<BITS>& kw, const KeyA<NR
     acc[rs][1] = v4f{0.f, 0.f, 0.f, 0.f};
   }
 #pragma unroll
-  for (int a2 = 0; a2 < 8; ++a2) {
+  for (int ks = 0; ks < Chan<D>::KS; ++ks) {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int c0 = 16 * a2 + 4 * k;  // first channel of the K-group
-      const h4 b = codes4<BITS>(kw.w[c0 / PPW], (c0 % PPW) / 4);
+    for (int a2 = 0; a2 < Chan<D>::KB; ++a2) {
 #pragma unroll
-      for (int rs = 0; rs < NRS; ++rs) {
-        acc[rs][0] = mfma16(A.hi[rs][k], b, acc[rs][0], a2);
-        acc[rs][1] = mfma16(A.lo[rs][k], b, acc[rs][1], a2);
+      for (int k = 0; k < 4; ++k) {
+        const int c0 = 128 * ks + 16 * a2 + 4 * k;  // first channel of the K-group
+        const h4 b = codes4<BITS>(kw.w[c0 / PPW], (c0 % PPW) / 4);
+#pragma unroll
+        for (int rs = 0; rs < NRS; ++rs) {
+          acc[rs][0] = mfma16(A.hi[rs][ks][k], b, acc[rs][0], a2);
+          acc[rs][1] = mfma16(A.lo[rs][ks][k], b, acc[rs][1], a2);
+        }
       }
     }
   }
@@ -660,22 +687,22 @@ __device__ __forceinline__ void key_mfma(const KeyWords<BITS>& kw, const KeyA<NR
 }
 
 // Value-side A operands of one chunk: w * scale * 2^e per (head, token) of the lane's tokens
-// 8*la .. +7 and channel group (lc + 2*hv), split hi/lo into K-groups of 4 tokens. The zero
-// term sum_t w*zero accumulates into zacc (f32 VALU, unscaled).
-template <int NRS>
+// 8*la .. +7 and the channel group of channels 32*lc + 64*hv, split hi/lo into K-groups of 4
+// tokens. The zero term sum_t w*zero accumulates into zacc (f32 VALU, unscaled).
+template <int NRS, int D>
 struct ValueA {
-  h4 hi[NRS][2][2], lo[NRS][2][2];  // [rs][hv][tokens 8*la + 4j ..]
+  h4 hi[NRS][Chan<D>::HV][2], lo[NRS][Chan<D>::HV][2];  // [rs][hv][tokens 8*la + 4j ..]
 };
 
 // The weights w arrive times 2^e already (the exponent offset of the softmax), so zacc and
 // the caller's weight sum are in those units too.
-template <int NRS>
-__device__ __forceinline__ void value_operands(const ValueParams& vp, const float (&w)[NRS][8],
-                                               ValueA<NRS>& A, float (&zacc)[NRS][2]) {
+template <int NRS, int D>
+__device__ __forceinline__ void value_operands(const ValueParams<D>& vp, const float (&w)[NRS][8],
+                                               ValueA<NRS, D>& A, float (&zacc)[NRS][Chan<D>::HV]) {
 #pragma unroll
   for (int rs = 0; rs < NRS; ++rs) {
 #pragma unroll
-    for (int hv = 0; hv < 2; ++hv) {
+    for (int hv = 0; hv < Chan<D>::HV; ++hv) {
       float p[8];
 #pragma unroll
       for (int r = 0; r < 8; ++r) {
@@ -691,11 +718,11 @@ __device__ __forceinline__ void value_operands(const ValueParams& vp, const floa
   }
 }
 
-// Value mix of one chunk into vacc (lane = channels lane and 64+lane, scaled by 2^(e+kExp)).
+// Value mix of one chunk into vacc (lane = channels lane + 64*hv, scaled by 2^(e+kExp)).
 // K-group (word q, k) covers tokens q*PPW + 4k .. +3, whose A lives in block t0/8.
-template <int BITS, int NRS>
-__device__ __forceinline__ void value_mfma(const ValueWords<BITS>& vw, const ValueA<NRS>& A,
-                                           v4f (&vacc)[NRS][2]) {
+template <int BITS, int NRS, int D>
+__device__ __forceinline__ void value_mfma(const ValueWords<BITS, D>& vw, const ValueA<NRS, D>& A,
+                                           v4f (&vacc)[NRS][Chan<D>::HV]) {
   constexpr int VW = 64 * BITS / 32, PPW = 32 / BITS;
 #pragma unroll
   for (int q = 0; q < VW; ++q) {
@@ -703,14 +730,17 @@ __device__ __forceinline__ void value_mfma(const ValueWords<BITS>& vw, const Val
     for (int k = 0; k < PPW / 4; ++k) {
       const int t0 = q * PPW + 4 * k;
       const int a2 = t0 / 8, j = (t0 / 4) % 2;
-      const h4 b0 = codes4<BITS>(vw.w[0][q], k);
-      const h4 b1 = codes4<BITS>(vw.w[1][q], k);
+      h4 b[Chan<D>::HV];
+#pragma unroll
+      for (int hv = 0; hv < Chan<D>::HV; ++hv) b[hv] = codes4<BITS>(vw.w[hv][q], k);
+      // the hi products of every channel set, then the lo ones: consecutive MFMAs use
+      // different accumulators where D allows
 #pragma unroll
       for (int rs = 0; rs < NRS; ++rs) {
-        vacc[rs][0] = mfma16(A.hi[rs][0][j], b0, vacc[rs][0], a2);
-        vacc[rs][1] = mfma16(A.hi[rs][1][j], b1, vacc[rs][1], a2);
-        vacc[rs][0] = mfma16(A.lo[rs][0][j], b0, vacc[rs][0], a2);
-        vacc[rs][1] = mfma16(A.lo[rs][1][j], b1, vacc[rs][1], a2);
+#pragma unroll
+        for (int hv = 0; hv < Chan<D>::HV; ++hv) vacc[rs][hv] = mfma16(A.hi[rs][hv][j], b[hv], vacc[rs][hv], a2);
+#pragma unroll
+        for (int hv = 0; hv < Chan<D>::HV; ++hv) vacc[rs][hv] = mfma16(A.lo[rs][hv][j], b[hv], vacc[rs][hv], a2);
       }
     }
   }
@@ -758,7 +788,7 @@ __device__ __forceinline__ void load_key_rows(const AttnArgs& a, uint32_t unit, 
 // and the four channel groups' sums meet across lanes 16 and 32 apart.
 template <int NRS>
 __device__ __forceinline__ void key_fp32(const AttnArgs& a, uint64_t t0, uint32_t quarter, uint32_t lane,
-                                         const float (&qv)[NRS][16], const KeyRows& kr,
+                                         const float (&qv)[NRS][1][16], const KeyRows& kr,
                                          float unit_scale, float (&lg)[NRS][4]) {
   const uint64_t t = t0 + 16 * quarter + lane % 16;
   const float m = t >= a.st.kq && t < a.total ? unit_scale : 0.f;  // mask times 2^kExp
@@ -771,7 +801,7 @@ __device__ __forceinline__ void key_fp32(const AttnArgs& a, uint64_t t0, uint32_
 #pragma unroll
     for (int r = 0; r < 32; ++r) {
       const float x = (r % 4 == 0 ? kr.x[r / 4].x : r % 4 == 1 ? kr.x[r / 4].y : r % 4 == 2 ? kr.x[r / 4].z : kr.x[r / 4].w) * m;
-      const float q = __shfl(qv[rs][r % 16], r < 16 ? src0 : src1);
+      const float q = __shfl(qv[rs][0][r % 16], r < 16 ? src0 : src1);
       acc = __builtin_amdgcn_mfma_f32_4x4x1f32(q, x, acc, 0, 0, 0);
     }
 #pragma unroll
@@ -879,10 +909,11 @@ __device__ __forceinline__ void evict_groups(EvictRow& e, float levels, float& s
 // operands are prepared from the (scale, zero) registers first, then the next chunk's data
 // is requested into the same registers while this chunk's MFMAs run (code words are
 // double-buffered).
-template <int BITS, int NRS, int CPW, bool MIXED>
+template <int BITS, int NRS, int CPW, bool MIXED, int D>
 __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uint32_t split,
                                            uint32_t hg, float* lds) {
-  constexpr int D = 128;
+  static_assert(!MIXED || D == 128, "window / suffix chunks are taken at head_dim 128 only");
+  constexpr int KS = Chan<D>::KS, KB = Chan<D>::KB, HV = Chan<D>::HV;
   constexpr int ROW = CPW * 64 + kRowPad;  // logits row stride (floats)
   constexpr int NH = 4 * NRS;              // padded heads per unit
   const uint32_t b = unit / a.heads, kvh = unit % a.heads;
@@ -913,40 +944,44 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
 
   // The first chunk's key data are requested before anything else, so their latency
   // overlaps the query loads and the range set-up.
-  KeyParams kp;
-  KeyWords<BITS> kw0, kw1;
+  KeyParams<D> kp;
+  KeyWords<BITS, D> kw0, kw1;
   if (nch > 0) {
     const int32_t k0 = std::min(chunk_of(0), lastk);
-    load_key_params(a, unit, k0, la, lc, li, kp);
-    load_key_words<BITS>(a, unit, k0, lane, kw0);
+    load_key_params<D>(a, unit, k0, la, lc, li, kp);
+    load_key_words<BITS, D>(a, unit, k0, lane, kw0);
   }
 
   // a decode token appended by this launch evicts token vq-1 from the window: its row
   EvictRow er{};
-  if (a.pend_evict) {
+  if (D == 128 && a.pend_evict) {
     const float* row = a.c.vring + ((uint64_t)unit * a.c.geo.R + a.pend_vslot) * D;
     er.x[0] = row[lane];
     er.x[1] = row[lane + 64];
   }
 
-  // q in base-2 logit units for the lane's head, channels 16*la .. +15 (0 for padded heads).
-  float qv[NRS][16];
+  // q in base-2 logit units for the lane's head, channels 128*s + 16*la .. +15 of each set s
+  // (0 for padded heads; D = 64 repeats blocks la - 4 in blocks la >= 4).
+  float qv[NRS][KS][16];
   float qmax = 0.f;
 #pragma unroll
   for (int rs = 0; rs < NRS; ++rs) {
-    const uint32_t h = hg * 8 + rs * 4 + li;  // query head within the unit (head group hg)
-    const float* qp = a.query + ((uint64_t)b * a.qh + kvh * gq + min(h, gq - 1)) * D + 16 * la;
+    const uint32_t h = hg * NH + rs * 4 + li;  // query head within the unit (head group hg)
     const float s = h < gq ? a.scale2 : 0.f;
 #pragma unroll
-    for (int r = 0; r < 16; r += 4) {
-      const float4 v = *reinterpret_cast<const float4*>(qp + r);
-      qv[rs][r] = v.x * s;
-      qv[rs][r + 1] = v.y * s;
-      qv[rs][r + 2] = v.z * s;
-      qv[rs][r + 3] = v.w * s;
-    }
+    for (int ks = 0; ks < KS; ++ks) {
+      const float* qp = a.query + ((uint64_t)b * a.qh + kvh * gq + min(h, gq - 1)) * D + 128 * ks + 16 * (la % KB);
 #pragma unroll
-    for (int r = 0; r < 16; ++r) qmax = fmaxf(qmax, fabsf(qv[rs][r]));
+      for (int r = 0; r < 16; r += 4) {
+        const float4 v = *reinterpret_cast<const float4*>(qp + r);
+        qv[rs][ks][r] = v.x * s;
+        qv[rs][ks][r + 1] = v.y * s;
+        qv[rs][ks][r + 2] = v.z * s;
+        qv[rs][ks][r + 3] = v.w * s;
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) qmax = fmaxf(qmax, fabsf(qv[rs][ks][r]));
+    }
   }
   // Power-of-two operand ranges: every key A operand |q * scale| * 2^ek and every value A
   // operand |w * scale| * 2^ev (w <= 1) stays below 2^15, from the unit's largest scales.
@@ -955,7 +990,7 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
   float vmax = __uint_as_float(a.c.smax[4 * unit + 1]);
   constexpr float kLevels = static_cast<float>((1 << BITS) - 1);
   float ev_scale = 0.f, ev_amax = 0.f;  // the evicted row's largest scale and |x|
-  if (a.pend_evict) {
+  if (D == 128 && a.pend_evict) {
     evict_groups(er, kLevels, ev_scale, ev_amax);
     vmax = fmaxf(vmax, ev_scale);  // the maximum its quantization raises (as the append would)
   }
@@ -967,7 +1002,9 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
 #pragma unroll
   for (int rs = 0; rs < NRS; ++rs)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) qv[rs][r] *= kfac;
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) qv[rs][ks][r] *= kfac;
 
   // ---------------- phase 1: logits of every owned chunk into LDS (scaled by 2^(ek+kExp))
   // A chunk's keys are packed for t < kq and fp32 after; packed arrays hold zero codes and
@@ -980,27 +1017,29 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
 #pragma unroll
     for (int i = 0; i < 4; ++i) mx[rs][i] = -INFINITY;
   {
-    KeyA<NRS> A;
-    auto step = [&](int k, const KeyWords<BITS>& cur, KeyWords<BITS>& next) {
+    KeyA<NRS, D> A;
+    auto step = [&](int k, const KeyWords<BITS, D>& cur, KeyWords<BITS, D>& next) {
       const uint64_t t0 = (uint64_t)chunk_of(k) * 64;
       const bool packed = !MIXED || t0 < kq;
-      if (packed) key_operands<BITS, NRS>(kp, qv, A);
+      if (packed) key_operands<BITS, NRS, D>(kp, qv, la < KB, A);
       // unconditional (clamped to packed chunks; the last step re-reads an L2-resident chunk)
       if constexpr (CPW > 1) {
         const int32_t kn = std::min(chunk_of(std::min(k + 1, nch - 1)), lastk);
-        load_key_params(a, unit, kn, la, lc, li, kp);
-        load_key_words<BITS>(a, unit, kn, lane, next);
+        load_key_params<D>(a, unit, kn, la, lc, li, kp);
+        load_key_words<BITS, D>(a, unit, kn, lane, next);
       }
       float lg[NRS][4];
 #pragma unroll
       for (int rs = 0; rs < NRS; ++rs)
 #pragma unroll
         for (int i = 0; i < 4; ++i) lg[rs][i] = 0.f;
-      if (packed) key_mfma<BITS, NRS>(cur, A, lg);
-      if (MIXED && t0 + 64 > kq && t0 < total) {
-        KeyRows kr;  // one round of loads: the quarter's rows, four lanes per row
-        load_key_rows(a, unit, t0, quarter, lane, kr);
-        key_fp32<NRS>(a, t0, quarter, lane, qv, kr, kUnit, lg);
+      if (packed) key_mfma<BITS, NRS, D>(cur, A, lg);
+      if constexpr (MIXED) {
+        if (t0 + 64 > kq && t0 < total) {
+          KeyRows kr;  // one round of loads: the quarter's rows, four lanes per row
+          load_key_rows(a, unit, t0, quarter, lane, kr);
+          key_fp32<NRS>(a, t0, quarter, lane, qv, kr, kUnit, lg);
+        }
       }
       const bool live = !MIXED || (t0 + lane < total && lane / 16 == quarter);
 #pragma unroll
@@ -1038,23 +1077,26 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
   const float vinv = ldexpf(1.f, -ev);
 
   // ---------------- phase 2: value mix
-  v4f vacc[NRS][2];
-  float zacc[NRS][2];
+  v4f vacc[NRS][HV];
+  float zacc[NRS][HV];
   float lsum[NRS];
 #pragma unroll
   for (int rs = 0; rs < NRS; ++rs) {
-    vacc[rs][0] = v4f{0.f, 0.f, 0.f, 0.f};
-    vacc[rs][1] = v4f{0.f, 0.f, 0.f, 0.f};
-    zacc[rs][0] = zacc[rs][1] = 0.f;
+#pragma unroll
+    for (int hv = 0; hv < HV; ++hv) {
+      vacc[rs][hv] = v4f{0.f, 0.f, 0.f, 0.f};
+      zacc[rs][hv] = 0.f;
+    }
     lsum[rs] = 0.f;
   }
   {
-    ValueParams vp;
-    ValueWords<BITS> vw0, vw1;
-    ValueA<NRS> A;
-    auto step = [&](int k, ValueWords<BITS>& cur, ValueWords<BITS>& next) {
+    ValueParams<D> vp;
+    ValueWords<BITS, D> vw0, vw1;
+    ValueA<NRS, D> A;
+    auto step = [&](int k, ValueWords<BITS, D>& cur, ValueWords<BITS, D>& next) {
       const uint64_t t0 = (uint64_t)chunk_of(k) * 64;
       const bool packed = !MIXED || t0 < vq;
+      if constexpr (D == 128) {
       if (a.pend_evict && t0 + 64 >= vq && t0 < vq) {
         // the evicted token vq-1 is in this chunk: its codes and (scale, zero) join the chunk's
         // registers and go to memory (the only reader of those words this launch is here)
@@ -1092,6 +1134,7 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
           atomicMax(a.c.smax + 4 * unit + 3, __float_as_uint(ev_amax));
         }
       }
+      }  // D == 128 (the decode is fused into the launch at head_dim 128 only)
       float w[NRS][8];
 #pragma unroll
       for (int rs = 0; rs < NRS; ++rs) {
@@ -1104,23 +1147,25 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
           lsum[rs] += w[rs][r];
         }
       }
-      if (packed) value_operands<NRS>(vp, w, A, zacc);
+      if (packed) value_operands<NRS, D>(vp, w, A, zacc);
       if constexpr (CPW > 1) {
         const int32_t kn = std::min(chunk_of(std::min(k + 1, nch - 1)), lastv);
-        load_value_params(a, unit, kn, la, lc, li, vp);
-        load_value_words<BITS>(a, unit, kn, lane, next);
+        load_value_params<D>(a, unit, kn, la, lc, li, vp);
+        load_value_words<BITS, D>(a, unit, kn, lane, next);
       }
-      if (packed) value_mfma<BITS, NRS>(cur, A, vacc);
-      if (MIXED && t0 + 16 * quarter + 16 > vq && t0 + 16 * quarter < total) {
-        ValueRows vr;
-        load_value_rows(a, unit, t0, quarter, lane, vr);
-        value_fp32<NRS>(a, t0, quarter, la, wl + li * ROW, moff, kout, vfac * kUnit, vr, vacc);
+      if (packed) value_mfma<BITS, NRS, D>(cur, A, vacc);
+      if constexpr (MIXED) {
+        if (t0 + 16 * quarter + 16 > vq && t0 + 16 * quarter < total) {
+          ValueRows vr;
+          load_value_rows(a, unit, t0, quarter, lane, vr);
+          value_fp32<NRS>(a, t0, quarter, la, wl + li * ROW, moff, kout, vfac * kUnit, vr, vacc);
+        }
       }
     };
     if (nch > 0) {
       const int32_t v0 = std::min(chunk_of(0), lastv);
-      load_value_params(a, unit, v0, la, lc, li, vp);
-      load_value_words<BITS>(a, unit, v0, lane, vw0);
+      load_value_params<D>(a, unit, v0, la, lc, li, vp);
+      load_value_words<BITS, D>(a, unit, v0, lane, vw0);
     }
     for (int k = 0; k < nch; k += 2) {
       step(k, vw0, vw1);
@@ -1132,18 +1177,19 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
 #pragma unroll
   for (int rs = 0; rs < NRS; ++rs) {
     lsum[rs] = sum_over_blocks(lsum[rs]);
-    zacc[rs][0] = sum_over_blocks(zacc[rs][0]);
-    zacc[rs][1] = sum_over_blocks(zacc[rs][1]);
+#pragma unroll
+    for (int hv = 0; hv < HV; ++hv) zacc[rs][hv] = sum_over_blocks(zacc[rs][hv]);
   }
   __syncthreads();  // every wave is done with its logits; reuse LDS for the combine
   float* cw = lds + wave * NH * (D + 2);
 #pragma unroll
   for (int rs = 0; rs < NRS; ++rs) {
 #pragma unroll
-    for (int hv = 0; hv < 2; ++hv) {
+    for (int hv = 0; hv < HV; ++hv) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        // zero term of head i, channel group lc + 2*hv lives in lane 32*lc + i
+        // zero term of head i, the channel group of channels 32*lc + 64*hv, lives in lane
+        // 32*lc + i
         const float z = __shfl(zacc[rs][hv], 32 * lc + i) * vinv;
         cw[(rs * 4 + i) * (D + 2) + lane + 64 * hv] = fmaf(vacc[rs][hv][i], vout, z);
       }
@@ -1154,9 +1200,9 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
     }
   }
   __syncthreads();
-  // the head group's rows hg*8 .. (the unit's heads gq; NH = 8 whenever hg > 0)
-  const uint32_t hrows = std::min<uint32_t>(NH, gq - hg * 8);
-  float* part = a.ws + (((uint64_t)unit * a.nsplit_total + split_base + split) * gq + hg * 8) * (D + 2);
+  // the head group's rows hg*NH .. (the unit's heads gq)
+  const uint32_t hrows = std::min<uint32_t>(NH, gq - hg * NH);
+  float* part = a.ws + (((uint64_t)unit * a.nsplit_total + split_base + split) * gq + hg * NH) * (D + 2);
   for (uint32_t idx = threadIdx.x; idx < hrows * (D + 2); idx += blockDim.x) {
     const uint32_t h = idx / (D + 2), d = idx % (D + 2);
     float M = -INFINITY;
@@ -1184,19 +1230,33 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
 // Resident workgroups per CU asked of the register allocator per instantiation (4-wave
 // workgroups, so also waves per SIMD): it then packs the 4-bit GQA-4 kernel into 128 VGPRs
 // (4 waves) and the GQA-8 ones into 168 (3 waves) without spills.
-template <int BITS, int NRS>
-__global__ void __launch_bounds__(kThreads, (NRS == 1 && BITS <= 4) ? 4 : (BITS == 8 && NRS == 2) ? 2 : 3)
+constexpr int fast_min_groups(int bits, int nrs, int d) {
+  return d == 256 ? 3 : (nrs == 1 && bits <= 4) ? 4 : (bits == 8 && nrs == 2) ? 2 : 3;
+}
+template <int BITS, int NRS, int D>
+__global__ void __launch_bounds__(kThreads, fast_min_groups(BITS, NRS, D))
     k_attn_mfma(AttnArgs a) {
   extern __shared__ float lds[];
-  // workgroups of (unit, head group) pairs: vu = unit * hgroups + hg
+  // workgroups of (unit, head group) pairs: vu = unit * hgroups + hg. First in the grid, so
+  // their latency-bound fp32 rows overlap the packed chunks: at head_dim 128 the window /
+  // suffix chunks, at other head_dims the generic splits over the tokens after the packed
+  // chunks (one of the two counts is zero).
   const uint32_t nwin = a.units * a.hgroups * a.nsplit_win;
-  if (blockIdx.x < nwin) {
-    const uint32_t vu = blockIdx.x / a.nsplit_win;
-    mfma_split<BITS, NRS, 1, true>(a, vu / a.hgroups, blockIdx.x % a.nsplit_win, vu % a.hgroups, lds);
+  const uint32_t ngen = a.units * a.nsplit_gen;
+  if constexpr (D == 128) {
+    if (blockIdx.x < nwin) {
+      const uint32_t vu = blockIdx.x / a.nsplit_win;
+      mfma_split<BITS, NRS, 1, true, D>(a, vu / a.hgroups, blockIdx.x % a.nsplit_win, vu % a.hgroups, lds);
+      return;
+    }
   } else {
-    const uint32_t blk = blockIdx.x - nwin, vu = blk / a.nsplit_fast;
-    mfma_split<BITS, NRS, fast_cpw(BITS, NRS), false>(a, vu / a.hgroups, blk % a.nsplit_fast, vu % a.hgroups, lds);
+    if (blockIdx.x < ngen) {
+      generic_split<BITS, D, 0>(a, blockIdx.x / a.nsplit_gen, blockIdx.x % a.nsplit_gen, lds);
+      return;
+    }
   }
+  const uint32_t blk = blockIdx.x - nwin - ngen, vu = blk / a.nsplit_fast;
+  mfma_split<BITS, NRS, fast_cpw(BITS, NRS), false, D>(a, vu / a.hgroups, blk % a.nsplit_fast, vu % a.hgroups, lds);
 }
 
 // Arguments of session s of a batched call: its queries, partials and suffix.
@@ -1230,7 +1290,7 @@ __global__ void __launch_bounds__(kThreads) k_attn_sessions(AttnArgs a, SessionT
   if (blockIdx.x < nwin) {
     const uint32_t s = blockIdx.x / per_sess, r = blockIdx.x % per_sess;
     const AttnArgs as = session_args(a, t, s);
-    mfma_split<BITS, NRS, 1, true>(as, r / a.nsplit_win, r % a.nsplit_win, 0, lds);
+    mfma_split<BITS, NRS, 1, true, 128>(as, r / a.nsplit_win, r % a.nsplit_win, 0, lds);
   } else {
     const uint32_t blk = blockIdx.x - nwin;
     const uint32_t unit = blk / a.nsplit_fast, split = blk % a.nsplit_fast;
@@ -1238,7 +1298,7 @@ __global__ void __launch_bounds__(kThreads) k_attn_sessions(AttnArgs a, SessionT
       AttnArgs as = a;
       as.query = a.query + s * a.q_sess_stride;
       as.ws = a.ws + s * a.ws_sess_stride;
-      mfma_split<BITS, NRS, kSessCpw, false>(as, unit, split, 0, lds);
+      mfma_split<BITS, NRS, kSessCpw, false, 128>(as, unit, split, 0, lds);
       __syncthreads();  // the next session reuses the LDS
     }
   }
@@ -2051,15 +2111,22 @@ uint32_t split_tokens(uint32_t gq) {
   return s;
 }
 
-// Shapes of the matrix-core path: D = 128, G = 32 or a multiple of 64 (a chunk's half-waves
-// then read one key group), any GQA up to 32 (above 8 in head groups of 8).
+// Shapes of the matrix-core path: head_dim 128 or 64 (any bits) or 256 (2-bit: the code words
+// of wider codes would not fit the registers), G = 32 or a multiple of 64 (a chunk's half-waves
+// then read one key group), GQA up to 32 in head groups (of 8, or 4 at head_dim 256).
 bool fast_eligible(const AttnProblem& p) {
   const Geometry& g = p.cache.geo;
   const uint32_t gq = p.qh / p.heads;
-  return g.D == 128 && (g.G == 32 || g.G % 64 == 0) && (g.bits == 2 || g.bits == 4 || g.bits == 8) &&
-         gq >= 1 && gq <= 32;
+  const bool dim_ok = g.D == 128 || g.D == 64 || (g.D == 256 && g.bits == 2);
+  return dim_ok && (g.G == 32 || g.G % 64 == 0) && (g.bits == 2 || g.bits == 4 || g.bits == 8) && gq >= 1 &&
+         gq <= 32;
 }
-uint32_t head_groups(uint32_t gq) { return gq <= 8 ? 1u : (gq + 7) / 8; }
+// MFMA row sets (4 heads each) per workgroup, and the head groups of a unit
+int fast_nrs(uint32_t D, uint32_t gq) { return D == 256 || gq <= 4 ? 1 : 2; }
+uint32_t head_groups(uint32_t D, uint32_t gq) {
+  const uint32_t per = 4u * static_cast<uint32_t>(fast_nrs(D, gq));
+  return (gq + per - 1) / per;
+}
 
 // Shapes k_attn_vpack takes (outside the matrix-core path): D a multiple of 64 up to 256, G 32
 // or a multiple of 64, bits 2/4/8.
@@ -2094,25 +2161,35 @@ AttnArgs make_args(const AttnProblem& p, float* ws) {
   // [0, floor(vq/64)) (keys and values all packed) in one launch, the rest (the fp32 value
   // window and key residual, the session suffix) in a second launch of the MIXED kernel.
   // Without packed keys, or for other shapes, the generic splits cover everything.
+  // At head_dim 64 and 256 the MFMA launch takes only the fully packed chunks and the generic
+  // splits the rest.
   const bool fast = fast_eligible(p) && p.st.kq > 0;
+  const bool fast_win = fast && p.cache.geo.D == 128;
   a.S = split_tokens(a.gq);
   a.chunk_begin = 0;
-  a.chunk_end = fast ? static_cast<uint32_t>(p.st.vq / 64) : 0;
+  a.chunk_end = fast ? static_cast<uint32_t>(std::min(p.st.kq, p.st.vq) / 64) : 0;
   a.win_begin = a.chunk_end;
-  a.win_end = fast ? static_cast<uint32_t>((a.total + 63) / 64) : 0;
-  a.hgroups = fast ? head_groups(a.gq) : 1u;
+  a.win_end = fast_win ? static_cast<uint32_t>((a.total + 63) / 64) : a.chunk_end;
+  a.hgroups = fast ? head_groups(p.cache.geo.D, a.gq) : 1u;
   a.gshift = fast ? static_cast<uint32_t>(__builtin_ctz(p.cache.geo.G)) : 5u;
   // packed splits per unit: at most kFastCpw chunks per wave, at least one, and at least
   // kFastGroups workgroups (over units and head groups) when the chunks allow
   {
     const uint32_t units = p.cache.geo.units * a.hgroups;
-    const uint32_t cpw = static_cast<uint32_t>(fast_cpw(static_cast<int>(p.cache.geo.bits), a.gq <= 4 ? 1 : 2));
+    const uint32_t cpw = static_cast<uint32_t>(fast_cpw(static_cast<int>(p.cache.geo.bits), fast_nrs(p.cache.geo.D, a.gq)));
     const uint32_t fewest = (a.chunk_end + 4 * cpw - 1) / (4 * cpw);
     const uint32_t most = (a.chunk_end + 3) / 4;
     a.nsplit_fast = std::min(most, std::max(fewest, (kFastGroups + units - 1) / units));
   }
   a.nsplit_win = a.win_end - a.win_begin;  // one chunk per workgroup, a quarter per wave
-  a.t_begin = fast ? a.total : 0;
+  a.t_begin = fast_win ? a.total : fast ? (uint64_t)a.chunk_end * 64 : 0;
+  if (fast && !fast_win) {
+    // the rest is short (the fp32 residual and window, a suffix): shorter splits, down to 16
+    // tokens while the rest would fill fewer than ~1024 workgroups
+    a.S = std::max(32u, a.S / 4);
+    const uint64_t rest = a.total - a.t_begin;
+    while (a.S > 16 && (uint64_t)p.cache.geo.units * ((rest + a.S - 1) / a.S) < 1024) a.S >>= 1;
+  }
   a.vpack = 0;
   if (!fast && vpack_eligible(p)) {
     // packed 64-token blocks [0, floor(min(kq, vq)/64)) to k_attn_vpack, in splits of at least
@@ -2145,26 +2222,36 @@ AttnArgs make_args(const AttnProblem& p, float* ws) {
   return a;
 }
 
-template <int BITS, int NRS>
+template <int BITS, int NRS, int D>
 hipError_t launch_fast(const AttnArgs& a, double bytes, hipStream_t stream) {
   constexpr int NH = 4 * NRS;
   const size_t logits = (size_t)4 * NH * ((a.nsplit_fast > 0 ? fast_cpw(BITS, NRS) : 1) * 64 + kRowPad);
-  const size_t combine = (size_t)4 * NH * (128 + 2);
-  const size_t lds = std::max(logits, combine) * sizeof(float);
+  const size_t combine = (size_t)4 * NH * (D + 2);
+  const size_t gen = a.nsplit_gen > 0 ? (size_t)a.gq * (D + a.S) : 0;  // generic splits' q and weights
+  const size_t lds = std::max(std::max(logits, combine), gen) * sizeof(float);
   TimedLaunch timed(KIVI_KERNEL_ATTN_PACKED, stream, bytes);
-  k_attn_mfma<BITS, NRS><<<a.units * a.hgroups * (a.nsplit_win + a.nsplit_fast), kThreads, lds, stream>>>(a);
+  const uint32_t grid = a.units * (a.hgroups * (a.nsplit_win + a.nsplit_fast) + a.nsplit_gen);
+  k_attn_mfma<BITS, NRS, D><<<grid, kThreads, lds, stream>>>(a);
   return hipGetLastError();
 }
 
 hipError_t dispatch_fast(const AttnArgs& a, double bytes, hipStream_t stream) {
-  const int nrs = a.gq <= 4 ? 1 : 2;
-  switch (a.c.geo.bits * 10 + nrs) {
-    case 21: return launch_fast<2, 1>(a, bytes, stream);
-    case 22: return launch_fast<2, 2>(a, bytes, stream);
-    case 41: return launch_fast<4, 1>(a, bytes, stream);
-    case 42: return launch_fast<4, 2>(a, bytes, stream);
-    case 81: return launch_fast<8, 1>(a, bytes, stream);
-    case 82: return launch_fast<8, 2>(a, bytes, stream);
+  const uint32_t D = a.c.geo.D;
+  const int nrs = fast_nrs(D, a.gq);
+  switch (D * 100 + a.c.geo.bits * 10 + nrs) {
+    case 12821: return launch_fast<2, 1, 128>(a, bytes, stream);
+    case 12822: return launch_fast<2, 2, 128>(a, bytes, stream);
+    case 12841: return launch_fast<4, 1, 128>(a, bytes, stream);
+    case 12842: return launch_fast<4, 2, 128>(a, bytes, stream);
+    case 12881: return launch_fast<8, 1, 128>(a, bytes, stream);
+    case 12882: return launch_fast<8, 2, 128>(a, bytes, stream);
+    case 6421: return launch_fast<2, 1, 64>(a, bytes, stream);
+    case 6422: return launch_fast<2, 2, 64>(a, bytes, stream);
+    case 6441: return launch_fast<4, 1, 64>(a, bytes, stream);
+    case 6442: return launch_fast<4, 2, 64>(a, bytes, stream);
+    case 6481: return launch_fast<8, 1, 64>(a, bytes, stream);
+    case 6482: return launch_fast<8, 2, 64>(a, bytes, stream);
+    case 25621: return launch_fast<2, 1, 256>(a, bytes, stream);
     default: return hipErrorInvalidValue;
   }
 }
@@ -2244,7 +2331,7 @@ hipError_t launch_fill_zero(float* out, size_t n, hipStream_t stream) {
 bool attention_fuses_decode(const AttnProblem& p) {
   const AttnArgs a = make_args(p, nullptr);
   return a.total > 0 && !a.vpack && a.nsplit_gen == 0 && (a.nsplit_fast > 0 || a.nsplit_win > 0) &&
-         p.cache.geo.G == 32 && a.hgroups == 1;
+         p.cache.geo.D == 128 && p.cache.geo.G == 32 && a.hgroups == 1;
 }
 
 size_t attention_workspace_floats(const AttnProblem& p) {
@@ -2280,7 +2367,9 @@ hipError_t launch_attention(const AttnProblem& p, float* workspace, hipStream_t 
       if (e != hipSuccess) return e;
     }
   } else if (a.nsplit_fast > 0 || a.nsplit_win > 0) {
-    // one launch over every chunk: packed tokens at packed cost, the rest as fp32 rows
+    // one launch over every chunk (the tokens after the packed chunks as window chunks at
+    // head_dim 128, as generic splits in the same grid otherwise): packed tokens at packed
+    // cost, the rest as fp32 rows
     const double kpt = (double)std::min<uint64_t>(kq, p.seq), vpt = (double)vq;
     const double fp32_rows = (double)(p.seq - kq) + (double)(p.seq - vq) + 2.0 * p.suffix_len;
     hipError_t e = dispatch_fast(
@@ -2331,8 +2420,9 @@ bool sessions_supported(const SessionsProblem& sp) {
   p.st = sp.st;
   p.qh = sp.qh;
   p.heads = sp.heads;
-  // the batched-sessions kernels take G = 32 and GQA <= 8
-  return sp.n > 0 && fast_eligible(p) && sp.st.kq > 0 && sp.cache.geo.G == 32 && sp.qh / sp.heads <= 8;
+  // the batched-sessions kernels take head_dim 128, G = 32 and GQA <= 8
+  return sp.n > 0 && fast_eligible(p) && sp.st.kq > 0 && sp.cache.geo.D == 128 && sp.cache.geo.G == 32 &&
+         sp.qh / sp.heads <= 8;
 }
 
 uint64_t longest_suffix(const SessionsProblem& sp, uint32_t first, uint32_t count) {

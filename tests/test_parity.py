@@ -94,14 +94,16 @@ def test_streaming_cache_parity(amd, oracle, bits, group, residual, dim, schedul
 
 
 @pytest.mark.parametrize("dim,group,gqa,bits", [
-    (64, 32, 4, 2), (64, 64, 1, 4), (64, 32, 2, 8), (192, 64, 3, 2), (256, 32, 4, 4), (256, 128, 2, 8),
+    (64, 32, 4, 2), (64, 64, 1, 4), (64, 32, 2, 8), (64, 64, 12, 2), (64, 32, 8, 8), (192, 64, 3, 2),
+    (256, 32, 4, 4), (256, 128, 2, 8), (256, 32, 4, 2), (256, 64, 8, 2), (256, 128, 3, 2),
     (128, 64, 4, 2), (128, 32, 16, 2), (128, 128, 12, 4), (128, 128, 32, 2), (128, 64, 8, 8),
     (128, 64, 1, 4), (96, 32, 4, 2)])
 def test_other_shapes_attention_parity(amd, oracle, dim, group, gqa, bits):
-    """Shapes beyond head_dim 128 / G 32 / GQA <= 8. head_dim 128 with G a multiple of 64 or
-    GQA up to 32 stays on the matrix-core path (one key group per chunk half, query heads in
-    groups of 8 with a short last group); other head_dims go to the wave-per-split kernel
-    (head_dim a multiple of 64 up to 256, heads in passes of up to 8, the extra heads of a last
+    """Shapes beyond head_dim 128 / G 32 / GQA <= 8. head_dim 128 and 64 (and 256 at 2 bits)
+    stay on the matrix-core path: one key group per chunk half when G >= 64, query heads in
+    groups of 8 (4 at head_dim 256) with a short last group, and at head_dim 64/256 only the
+    fully packed chunks there, the rest on the generic splits. head_dim 192 and 256 at 4/8
+    bits go to the wave-per-split kernel (heads in passes of up to 8, the extra heads of a last
     pass dropped) and the generic splits; head_dim 96 stays on the generic splits alone. Many
     splits, against the oracle and f64 dense attention on the dequantized cache."""
     batch, heads = 2, 2
@@ -395,18 +397,19 @@ def test_runtime_decode_parity(amd, oracle):
     assert_streams_equal(ra.cache(), ro.cache())
 
 
-@pytest.mark.parametrize("bits,residual,gqa,group", [(2, 64, 4, 32), (4, 64, 8, 32), (8, 128, 4, 32),
-                                                     (2, 128, 1, 32), (2, 128, 4, 64), (4, 128, 16, 128)])
-def test_runtime_decode_device_parity(amd, oracle, bits, residual, gqa, group):
+@pytest.mark.parametrize("bits,residual,gqa,group,dim", [
+    (2, 64, 4, 32, 128), (4, 64, 8, 32, 128), (8, 128, 4, 32, 128), (2, 128, 1, 32, 128), (2, 128, 4, 64, 128),
+    (4, 128, 16, 128, 128), (4, 64, 4, 32, 64), (2, 128, 8, 64, 256)])
+def test_runtime_decode_device_parity(amd, oracle, bits, residual, gqa, group, dim):
     """RuntimeKv::decode on device pointers, which runs append + attention in one attention
     launch (the token the window evicts quantized inside it) for G = 32 and GQA <= 8 when no
     key flush is due, and as an append then an attention launch otherwise: bit for bit equal to
     a cache taking append_device then attention_device (tests/runtime.rs:13-52), and within
     tolerance of the oracle's decode, streams bit-exact, across evictions and flushes."""
-    heads, dim, prefill, steps = 2, 128, 3 * residual + 17, 2 * residual + 5
+    heads, prefill, steps = 2, 3 * residual + 17, 2 * residual + 5
     qh = heads * gqa
     cfg = KiviConfig(bits, group, residual)
-    rng = np.random.default_rng(300 + bits + residual + gqa + group)
+    rng = np.random.default_rng(300 + bits + residual + gqa + group + dim)
     k = rng.standard_normal(heads * prefill * dim).astype(np.float32)
     v = rng.standard_normal(heads * prefill * dim).astype(np.float32)
     k.reshape(heads, prefill, dim)[:, :, 5] *= 10
