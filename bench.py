@@ -79,6 +79,8 @@ CONFIGS = {
     "g_d256": (4, 8, 32, 256, 32768, 2, 32, 128, "generic path: batch 4, 32q/8kv heads, head_dim 256, 32768 tokens, 2-bit"),
     "g_gqa16": (4, 4, 64, 128, 32768, 2, 32, 128, "generic path: batch 4, 64q/4kv heads (GQA 16), head_dim 128, 32768 tokens, 2-bit"),
     "g_g64": (16, 8, 32, 128, 32768, 2, 64, 128, "generic path: batch 16, 32q/8kv heads, head_dim 128, 32768 tokens, 2-bit G=64"),
+    "g_d256_b4": (4, 8, 32, 256, 32768, 4, 32, 128, "generic path: batch 4, 32q/8kv heads, head_dim 256, 32768 tokens, 4-bit"),
+    "g_d256_b8": (4, 8, 32, 256, 32768, 8, 32, 128, "generic path: batch 4, 32q/8kv heads, head_dim 256, 32768 tokens, 8-bit"),
 }
 SECONDARY = ("c0", "c1", "c3_4", "c3_8", "c4")
 # batched-sessions workloads: name -> (sessions, suffix tokens per session)
@@ -87,7 +89,7 @@ SESSIONS = {"c4": (64, 96)}
 DECODE = {"c1": 512}
 # CPU-baseline time per workload (seconds of oracle work, beyond its prefill)
 CPU_SECONDS = {"c2": 12.0, "c0": 3.0, "c1": 5.0, "c3_4": 4.0, "c3_8": 4.0, "c4": 5.0,
-               "g_d64": 3.0, "g_d256": 3.0, "g_gqa16": 3.0, "g_g64": 3.0}
+               "g_d64": 3.0, "g_d256": 3.0, "g_gqa16": 3.0, "g_g64": 3.0, "g_d256_b4": 3.0, "g_d256_b8": 3.0}
 
 
 def log(*a):
@@ -520,10 +522,9 @@ def measure(name, args, torch, kivi, amd, stream, with_cpu):
     if sessions_cfg and "attn_shared" in kernels:
         dom_fam, dom_name = "attn_shared", "k_attn_shared"
     elif "attn_packed" in kernels:
-        # the matrix-core kernel takes head_dim 128 and 64 (and 256 at 2 bits), G = 32 or a
-        # multiple of 64, GQA up to 32; other head_dims the packed-token kernel
-        fast_shape = (dim in (64, 128) or (dim == 256 and bits == 2)) and (G == 32 or G % 64 == 0) \
-            and qh // heads <= 32
+        # the matrix-core kernel takes head_dim 64, 128 and 256, G = 32 or a multiple of 64,
+        # GQA up to 32; other head_dims the packed-token kernel
+        fast_shape = dim in (64, 128, 256) and (G == 32 or G % 64 == 0) and qh // heads <= 32
         dom_fam, dom_name = "attn_packed", "k_attn_mfma" if fast_shape else "k_attn_vpack"
     elif "attn_sessions" in kernels:
         dom_fam, dom_name = "attn_sessions", "k_attn_sessions"

@@ -1229,9 +1229,10 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
 //
 // Resident workgroups per CU asked of the register allocator per instantiation (4-wave
 // workgroups, so also waves per SIMD): it then packs the 4-bit GQA-4 kernel into 128 VGPRs
-// (4 waves) and the GQA-8 ones into 168 (3 waves) without spills.
+// (4 waves) and the GQA-8 ones into 168 (3 waves) without spills; head_dim 256 at 4/8 bits
+// holds twice the code words and takes two (up to 256 VGPRs).
 constexpr int fast_min_groups(int bits, int nrs, int d) {
-  return d == 256 ? 3 : (nrs == 1 && bits <= 4) ? 4 : (bits == 8 && nrs == 2) ? 2 : 3;
+  return d == 256 ? (bits == 2 ? 3 : 2) : (nrs == 1 && bits <= 4) ? 4 : (bits == 8 && nrs == 2) ? 2 : 3;
 }
 template <int BITS, int NRS, int D>
 __global__ void __launch_bounds__(kThreads, fast_min_groups(BITS, NRS, D))
@@ -2111,13 +2112,13 @@ uint32_t split_tokens(uint32_t gq) {
   return s;
 }
 
-// Shapes of the matrix-core path: head_dim 128 or 64 (any bits) or 256 (2-bit: the code words
-// of wider codes would not fit the registers), G = 32 or a multiple of 64 (a chunk's half-waves
-// then read one key group), GQA up to 32 in head groups (of 8, or 4 at head_dim 256).
+// Shapes of the matrix-core path: head_dim 64, 128 or 256, G = 32 or a multiple of 64 (a
+// chunk's half-waves then read one key group), GQA up to 32 in head groups (of 8, or 4 at
+// head_dim 256).
 bool fast_eligible(const AttnProblem& p) {
   const Geometry& g = p.cache.geo;
   const uint32_t gq = p.qh / p.heads;
-  const bool dim_ok = g.D == 128 || g.D == 64 || (g.D == 256 && g.bits == 2);
+  const bool dim_ok = g.D == 128 || g.D == 64 || g.D == 256;
   return dim_ok && (g.G == 32 || g.G % 64 == 0) && (g.bits == 2 || g.bits == 4 || g.bits == 8) && gq >= 1 &&
          gq <= 32;
 }
@@ -2252,6 +2253,8 @@ hipError_t dispatch_fast(const AttnArgs& a, double bytes, hipStream_t stream) {
     case 6481: return launch_fast<8, 1, 64>(a, bytes, stream);
     case 6482: return launch_fast<8, 2, 64>(a, bytes, stream);
     case 25621: return launch_fast<2, 1, 256>(a, bytes, stream);
+    case 25641: return launch_fast<4, 1, 256>(a, bytes, stream);
+    case 25681: return launch_fast<8, 1, 256>(a, bytes, stream);
     default: return hipErrorInvalidValue;
   }
 }
