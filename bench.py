@@ -82,7 +82,7 @@ CONFIGS = {
     "g_d256_b4": (4, 8, 32, 256, 32768, 4, 32, 128, "generic path: batch 4, 32q/8kv heads, head_dim 256, 32768 tokens, 4-bit"),
     "g_d256_b8": (4, 8, 32, 256, 32768, 8, 32, 128, "generic path: batch 4, 32q/8kv heads, head_dim 256, 32768 tokens, 8-bit"),
 }
-SECONDARY = ("c0", "c1", "c3_4", "c3_8", "c4")
+SECONDARY = ("c0", "c1", "c3_4", "c3_8", "c4", "g_d64", "g_d256", "g_d256_b4", "g_d256_b8", "g_g64", "g_gqa16")
 # batched-sessions workloads: name -> (sessions, suffix tokens per session)
 SESSIONS = {"c4": (64, 96)}
 # streaming-decode workloads: name -> decode steps the workload allows after the prefill
