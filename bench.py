@@ -23,8 +23,7 @@ Infinity Cache rotate over identical copies between steps (`cache_copies`), so e
 HBM; C0 and C1 are too small for that and report `cache_resident: true`.
 
 `roofline` is for the dominant kernel: the packed-chunk attention kernel (k_attn_mfma, HBM
-bound: algorithmic bytes per launch over its mean launch duration; k_attn_vpack for shapes
-outside the matrix-core path), or for c4 the shared-prefix
+bound: algorithmic bytes per launch over its mean launch duration), or for c4 the shared-prefix
 GEMM kernel (k_attn_shared, matrix-core bound: 4*D flops per (session row, prefix token) over
 its mean duration, against the dense f16 MFMA peak). `traffic` is that kernel's HBM bytes per
 launch from rocprofv3 FETCH_SIZE + WRITE_SIZE runs calibrated on a plain copy kernel
@@ -522,10 +521,7 @@ def measure(name, args, torch, kivi, amd, stream, with_cpu):
     if sessions_cfg and "attn_shared" in kernels:
         dom_fam, dom_name = "attn_shared", "k_attn_shared"
     elif "attn_packed" in kernels:
-        # the matrix-core kernel takes head_dim 64, 128 and 256, G = 32 or a multiple of 64,
-        # GQA up to 32; other head_dims the packed-token kernel
-        fast_shape = dim in (64, 128, 256) and (G == 32 or G % 64 == 0) and qh // heads <= 32
-        dom_fam, dom_name = "attn_packed", "k_attn_mfma" if fast_shape else "k_attn_vpack"
+        dom_fam, dom_name = "attn_packed", "k_attn_mfma"
     elif "attn_sessions" in kernels:
         dom_fam, dom_name = "attn_sessions", "k_attn_sessions"
     else:

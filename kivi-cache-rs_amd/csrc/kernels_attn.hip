@@ -8,20 +8,28 @@
 // within f32 rounding (never bitwise). Logits are kept in base-2 units
 // (q pre-multiplied by scale*log2(e)) so every exponential is one v_exp_f32.
 //
-// Two split kinds write one workspace of partials (m, l, acc[D]) per (unit, split, head):
-//  * k_attn_mfma — every 64-token chunk whose keys AND values are packed
-//    (tokens [0, 64*floor(vq/64))), for G=32, D=128, bits 2/4/8 and GQA <= 8. Both
-//    contractions run on the matrix cores (v_mfma_f32_4x4x1_16B, fp32 products):
+// The split kernels write one workspace of partials (m, l, acc[D]) per (unit, split, head);
+// k_attn_merge combines them:
+//  * k_attn_mfma<BITS,NRS,D> — every 64-token chunk whose keys AND values are packed, for
+//    head_dim 64/128/192/256, G = 32 or a multiple of 64, bits 2/4/8, any GQA (rows of 4
+//    heads, NRS row sets per workgroup, head groups beyond that). Both contractions run on
+//    the matrix cores (v_mfma_f32_4x4x4_16b_f16; the non-code operand as f16 hi + lo, about
+//    22 significant bits; the codes exact):
 //      logits[h][t] = bias_g[h] + sum_d (q[h][d]*scale_g[d]) * code[d][t]
 //      out[h][d]   += sum_t (w[h][t]*scale_t[cg]) * code[t][d] + sum_t w[h][t]*zero_t[cg]
 //    The GQA heads are the 4 MFMA rows; the 16 4x4 blocks tile 64 tokens (keys) or 64
-//    channels (values); CBSZ/ABID broadcast lets one A register feed 8 K-steps. A lane
-//    owns a token (keys) or a channel (values), and the native layout packs exactly that
-//    lane's codes into its words, so a word unpacks into 4-16 MFMA B operands.
-//  * k_attn_generic — the remaining tokens (the fp32 window and its band of packed keys,
-//    the session suffix) and every shape the MFMA kernel does not cover: one
-//    thread per token in the reference's operation order (recon = fma(code, scale, zero);
-//    logit = fma(recon, q, logit), channels ascending, src/attention.rs:143-177, 289-300).
+//    channels (values); CBSZ/ABID broadcast lets one A register feed 8 K-steps. A lane owns
+//    a token (keys) or D/64 channels (values), and the native layout packs exactly that
+//    lane's codes into its words, so a word unpacks into 4-16 MFMA B operands. At head_dim
+//    128 the same launch takes the window / suffix chunks (fp32 rows, a quarter chunk per
+//    wave); at other head_dims the tokens after the packed chunks run as generic splits in
+//    its grid.
+//  * k_attn_shared / k_attn_sessions / k_attn_suffix — batched sessions over one shared
+//    prefix (the prefix read once for all sessions).
+//  * k_attn_generic — every shape the MFMA kernel does not cover, caches with no packed keys
+//    yet and the quality guard's fp32 attention: one wavefront per token in the reference's
+//    operation order (recon = fma(code, scale, zero); logit = fma(recon, q, logit), channels
+//    ascending, src/attention.rs:143-177, 289-300).
 #include "common.hpp"
 #include "kivi.h"
 
@@ -63,9 +71,6 @@ struct AttnArgs {
   uint32_t win_begin, win_end;
   uint32_t nsplit_win;
   uint32_t nsplit_total;   // splits per unit in the workspace
-  // shapes outside the matrix-core path: k_attn_vpack takes 64-token blocks [0, chunk_end)
-  // (keys and values packed) in splits 0 .. nsplit_fast-1, the generic splits the rest
-  uint32_t vpack;
   // query heads in groups of up to 8 (GQA > 8 on the matrix-core path): one workgroup per
   // (unit, head group, split), each writing its group's partial rows
   uint32_t hgroups;
@@ -269,136 +274,6 @@ __global__ void __launch_bounds__(kThreads) k_attn_generic(AttnArgs a) {
   generic_split<BITS, DD, GG>(a, unit, blockIdx.x % a.nsplit_gen, lds);
 }
 
-// ------------------------------------------------------------------ packed blocks, other shapes
-// Shapes outside the matrix-core path with D % 64 == 0, D <= 256 and G 32 or a multiple of 64:
-// one wave per (unit, split) over 64-token blocks whose keys and values are all packed, with a
-// running maximum and rescaled sums across the blocks. The wave-uniform operands sit in LDS
-// and are read as broadcasts: the pass's queries ([channel][head]) and each block's key and
-// value (scale, zero). Keys: lane = token, a code becomes fma(code, scale, zero), then one fma
-// per head. Values: lane = channels c = lane + 64j, with the block's probabilities from LDS.
-// With G = 32 a block holds two key groups (lanes 0-31 and 32-63) and a 64-channel slot two
-// value groups. Heads go in passes of HP (the last pass's extra heads read the last head's
-// query and are dropped).
-template <int BITS, bool G32, int HP>
-__global__ void __launch_bounds__(64) k_attn_vpack(AttnArgs a) {
-  constexpr uint32_t PPW = 32 / BITS, MASK = (1u << BITS) - 1u, VW = 64 / PPW;
-  __shared__ float qs[256][HP];     // the pass's queries [channel][head]
-  __shared__ float2 kps[2][256];    // the block's key (scale, zero) [group][channel]
-  __shared__ float2 vps[8][64];     // the block's value (scale, zero) [channel group][token]
-  __shared__ float pl[64][HP];      // the block's probabilities [token][head]
-  const Geometry& g = a.c.geo;
-  // KW = D / PPW is a multiple of 4 (D % 64 == 0, PPW <= 16): a token row is whole uint4 words
-  const uint32_t D = g.D, G = g.G, gq = a.gq, ncg = D / G, KW = D / PPW, DC = D / 64;
-  const uint32_t lane = threadIdx.x;
-  const uint32_t unit = blockIdx.x / a.nsplit_fast, split = blockIdx.x % a.nsplit_fast;
-  const uint32_t nblk = a.chunk_end;
-  const uint32_t bps = (nblk + a.nsplit_fast - 1) / a.nsplit_fast;
-  const uint32_t b0 = std::min(nblk, split * bps), b1 = std::min(nblk, b0 + bps);
-  const uint32_t bb = unit / a.heads, kvh = unit % a.heads;
-  const float* qbase = a.query + ((uint64_t)bb * a.qh + kvh * gq) * D;
-  const uint32_t* kc = a.c.kcodes + unit * g.kcodes_unit();
-  const float2* kp = reinterpret_cast<const float2*>(a.c.kparams + unit * g.kparams_unit());
-  const uint32_t* vc = a.c.vcodes + unit * g.vcodes_unit();
-  const float2* vp = reinterpret_cast<const float2*>(a.c.vparams + unit * g.vparams_unit());
-  const uint32_t hk = G32 && lane >= 32 ? 1 : 0;  // the lane's key group within a block
-  for (uint32_t h0 = 0; h0 < gq; h0 += HP) {
-    __syncthreads();  // the previous pass is done with the queries
-    for (uint32_t d = lane; d < D; d += 64)
-#pragma unroll
-      for (int h = 0; h < HP; ++h) qs[d][h] = qbase[(uint64_t)std::min<uint32_t>(h0 + h, gq - 1) * D + d];
-    float m[HP], ls[HP], o[HP][4];
-#pragma unroll
-    for (int h = 0; h < HP; ++h) {
-      m[h] = -INFINITY;
-      ls[h] = 0.f;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) o[h][j] = 0.f;
-    }
-    for (uint32_t blk = b0; blk < b1; ++blk) {
-      // the block's (scale, zero): key groups blk*64/G (+1 when G = 32), value groups of all
-      // channels for its 64 tokens
-      {
-        const float2* kpg = kp + (uint64_t)((uint64_t)blk * 64 / G) * D;
-        for (uint32_t i = lane; i < (G32 ? 2 : 1) * D; i += 64) kps[i / D][i % D] = kpg[i];
-        const float2* vpg = vp + (uint64_t)blk * ncg * 64;
-        for (uint32_t i = lane; i < ncg * 64; i += 64) vps[i / 64][i % 64] = vpg[i];
-      }
-      __syncthreads();
-      // logits, lane = token blk*64 + lane (base-2 units after the scale)
-      float acc[HP];
-#pragma unroll
-      for (int h = 0; h < HP; ++h) acc[h] = 0.f;
-      const uint4* kw = reinterpret_cast<const uint4*>(kc + ((uint64_t)blk * 64 + lane) * KW);
-      for (uint32_t w4 = 0; w4 < KW / 4; ++w4) {
-        const uint4 x = kw[w4];
-        const uint32_t words[4] = {x.x, x.y, x.z, x.w};
-#pragma unroll
-        for (uint32_t i = 0; i < 4 * PPW; ++i) {
-          const uint32_t d = (w4 * 4 + i / PPW) * PPW + i % PPW;
-          const float2 sz = kps[hk][d];
-          const float r = fmaf(static_cast<float>((words[i / PPW] >> code_shift(BITS, i % PPW)) & MASK), sz.x, sz.y);
-#pragma unroll
-          for (int h = 0; h < HP; ++h) acc[h] = fmaf(r, qs[d][h], acc[h]);
-        }
-      }
-      // running maxima, rescaled sums, the block's probabilities into LDS
-#pragma unroll
-      for (int h = 0; h < HP; ++h) {
-        const float lg = acc[h] * a.scale2;
-        float bm = lg;
-#pragma unroll
-        for (int sft = 32; sft >= 1; sft >>= 1) bm = fmaxf(bm, __shfl_xor(bm, sft));
-        const float mnew = fmaxf(m[h], bm);
-        const float alpha = m[h] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m[h] - mnew);
-        const float pr = __builtin_amdgcn_exp2f(lg - mnew);
-        ls[h] = fmaf(ls[h], alpha, pr);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) o[h][j] *= alpha;
-        m[h] = mnew;
-        pl[lane][h] = pr;
-      }
-      __syncthreads();
-      // values, lane = channels lane + 64j
-#pragma unroll
-      for (uint32_t j = 0; j < 4; ++j) {
-        if (j >= DC) break;
-        const uint32_t c = lane + 64 * j;
-        uint32_t words[VW];
-        const uint32_t* cw = vc + ((uint64_t)blk * D + c) * VW;
-#pragma unroll
-        for (uint32_t q = 0; q < VW; q += 4) {
-          const uint4 x = *reinterpret_cast<const uint4*>(cw + q);
-          words[q] = x.x; words[q + 1] = x.y; words[q + 2] = x.z; words[q + 3] = x.w;
-        }
-        const float2* vg = vps[c / G];
-        for (uint32_t tt = 0; tt < 64; ++tt) {
-          const float2 sz = vg[tt];
-          const float r = fmaf(static_cast<float>((words[tt / PPW] >> code_shift(BITS, tt % PPW)) & MASK), sz.x, sz.y);
-#pragma unroll
-          for (int h = 0; h < HP; ++h) o[h][j] = fmaf(pl[tt][h], r, o[h][j]);
-        }
-      }
-      __syncthreads();  // the block's operands are rewritten by the next block
-    }
-    // partials of the pass's heads
-#pragma unroll
-    for (int h = 0; h < HP; ++h) {
-      float l = ls[h];
-#pragma unroll
-      for (int sft = 32; sft >= 1; sft >>= 1) l += __shfl_xor(l, sft);
-      if (h0 + h >= gq) continue;
-      float* part = a.ws + (((uint64_t)unit * a.nsplit_total + split) * gq + h0 + h) * (D + 2);
-#pragma unroll
-      for (uint32_t j = 0; j < 4; ++j)
-        if (j < DC) part[lane + 64 * j] = o[h][j];
-      if (lane == 0) {
-        part[D] = b1 > b0 ? m[h] : -INFINITY;
-        part[D + 1] = b1 > b0 ? l : 0.f;
-      }
-    }
-  }
-}
-
 // ------------------------------------------------------------------ MFMA splits
 
 constexpr int kFastCpw = 8;  // chunks (64 tokens) per wave in the MFMA kernel
@@ -523,22 +398,22 @@ __device__ __forceinline__ void load_words(const uint32_t* p, uint32_t* w) {
   }
 }
 
-// Channel geometry of the matrix-core path for head_dim D (64, 128 or 256): keys in sets of
-// 128 channels (KS of them), each set's channel blocks of 16 (KB per set: 4 for D = 64, else
-// 8) held by blocks 0..KB-1 of each half-wave for the broadcast; values D/64 channels per lane
-// (channels lane + 64*hv).
+// Channel geometry of the matrix-core path for head_dim D (64, 128, 192 or 256): keys in sets
+// of up to 128 channels (KS of them), set s's channel blocks of 16 (kb(s): 8, or 4 for a
+// 64-channel set) held by blocks 0..kb(s)-1 of each half-wave for the broadcast; values D/64
+// channels per lane (channels lane + 64*hv).
 template <int D>
 struct Chan {
-  static constexpr int KS = D > 128 ? D / 128 : 1;
-  static constexpr int KB = D >= 128 ? 8 : D / 16;
+  static constexpr int KS = (D + 127) / 128;
+  static constexpr int kb(int s) { return D - 128 * s >= 128 ? 8 : (D - 128 * s) / 16; }
   static constexpr int HV = D / 64;
 };
 
 // One chunk's key data for the lane's token: its code words, and the (scale, zero) pairs of
 // its half's key group (tokens 32*lc .. +31 of the chunk; the same group for both halves when
 // G >= 64) for channels 128*s + 16*la + 4*li .. +3 of each set s (the quad's four lanes hold
-// the block's 16 channels between them; quad_bcast shares them; for D = 64 the blocks la >= 4
-// repeat blocks la - 4, whose operands are never broadcast).
+// the block's 16 channels between them; quad_bcast shares them; in a 64-channel set the
+// blocks la >= 4 repeat blocks la - 4, whose operands are never broadcast).
 template <int BITS, int D>
 struct KeyWords {
   uint32_t w[D * BITS / 32];
@@ -581,9 +456,9 @@ __device__ __forceinline__ void load_key_params(const AttnArgs& a, uint32_t unit
                                                 uint32_t la, uint32_t lc, uint32_t li, KeyParams<D>& kp) {
   // the key group of the half's tokens 64*ch + 32*lc .. +31 (G a multiple of 32)
   const uint32_t grp = (64 * ch + 32 * lc) >> a.gshift;
-  const uint32_t blk = la % Chan<D>::KB;
 #pragma unroll
   for (int ks = 0; ks < Chan<D>::KS; ++ks) {
+    const uint32_t blk = la % Chan<D>::kb(ks);
     const float4* pp = reinterpret_cast<const float4*>(
         a.c.kparams + unit * a.c.geo.kparams_unit() + ((uint64_t)grp * D + 128 * ks + 16 * blk + 4 * li) * 2);
     kp.sz[ks][0] = pp[0];
@@ -616,8 +491,8 @@ __device__ __forceinline__ void load_value_params(const AttnArgs& a, uint32_t un
 
 // Key-side A operands of one chunk: q * scale (already times 2^e) per (head, channel) of the
 // lane's group, split hi/lo, for K-groups of channels 128*s + 16*la + 4k .. +3; bias[h] =
-// sum_d q*zero summed over the blocks of the half (the repeated blocks of D = 64 add 0), times
-// 2^kExp (it enters through an f32 MFMA).
+// sum_d q*zero summed over the blocks of the half (the repeated blocks of a 64-channel set add
+// 0), times 2^kExp (it enters through an f32 MFMA).
 template <int NRS, int D>
 struct KeyA {
   h4 hi[NRS][Chan<D>::KS][4], lo[NRS][Chan<D>::KS][4];
@@ -626,7 +501,7 @@ struct KeyA {
 
 template <int BITS, int NRS, int D>
 __device__ __forceinline__ void key_operands(const KeyParams<D>& kp, const float (&qv)[NRS][Chan<D>::KS][16],
-                                             bool live_block, KeyA<NRS, D>& A) {
+                                             uint32_t la, KeyA<NRS, D>& A) {
   constexpr float kUnit = CodeUnit<BITS>::kExp == 0 ? 1.0f : CodeUnit<BITS>::kExp == -1 ? 0.5f : 0.001953125f;
 #pragma unroll
   for (int rs = 0; rs < NRS; ++rs) {
@@ -640,12 +515,12 @@ __device__ __forceinline__ void key_operands(const KeyParams<D>& kp, const float
         const float sc = quad_bcast(c % 2 ? sz.z : sz.x, c / 4);
         const float zc = quad_bcast(c % 2 ? sz.w : sz.y, c / 4);
         p[c] = qv[rs][ks][c] * sc;
-        bias = fmaf(qv[rs][ks][c], zc, bias);
+        if (la < (uint32_t)Chan<D>::kb(ks)) bias = fmaf(qv[rs][ks][c], zc, bias);
       }
 #pragma unroll
       for (int k = 0; k < 4; ++k) split4(p + 4 * k, A.hi[rs][ks][k], A.lo[rs][ks][k]);
     }
-    A.bias[rs] = sum_over_blocks(live_block ? bias : 0.f) * kUnit;
+    A.bias[rs] = sum_over_blocks(bias) * kUnit;
   }
 }
 
@@ -665,7 +540,7 @@ __device__ __forceinline__ void key_mfma(const KeyWords<BITS, D>& kw, const KeyA
 #pragma unroll
   for (int ks = 0; ks < Chan<D>::KS; ++ks) {
 #pragma unroll
-    for (int a2 = 0; a2 < Chan<D>::KB; ++a2) {
+    for (int a2 = 0; a2 < Chan<D>::kb(ks); ++a2) {
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const int c0 = 128 * ks + 16 * a2 + 4 * k;  // first channel of the K-group
@@ -913,7 +788,7 @@ template <int BITS, int NRS, int CPW, bool MIXED, int D>
 __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uint32_t split,
                                            uint32_t hg, float* lds) {
   static_assert(!MIXED || D == 128, "window / suffix chunks are taken at head_dim 128 only");
-  constexpr int KS = Chan<D>::KS, KB = Chan<D>::KB, HV = Chan<D>::HV;
+  constexpr int KS = Chan<D>::KS, HV = Chan<D>::HV;
   constexpr int ROW = CPW * 64 + kRowPad;  // logits row stride (floats)
   constexpr int NH = 4 * NRS;              // padded heads per unit
   const uint32_t b = unit / a.heads, kvh = unit % a.heads;
@@ -970,7 +845,8 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
     const float s = h < gq ? a.scale2 : 0.f;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      const float* qp = a.query + ((uint64_t)b * a.qh + kvh * gq + min(h, gq - 1)) * D + 128 * ks + 16 * (la % KB);
+      const float* qp =
+          a.query + ((uint64_t)b * a.qh + kvh * gq + min(h, gq - 1)) * D + 128 * ks + 16 * (la % Chan<D>::kb(ks));
 #pragma unroll
       for (int r = 0; r < 16; r += 4) {
         const float4 v = *reinterpret_cast<const float4*>(qp + r);
@@ -1021,7 +897,7 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
     auto step = [&](int k, const KeyWords<BITS, D>& cur, KeyWords<BITS, D>& next) {
       const uint64_t t0 = (uint64_t)chunk_of(k) * 64;
       const bool packed = !MIXED || t0 < kq;
-      if (packed) key_operands<BITS, NRS, D>(kp, qv, la < KB, A);
+      if (packed) key_operands<BITS, NRS, D>(kp, qv, la, A);
       // unconditional (clamped to packed chunks; the last step re-reads an L2-resident chunk)
       if constexpr (CPW > 1) {
         const int32_t kn = std::min(chunk_of(std::min(k + 1, nch - 1)), lastk);
@@ -1232,7 +1108,7 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
 // (4 waves) and the GQA-8 ones into 168 (3 waves) without spills; head_dim 256 at 4/8 bits
 // holds twice the code words and takes two (up to 256 VGPRs).
 constexpr int fast_min_groups(int bits, int nrs, int d) {
-  return d == 256 ? (bits == 2 ? 3 : 2) : (nrs == 1 && bits <= 4) ? 4 : (bits == 8 && nrs == 2) ? 2 : 3;
+  return d > 128 ? (bits == 2 ? 3 : 2) : (nrs == 1 && bits <= 4) ? 4 : (bits == 8 && nrs == 2) ? 2 : 3;
 }
 template <int BITS, int NRS, int D>
 __global__ void __launch_bounds__(kThreads, fast_min_groups(BITS, NRS, D))
@@ -2112,29 +1988,20 @@ uint32_t split_tokens(uint32_t gq) {
   return s;
 }
 
-// Shapes of the matrix-core path: head_dim 64, 128 or 256, G = 32 or a multiple of 64 (a
-// chunk's half-waves then read one key group), GQA up to 32 in head groups (of 8, or 4 at
-// head_dim 256).
+// Shapes of the matrix-core path: head_dim 64, 128, 192 or 256, G = 32 or a multiple of 64 (a
+// chunk's half-waves then read one key group), any GQA, above one row set in head groups (of 8,
+// or 4 above head_dim 128) that each read the chunks.
 bool fast_eligible(const AttnProblem& p) {
   const Geometry& g = p.cache.geo;
   const uint32_t gq = p.qh / p.heads;
-  const bool dim_ok = g.D == 128 || g.D == 64 || g.D == 256;
-  return dim_ok && (g.G == 32 || g.G % 64 == 0) && (g.bits == 2 || g.bits == 4 || g.bits == 8) && gq >= 1 &&
-         gq <= 32;
+  const bool dim_ok = g.D == 64 || g.D == 128 || g.D == 192 || g.D == 256;
+  return dim_ok && (g.G == 32 || g.G % 64 == 0) && (g.bits == 2 || g.bits == 4 || g.bits == 8) && gq >= 1;
 }
 // MFMA row sets (4 heads each) per workgroup, and the head groups of a unit
-int fast_nrs(uint32_t D, uint32_t gq) { return D == 256 || gq <= 4 ? 1 : 2; }
+int fast_nrs(uint32_t D, uint32_t gq) { return D > 128 || gq <= 4 ? 1 : 2; }
 uint32_t head_groups(uint32_t D, uint32_t gq) {
   const uint32_t per = 4u * static_cast<uint32_t>(fast_nrs(D, gq));
   return (gq + per - 1) / per;
-}
-
-// Shapes k_attn_vpack takes (outside the matrix-core path): D a multiple of 64 up to 256, G 32
-// or a multiple of 64, bits 2/4/8.
-bool vpack_eligible(const AttnProblem& p) {
-  const Geometry& g = p.cache.geo;
-  return !fast_eligible(p) && g.D % 64 == 0 && g.D <= 256 && (g.G == 32 || g.G % 64 == 0) &&
-         (g.bits == 2 || g.bits == 4 || g.bits == 8);
 }
 
 // MFMA chunks: [0, floor(vq/64)) (keys and values packed; vq <= kq). Everything after
@@ -2191,27 +2058,6 @@ AttnArgs make_args(const AttnProblem& p, float* ws) {
     const uint64_t rest = a.total - a.t_begin;
     while (a.S > 16 && (uint64_t)p.cache.geo.units * ((rest + a.S - 1) / a.S) < 1024) a.S >>= 1;
   }
-  a.vpack = 0;
-  if (!fast && vpack_eligible(p)) {
-    // packed 64-token blocks [0, floor(min(kq, vq)/64)) to k_attn_vpack, in splits of at least
-    // max(4, gq/2) blocks (partials stay small against the blocks) and ~2048 waves when the
-    // blocks allow; the generic splits take the rest
-    const uint32_t nblk = static_cast<uint32_t>(std::min(p.st.kq, p.st.vq) / 64);
-    if (nblk > 0) {
-      const uint32_t units = p.cache.geo.units;
-      const uint32_t minb = std::max(4u, a.gq / 2);
-      const uint32_t most = std::max(1u, nblk / minb);
-      a.vpack = 1;
-      a.chunk_end = nblk;
-      a.nsplit_fast = std::max(1u, std::min(most, (2048 + units - 1) / units));
-      a.t_begin = (uint64_t)nblk * 64;
-      // the rest is short (the fp32 residual and window, a suffix): shorter splits, down to 16
-      // tokens while the rest would fill fewer than ~1024 workgroups
-      a.S = std::max(32u, a.S / 4);
-      const uint64_t rest = a.total - a.t_begin;
-      while (a.S > 16 && (uint64_t)units * ((rest + a.S - 1) / a.S) < 1024) a.S >>= 1;
-    }
-  }
   a.nsplit_gen = static_cast<uint32_t>((a.total - a.t_begin + a.S - 1) / a.S);
   a.nsplit_total = a.nsplit_fast + a.nsplit_win + a.nsplit_gen;
   a.ws = ws;
@@ -2252,6 +2098,9 @@ hipError_t dispatch_fast(const AttnArgs& a, double bytes, hipStream_t stream) {
     case 6442: return launch_fast<4, 2, 64>(a, bytes, stream);
     case 6481: return launch_fast<8, 1, 64>(a, bytes, stream);
     case 6482: return launch_fast<8, 2, 64>(a, bytes, stream);
+    case 19221: return launch_fast<2, 1, 192>(a, bytes, stream);
+    case 19241: return launch_fast<4, 1, 192>(a, bytes, stream);
+    case 19281: return launch_fast<8, 1, 192>(a, bytes, stream);
     case 25621: return launch_fast<2, 1, 256>(a, bytes, stream);
     case 25641: return launch_fast<4, 1, 256>(a, bytes, stream);
     case 25681: return launch_fast<8, 1, 256>(a, bytes, stream);
@@ -2263,27 +2112,6 @@ hipError_t dispatch_generic(const AttnArgs& a, hipStream_t stream) {
   const size_t lds = ((size_t)a.gq * a.c.geo.D + (size_t)a.gq * a.S) * sizeof(float);
   k_attn_generic<0, 0, 0><<<a.units * a.nsplit_gen, kThreads, lds, stream>>>(a);
   return hipGetLastError();
-}
-
-template <int BITS, bool G32>
-hipError_t launch_vpack(const AttnArgs& a, hipStream_t stream) {
-  const unsigned grid = a.units * a.nsplit_fast;
-  switch (a.gq <= 1 ? 1 : a.gq <= 2 ? 2 : a.gq <= 4 ? 4 : 8) {
-    case 1: k_attn_vpack<BITS, G32, 1><<<grid, 64, 0, stream>>>(a); break;
-    case 2: k_attn_vpack<BITS, G32, 2><<<grid, 64, 0, stream>>>(a); break;
-    case 4: k_attn_vpack<BITS, G32, 4><<<grid, 64, 0, stream>>>(a); break;
-    default: k_attn_vpack<BITS, G32, 8><<<grid, 64, 0, stream>>>(a); break;
-  }
-  return hipGetLastError();
-}
-
-hipError_t dispatch_vpack(const AttnArgs& a, hipStream_t stream) {
-  const bool g32 = a.c.geo.G == 32;
-  switch (a.c.geo.bits) {
-    case 2: return g32 ? launch_vpack<2, true>(a, stream) : launch_vpack<2, false>(a, stream);
-    case 4: return g32 ? launch_vpack<4, true>(a, stream) : launch_vpack<4, false>(a, stream);
-    default: return g32 ? launch_vpack<8, true>(a, stream) : launch_vpack<8, false>(a, stream);
-  }
 }
 
 }  // namespace
@@ -2333,7 +2161,7 @@ hipError_t launch_fill_zero(float* out, size_t n, hipStream_t stream) {
 // 32-channel value groups of one half-wave, once per chunk workgroup: G = 32, one head group.
 bool attention_fuses_decode(const AttnProblem& p) {
   const AttnArgs a = make_args(p, nullptr);
-  return a.total > 0 && !a.vpack && a.nsplit_gen == 0 && (a.nsplit_fast > 0 || a.nsplit_win > 0) &&
+  return a.total > 0 && a.nsplit_gen == 0 && (a.nsplit_fast > 0 || a.nsplit_win > 0) &&
          p.cache.geo.D == 128 && p.cache.geo.G == 32 && a.hgroups == 1;
 }
 
@@ -2356,20 +2184,7 @@ hipError_t launch_attention(const AttnProblem& p, float* workspace, hipStream_t 
   const double kp = kq > t0 ? (double)(kq - t0) : 0.0, vp = vq > t0 ? (double)(vq - t0) : 0.0;
   const double kd = (double)(p.seq - std::max(kq, t0)), vd = (double)(p.seq - std::max(vq, t0));
   const double tail_bytes = units * (kp * key_tok + vp * val_tok + (kd + vd + 2.0 * p.suffix_len) * row);
-  if (a.vpack) {
-    // packed blocks on k_attn_vpack, then the generic splits over the rest
-    const double pk = (double)a.chunk_end * 64;
-    {
-      TimedLaunch timed(KIVI_KERNEL_ATTN_PACKED, stream, units * pk * (key_tok + val_tok) + q_bytes);
-      hipError_t e = dispatch_vpack(a, stream);
-      if (e != hipSuccess) return e;
-    }
-    if (a.nsplit_gen > 0) {
-      TimedLaunch timed(KIVI_KERNEL_ATTN_TAIL, stream, tail_bytes + q_bytes);
-      hipError_t e = dispatch_generic(a, stream);
-      if (e != hipSuccess) return e;
-    }
-  } else if (a.nsplit_fast > 0 || a.nsplit_win > 0) {
+  if (a.nsplit_fast > 0 || a.nsplit_win > 0) {
     // one launch over every chunk (the tokens after the packed chunks as window chunks at
     // head_dim 128, as generic splits in the same grid otherwise): packed tokens at packed
     // cost, the rest as fp32 rows

@@ -95,17 +95,18 @@ def test_streaming_cache_parity(amd, oracle, bits, group, residual, dim, schedul
 
 @pytest.mark.parametrize("dim,group,gqa,bits", [
     (64, 32, 4, 2), (64, 64, 1, 4), (64, 32, 2, 8), (64, 64, 12, 2), (64, 32, 8, 8), (192, 64, 3, 2),
+    (192, 32, 8, 8), (192, 64, 5, 4), (128, 32, 48, 2), (64, 64, 40, 4),
     (256, 32, 4, 4), (256, 128, 2, 8), (256, 64, 8, 8), (256, 32, 4, 2), (256, 64, 8, 2), (256, 128, 3, 2),
     (128, 64, 4, 2), (128, 32, 16, 2), (128, 128, 12, 4), (128, 128, 32, 2), (128, 64, 8, 8),
     (128, 64, 1, 4), (96, 32, 4, 2)])
 def test_other_shapes_attention_parity(amd, oracle, dim, group, gqa, bits):
-    """Shapes beyond head_dim 128 / G 32 / GQA <= 8. head_dim 64, 128 and 256 stay on the
-    matrix-core path: one key group per chunk half when G >= 64, query heads in groups of 8
-    (4 at head_dim 256) with a short last group, and at head_dim 64/256 only the fully packed
-    chunks there, the rest on the generic splits in the same launch. head_dim 192 goes to the
-    wave-per-split kernel (heads in passes of up to 8, the extra heads of a last pass dropped)
-    and the generic splits; head_dim 96 stays on the generic splits alone. Many splits,
-    against the oracle and f64 dense attention on the dequantized cache."""
+    """Shapes beyond head_dim 128 / G 32 / GQA <= 8. head_dim 64, 128, 192 and 256 stay on the
+    matrix-core path: one key group per chunk half when G >= 64 (a 64-channel key set uses
+    four of the eight broadcast blocks), query heads in groups of 8 (4 above head_dim 128)
+    with a short last group, and at head_dims other than 128 only the fully packed chunks
+    there, the rest on the generic splits in the same launch. head_dim 96 stays on the
+    generic splits alone. Many splits, against the oracle and f64 dense attention on the
+    dequantized cache."""
     batch, heads = 2, 2
     seq = 2500 + 13 * bits
     rng = np.random.default_rng(dim + group + gqa + bits)
