@@ -826,6 +826,14 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
     load_key_params<D>(a, unit, k0, la, lc, li, kp);
     load_key_words<BITS, D>(a, unit, k0, lane, kw0);
   }
+  // MIXED (one chunk, tw): its fp32 key rows are requested with the packed data, and its fp32
+  // value rows as soon as the logits are done, so the workgroup's memory round trips overlap
+  // (these workgroups are on the critical path of short launches such as a decode step)
+  const uint64_t tw = (uint64_t)chunk_of(0) * 64;
+  const bool key_rows = MIXED && nch > 0 && tw + 64 > kq && tw < total;
+  const bool value_rows = MIXED && nch > 0 && tw + 16 * quarter + 16 > vq && tw + 16 * quarter < total;
+  KeyRows krw;
+  ValueRows vrw;
 
   // a decode token appended by this launch evicts token vq-1 from the window: its row
   EvictRow er{};
@@ -911,10 +919,9 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
         for (int i = 0; i < 4; ++i) lg[rs][i] = 0.f;
       if (packed) key_mfma<BITS, NRS, D>(cur, A, lg);
       if constexpr (MIXED) {
-        if (t0 + 64 > kq && t0 < total) {
-          KeyRows kr;  // one round of loads: the quarter's rows, four lanes per row
-          load_key_rows(a, unit, t0, quarter, lane, kr);
-          key_fp32<NRS>(a, t0, quarter, lane, qv, kr, kUnit, lg);
+        if (key_rows) {  // t0 == tw
+          load_key_rows(a, unit, tw, quarter, lane, krw);
+          key_fp32<NRS>(a, t0, quarter, lane, qv, krw, kUnit, lg);
         }
       }
       const bool live = !MIXED || (t0 + lane < total && lane / 16 == quarter);
@@ -933,6 +940,9 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
     }
   }
   // wave max per head; each lane keeps the max of its own MFMA row (true base-2 units)
+  if constexpr (MIXED) {
+    if (value_rows) load_value_rows(a, unit, tw, quarter, lane, vrw);
+  }
   float mrow[NRS];
 #pragma unroll
   for (int rs = 0; rs < NRS; ++rs) {
@@ -1031,11 +1041,7 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
       }
       if (packed) value_mfma<BITS, NRS, D>(cur, A, vacc);
       if constexpr (MIXED) {
-        if (t0 + 16 * quarter + 16 > vq && t0 + 16 * quarter < total) {
-          ValueRows vr;
-          load_value_rows(a, unit, t0, quarter, lane, vr);
-          value_fp32<NRS>(a, t0, quarter, la, wl + li * ROW, moff, kout, vfac * kUnit, vr, vacc);
-        }
+        if (value_rows) value_fp32<NRS>(a, t0, quarter, la, wl + li * ROW, moff, kout, vfac * kUnit, vrw, vacc);
       }
     };
     if (nch > 0) {
