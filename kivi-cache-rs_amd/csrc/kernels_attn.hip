@@ -37,6 +37,12 @@
 #include <mutex>
 
 namespace kivi {
+
+// 1.0 that the compiler cannot fold (external linkage, and constant memory is initialised from
+// the host): x * kUnit - hi stays an fma with an f32 and an f16 source, one mixed-precision
+// instruction (lo_pair).
+__constant__ float kUnit = 1.0f;
+
 namespace {
 
 constexpr int kThreads = 256;
@@ -373,14 +379,28 @@ __device__ __forceinline__ h4 codes4(uint32_t w, int k) {
   }
 }
 
-// x = hi + lo with hi = f16(x) rounded toward zero and lo = f16(x - hi) (x - hi is exact in
-// f32): 22 significant bits in two f16 operands, two values per packed conversion (x must be
-// below 2^15 in magnitude; the callers scale their operands by a power of two).
+// The lo halves of two values x, y whose f16 hi halves are the packed pair `hi`:
+// (f16(x - hi.x), f16(y - hi.y)), each rounded to nearest from the exact difference: two
+// mixed-precision fmas and one packed conversion, in place of two conversions back to f32, two
+// subtractions and the packed conversion.
+__device__ __forceinline__ uint32_t lo_pair(float x, float y, uint32_t hi) {
+  const h2 h = __builtin_bit_cast(h2, hi);
+  const float one = kUnit;
+  h2 l;
+  l.x = static_cast<_Float16>(__builtin_fmaf(x, one, -static_cast<float>(h.x)));
+  l.y = static_cast<_Float16>(__builtin_fmaf(y, one, -static_cast<float>(h.y)));
+  return __builtin_bit_cast(uint32_t, l);
+}
+
+// x = hi + lo with hi = f16(x) rounded toward zero and lo = f16(x - hi) rounded to nearest:
+// 22 significant bits in two f16 operands, two values per packed conversion (x must be below
+// 2^15 in magnitude; the callers scale their operands by a power of two).
 __device__ __forceinline__ void split4(const float* x, h4& hi, h4& lo) {
-  const h2 h01 = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(x[0], x[1]));
-  const h2 h23 = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(x[2], x[3]));
-  const h2 l01 = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(x[0] - (float)h01.x, x[1] - (float)h01.y));
-  const h2 l23 = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(x[2] - (float)h23.x, x[3] - (float)h23.y));
+  const uint32_t w01 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(x[0], x[1]));
+  const uint32_t w23 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(x[2], x[3]));
+  const h2 h01 = __builtin_bit_cast(h2, w01), h23 = __builtin_bit_cast(h2, w23);
+  const h2 l01 = __builtin_bit_cast(h2, lo_pair(x[0], x[1], w01));
+  const h2 l23 = __builtin_bit_cast(h2, lo_pair(x[2], x[3], w23));
   hi = h4{h01.x, h01.y, h23.x, h23.y};
   lo = h4{l01.x, l01.y, l23.x, l23.y};
 }
@@ -1166,7 +1186,7 @@ constexpr int kSessCpw = 4;
 // suffix chunk of one session; the rest one packed-chunk split of a unit, for every session
 // in turn (the split's chunks are re-read from L2, not HBM, after the first session).
 template <int BITS, int NRS>
-__global__ void __launch_bounds__(kThreads) k_attn_sessions(AttnArgs a, SessionTable t) {
+__global__ void __launch_bounds__(kThreads, BITS == 2 && NRS == 1 ? 3 : 2) k_attn_sessions(AttnArgs a, SessionTable t) {
   extern __shared__ float lds[];
   const uint32_t per_sess = a.units * a.nsplit_win;
   const uint32_t nwin = a.nsess * per_sess;
@@ -1483,21 +1503,22 @@ constexpr uint32_t kShVRow = 64 + 8;   // V^T LDS row (one channel) stride in ha
 constexpr uint32_t kShBufHalves = 2 * 64 * kShKRow + 2 * 128 * kShVRow;  // khi, klo, vhi, vlo
 constexpr uint32_t kShParamFloats = 1024;  // keys [2 groups][128][2], values [4 groups][64][2]
 constexpr size_t kShLdsBytes = 2 * (size_t)kShBufHalves * sizeof(_Float16) + 2 * kShParamFloats * sizeof(float);
-constexpr float kShPScale = 16384.f;   // P operands are p * 2^14 (p <= 1)
+// P operands are p * 2^kShPExp with p <= 2^kShSlack (below 2^14); the f16 subnormal floor of
+// the lo halves then costs at most 2^-(kShPExp + 25) per token against a row sum l >= 1.
+constexpr float kShSlack = 6.f;
+constexpr float kShPExp = 8.f;
+constexpr float kShPScale = 256.f;  // 2^kShPExp
+static_assert(kShSlack + kShPExp <= 14.f, "P operands stay below 2^14");
 constexpr uint32_t kShOutRow = 128 + 4;  // partial row (acc[128], m, l) in LDS, 16 B aligned
 static_assert((size_t)kShRows * kShOutRow * sizeof(float) <= kShLdsBytes, "partials fit the chunk buffers");
 
 typedef uint32_t ux4 __attribute__((ext_vector_type(4)));
 
-// hi + lo f16 pairs of two floats (hi rounded toward zero: lo = x - hi is exact in f32, and
-// hi + lo keeps ~22 significant bits whatever the rounding of hi).
-// Returns (hi pair, lo pair).
+// hi + lo f16 pairs of two floats (hi rounded toward zero, lo = f16(x - hi) rounded to
+// nearest: ~22 significant bits). Returns (hi pair, lo pair).
 __device__ __forceinline__ uint2 split2(float x, float y) {
-  typedef _Float16 hh2 __attribute__((ext_vector_type(2)));
-  const hh2 h = __builtin_bit_cast(hh2, __builtin_amdgcn_cvt_pkrtz(x, y));
-  return make_uint2(__builtin_bit_cast(uint32_t, h),
-                    __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(x - static_cast<float>(h[0]),
-                                                                            y - static_cast<float>(h[1]))));
+  const uint32_t h = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(x, y));
+  return make_uint2(h, lo_pair(x, y, h));
 }
 
 __device__ __forceinline__ fx16 mfma32(const hx8& a, const hx8& b, const fx16& c) {
@@ -1704,23 +1725,27 @@ __device__ __forceinline__ void shared_mix(const _Float16* buf, fx16 s0, fx16 s1
   }
   const _Float16* vhi = buf + 2 * 64 * kShKRow;
   const _Float16* vlo = vhi + 128 * kShVRow;
-  // online softmax over the chunk (the lane pair r, r + 32 holds the row's 64 logits); the
-  // probabilities come out as p * 2^14 (the P operand range), and so does l
+  // online softmax over the chunk (the lane pair r, r + 32 holds the row's 64 logits) against
+  // a reference maximum m that moves only when a row's chunk maximum exceeds it by more than
+  // kShSlack: then every row of the wave takes max(m, chunk maximum) and rescales what it has
+  // summed. The probabilities p = 2^(x - m) <= 2^kShSlack come out as p * kShPScale (the P
+  // operand range), and so does l.
   float mx = -INFINITY;
 #pragma unroll
   for (int v = 0; v < 16; ++v) mx = fmaxf(mx, fmaxf(s0[v], s1[v]));
   mx = fmaxf(mx, __shfl_xor(mx, 32));
-  const float mnew = fmaxf(m, mx * s_unscale);
-  const float alpha = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mnew);
-  m = mnew;
-  const float off = 14.f - mnew;
-  if (__ballot(alpha != 1.f)) {
+  const float cm = mx * s_unscale;
+  if (__ballot(cm > m + kShSlack)) {  // wave-uniform
+    const float mnew = fmaxf(m, cm);
+    const float alpha = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mnew);
+    m = mnew;
     l *= alpha;
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
       for (int v = 0; v < 16; ++v) o[mt][v] *= alpha;
   }
+  const float off = kShPExp - m;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     // P^T K-step j: tokens 16j .. 16j + 15 = tile j/2, values 8(j%2) .. 8(j%2) + 7
@@ -1892,7 +1917,7 @@ __device__ __forceinline__ void shared_split(const AttnArgs& a, uint32_t unit, u
   const int ev = range_exp(__uint_as_float(a.c.smax[4 * unit + 3]));
   const float kf = ldexpf(1.f, ek), vf = ldexpf(1.f, ev);
   const float s_unscale = ldexpf(1.f, -ek - eq);
-  const float o_unscale = ldexpf(1.f, -ev) / kShPScale;  // O and l carry the 2^14 of P
+  const float o_unscale = ldexpf(1.f, -ev) / kShPScale;  // O and l carry the P operand scale
 
   // contiguous chunk ranges over [0, gemm_end); chunks from chunk_end on hold fp32 rows
   const uint32_t cps = (a.gemm_end + a.nsplit_fast - 1) / a.nsplit_fast;
