@@ -39,9 +39,9 @@
 namespace kivi {
 
 // 1.0 that the compiler cannot fold (external linkage, and constant memory is initialised from
-// the host): x * kUnit - hi stays an fma with an f32 and an f16 source, one mixed-precision
+// the host): x * kMixOne - hi stays an fma with an f32 and an f16 source, one mixed-precision
 // instruction (lo_pair).
-__constant__ float kUnit = 1.0f;
+__constant__ float kMixOne = 1.0f;
 
 namespace {
 
@@ -385,7 +385,7 @@ __device__ __forceinline__ h4 codes4(uint32_t w, int k) {
 // subtractions and the packed conversion.
 __device__ __forceinline__ uint32_t lo_pair(float x, float y, uint32_t hi) {
   const h2 h = __builtin_bit_cast(h2, hi);
-  const float one = kUnit;
+  const float one = kMixOne;
   h2 l;
   l.x = static_cast<_Float16>(__builtin_fmaf(x, one, -static_cast<float>(h.x)));
   l.y = static_cast<_Float16>(__builtin_fmaf(y, one, -static_cast<float>(h.y)));
