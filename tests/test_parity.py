@@ -378,6 +378,45 @@ def test_batched_sessions_kernel_parity(amd, oracle, bits, batch, qh, n_sess, do
     assert_close(few, got[per:3 * per], "sessions 1..2 alone")
 
 
+@pytest.mark.parametrize("bits", [2, 8])
+def test_shared_prefix_rising_logits_parity(amd, oracle, bits):
+    """Batched sessions in the GEMM form over a prefix whose logits climb by ~2 (base 2) per
+    64-token chunk in a 12-chunk sawtooth: each workgroup's ~10-chunk range sees its running
+    maximum rise past the lazy-rescale slack several times, so the rescale of the accumulated
+    rows runs repeatedly. Every session against the oracle's RagSession::attention
+    (src/prefix.rs:223-289)."""
+    heads, dim, qh, doc, n_sess = 8, 128, 32, 20480, 4
+    rng = np.random.default_rng(4100 + bits)
+    u = np.where(rng.random((heads, dim)) < 0.5, -1.0, 1.0).astype(np.float32)  # q.u = 128
+    ramp = (0.1227 * ((np.arange(doc) // 64) % 12)).astype(np.float32)            # ~2 per chunk
+    k = rng.standard_normal((1, heads, doc, dim)).astype(np.float32)
+    k += ramp[None, None, :, None] * u[None, :, None, :]
+    v = rng.standard_normal((1, heads, doc, dim)).astype(np.float32)
+    cfg = KiviConfig(bits, 32, 128)
+    ca, co = KiviCache(amd, cfg, 1, heads, dim), KiviCache(oracle, cfg, 1, heads, dim)
+    ca.append(k.reshape(-1), v.reshape(-1), doc)
+    co.append(k.reshape(-1), v.reshape(-1), doc)
+    pa, po = ca.share_prefix(), co.share_prefix()
+    sa = [pa.session() for _ in range(n_sess)]
+    so = [po.session() for _ in range(n_sess)]
+    lens = (0, 64, 97, 1)
+    for a, o, n in zip(sa, so, lens):
+        if n:
+            sk = rng.standard_normal(heads * n * dim).astype(np.float32)
+            sv = rng.standard_normal(heads * n * dim).astype(np.float32)
+            a.append(sk, sv, n)
+            o.append(sk, sv, n)
+    # queries along each KV head's ramp direction, plus noise
+    q = np.repeat(u, qh // heads, axis=0)[None] + 0.3 * rng.standard_normal((n_sess, qh, dim))
+    qs = q.astype(np.float32).reshape(-1)
+    per = qh * dim
+    scale = np.float32(1 / np.sqrt(128))
+    got = kivi.sessions_attention(amd, sa, qs, qh, scale)
+    for i, o in enumerate(so):
+        assert_close(got[i * per:(i + 1) * per], o.attention(qs[i * per:(i + 1) * per], qh, scale),
+                     f"session {i} (suffix {lens[i]})")
+
+
 def test_runtime_decode_parity(amd, oracle):
     """512-step streaming decode shape of config 1, scaled down: prefill, then decode steps
     crossing key flushes and window evictions, compared with the oracle each step."""
