@@ -10,14 +10,20 @@ and one of three workloads:
   session attention against each session's oracle attention (src/prefix.rs:228-289), at the
   shapes the batched kernels take (head_dim 128, G 32);
 - RuntimeKv prefill then up to 2R+2 decode steps, crossing key flushes and window
-  evictions (src/runtime.rs:33-56, tests/runtime.rs:13-52).
+  evictions (src/runtime.rs:33-56, tests/runtime.rs:13-52); every other such case decodes on
+  device pointers, where a step without a key flush is one attention launch carrying the
+  append and the eviction.
+One cache case in four also runs the allocation-free attention entry point and requires it
+to equal the allocating one bit for bit (or to refuse with Capacity when the call's split
+partials exceed its static workspace).
 """
 
 import numpy as np
 import pytest
 
 import kivi
-from kivi import KiviCache, KiviConfig, RuntimeKv
+from kivi import KiviCache, KiviConfig, KiviError, RuntimeKv
+from helpers import DeviceArrays
 from test_parity import assert_close, assert_same_state, assert_streams_equal
 
 pytestmark = pytest.mark.gpu
@@ -52,11 +58,21 @@ def test_random_shapes_match_oracle(amd, oracle, seed):
         v = rng.standard_normal(B * H * n * D).astype(np.float32)
         ra.prefill(k, v, n)
         ro.prefill(k, v, n)
+        on_device = seed % 8 == 7
+        mem = DeviceArrays()
+        n_kv, n_q = B * H * D, B * qh * D
+        out = mem.empty(n_q)
         for s in range(int(rng.integers(1, 2 * cfg.residual_length + 3))):
-            kk = rng.standard_normal(B * H * D).astype(np.float32)
-            vv = rng.standard_normal(B * H * D).astype(np.float32)
-            q = rng.standard_normal(B * qh * D).astype(np.float32)
-            assert_close(ra.decode(kk, vv, q, qh, scale), ro.decode(kk, vv, q, qh, scale), f"step {s}")
+            kk = rng.standard_normal(n_kv).astype(np.float32)
+            vv = rng.standard_normal(n_kv).astype(np.float32)
+            q = rng.standard_normal(n_q).astype(np.float32)
+            if on_device:
+                ra.decode_device(mem.upload(kk), n_kv, mem.upload(vv), n_kv, mem.upload(q), n_q, qh, scale, out, n_q)
+                got = mem.download(out, n_q)
+            else:
+                got = ra.decode(kk, vv, q, qh, scale)
+            assert_close(got, ro.decode(kk, vv, q, qh, scale), f"step {s}")
+        mem.free()
         assert_same_state(ra.cache(), ro.cache())
         assert_streams_equal(ra.cache(), ro.cache())
         return
@@ -72,7 +88,23 @@ def test_random_shapes_match_oracle(amd, oracle, seed):
     assert_streams_equal(ca, co)
     if kind == "cache":
         q = rng.standard_normal(B * qh * D).astype(np.float32)
-        assert_close(ca.attention(q, qh, scale), co.attention(q, qh, scale))
+        got = ca.attention(q, qh, scale)
+        assert_close(got, co.attention(q, qh, scale))
+        if seed % 8 == 1 and ca.sequence_length() > 0:
+            mem = DeviceArrays()
+            dq, out_a, out_b = mem.upload(q), mem.empty(q.size), mem.empty(q.size)
+            ca.attention_device(dq, q.size, qh, scale, out_a, q.size)
+            try:
+                ca.attention_device_noalloc(dq, q.size, qh, scale, out_b, q.size)
+                refused = False
+            except KiviError as e:
+                assert e.variant == "Capacity"
+                refused = True
+            a, b = mem.download(out_a, q.size), mem.download(out_b, q.size)
+            mem.free()
+            if not refused:
+                assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+            assert np.array_equal(a.view(np.uint32), got.view(np.uint32))
         return
     pa, po = ca.share_prefix(), co.share_prefix()
     ns = int(rng.integers(1, 21))
