@@ -1210,9 +1210,25 @@ __global__ void __launch_bounds__(kThreads, BITS == 2 && NRS == 1 ? 3 : 2) k_att
 // Session suffixes of the shared-prefix form (fp32 rows, head_dim 128, GQA <= 8): one
 // workgroup per (session, unit, run of kSufTokens suffix tokens) writes one partial per head
 // into split nsplit_fast + run (runs past a session's suffix write empty partials). Keys: lane
-// pair (l, l + 32) of wave w owns token 32w + l%32, 64 channels each; values: lane l owns
-// channels 2l, 2l+1 of wave w's 32 tokens, and the four waves' sums meet in LDS. Every key and
-// value load of a workgroup is issued before the softmax.
+// pair (l, l + 32) of wave w owns token 32w + l%32, 64 channels each; values: half-wave h of
+// wave w owns rows 32w + 2j + h (j < 16), lane l channels 4 (l % 32) .. + 3, and the eight
+// half-waves' sums meet in LDS. Every load of a workgroup is issued before the first wait.
+// Raw buffer resource over `floats` floats at p (stride 0, 32-bit data format): loads at byte
+// offsets past the range return zeros.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const float* p, uint32_t floats) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p), 0, static_cast<int>(floats * 4), 0x00020000);
+}
+__device__ __forceinline__ float4 rsrc_load4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  using u4 = uint32_t __attribute__((ext_vector_type(4)));
+  const u4 x = __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0);
+  return make_float4(__uint_as_float(x.x), __uint_as_float(x.y), __uint_as_float(x.z), __uint_as_float(x.w));
+}
+__device__ __forceinline__ float2 rsrc_load2(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  using u2 = uint32_t __attribute__((ext_vector_type(2)));
+  const u2 x = __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, 0);
+  return make_float2(__uint_as_float(x.x), __uint_as_float(x.y));
+}
+
 constexpr uint32_t kSufTokens = 128;
 constexpr uint32_t kSufMaxHeads = 8;
 
@@ -1221,7 +1237,7 @@ __global__ void __launch_bounds__(kThreads) k_attn_suffix(AttnArgs a, SessionTab
   __shared__ float qs[kSufMaxHeads][D];
   __shared__ float sp[kSufMaxHeads][kSufTokens];
   __shared__ float ml[kSufMaxHeads][2];
-  __shared__ float red[4][kSufMaxHeads][D];
+  __shared__ float red[4][2][kSufMaxHeads][D];  // [wave][half-wave][head][channel]
   const uint32_t lane = threadIdx.x % 64, wave = threadIdx.x / 64;
   const uint32_t gq = a.gq;
   const uint32_t per_sess = a.units * a.nsplit_win;
@@ -1244,21 +1260,35 @@ __global__ void __launch_bounds__(kThreads) k_attn_suffix(AttnArgs a, SessionTab
     }
     return;
   }
-  // queries in base-2 logit units
+  // Loads in the order they are used, all issued before the first wait: the queries (four
+  // floats per thread: gq * D <= 4 * kThreads), this wave's keys (half a row per lane), its
+  // values (two channels per lane). The dot products then start as the keys arrive, while the
+  // values are still on their way.
+  static_assert(kSufMaxHeads * D == 4 * kThreads, "one float4 of queries per thread");
   const float* qp = a.query + (uint64_t)sess * a.q_sess_stride + ((uint64_t)b * a.qh + kvh * gq) * D;
-  for (uint32_t i = threadIdx.x; i < gq * D; i += blockDim.x) qs[i / D][i % D] = qp[i] * a.scale2;
-  // this wave's tokens: keys (half a row per lane) and values (two channels per lane)
+  const bool qlive = 4 * threadIdx.x < gq * D;
+  const float4 q4 = reinterpret_cast<const float4*>(qp)[qlive ? threadIdx.x : 0];
+  __builtin_amdgcn_sched_barrier(0);
+  // The run's rows through buffer resources of n rows: a row past n reads as zeros (its weight
+  // is 0) without a memory request and without a branch around the load.
   const uint32_t tk = 32 * wave + lane % 32, hh = lane / 32;
-  const float* krow = d.k + unit * d.stride + (t0 + (tk < n ? tk : 0)) * D + 64 * hh;
+  const __amdgpu_buffer_rsrc_t krs = rows_rsrc(d.k + unit * d.stride + t0 * D, n * D);
   float4 kv[16];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) kv[i] = reinterpret_cast<const float4*>(krow)[i];
-  float2 vv[32];
-  const float* vbase = d.v + unit * d.stride + t0 * D + 2 * lane;
+  for (int i = 0; i < 16; ++i) kv[i] = rsrc_load4(krs, (tk * D + 64 * hh + 4 * i) * 4);
+  __builtin_amdgcn_sched_barrier(0);
+  const __amdgpu_buffer_rsrc_t vrs = rows_rsrc(d.v + unit * d.stride + t0 * D, n * D);
+  float4 vv[16];  // row 32w + 2j + hh, channels 4 (l % 32) .. + 3
 #pragma unroll
-  for (int j = 0; j < 32; ++j) {
-    const uint32_t tv = 32 * wave + j;
-    vv[j] = *reinterpret_cast<const float2*>(vbase + (uint64_t)(tv < n ? tv : 0) * D);
+  for (int j = 0; j < 16; ++j) vv[j] = rsrc_load4(vrs, ((32 * wave + 2 * j + hh) * D + 4 * (lane % 32)) * 4);
+  __builtin_amdgcn_sched_barrier(0);
+  // queries in base-2 logit units
+  if (qlive) {
+    float* qd = &qs[0][0] + 4 * threadIdx.x;
+    qd[0] = q4.x * a.scale2;
+    qd[1] = q4.y * a.scale2;
+    qd[2] = q4.z * a.scale2;
+    qd[3] = q4.w * a.scale2;
   }
   __syncthreads();  // queries in LDS
   float dot[kSufMaxHeads];
@@ -1303,32 +1333,37 @@ __global__ void __launch_bounds__(kThreads) k_attn_suffix(AttnArgs a, SessionTab
     }
   }
   __syncthreads();
-  // value sums of this wave's tokens
-  float2 acc[kSufMaxHeads];
+  // value sums of this half-wave's 16 rows
+  float4 acc[kSufMaxHeads];
 #pragma unroll
-  for (uint32_t h = 0; h < kSufMaxHeads; ++h) acc[h] = make_float2(0.f, 0.f);
+  for (uint32_t h = 0; h < kSufMaxHeads; ++h) acc[h] = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-  for (int j = 0; j < 32; ++j) {
+  for (int j = 0; j < 16; ++j) {
 #pragma unroll
     for (uint32_t h = 0; h < kSufMaxHeads; ++h) {
       if (h < gq) {
-        const float p = sp[h][32 * wave + j];  // 0 for tokens past n
+        const float p = sp[h][32 * wave + 2 * j + hh];  // 0 for tokens past n
         acc[h].x = fmaf(p, vv[j].x, acc[h].x);
         acc[h].y = fmaf(p, vv[j].y, acc[h].y);
+        acc[h].z = fmaf(p, vv[j].z, acc[h].z);
+        acc[h].w = fmaf(p, vv[j].w, acc[h].w);
       }
     }
   }
 #pragma unroll
   for (uint32_t h = 0; h < kSufMaxHeads; ++h)
-    if (h < gq) *reinterpret_cast<float2*>(&red[wave][h][2 * lane]) = acc[h];
+    if (h < gq) *reinterpret_cast<float4*>(&red[wave][hh][h][4 * (lane % 32)]) = acc[h];
   __syncthreads();
   for (uint32_t h = wave; h < gq; h += 4) {
     float2 o = make_float2(0.f, 0.f);
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-      const float2 x = *reinterpret_cast<const float2*>(&red[w][h][2 * lane]);
-      o.x += x.x;
-      o.y += x.y;
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const float2 x = *reinterpret_cast<const float2*>(&red[w][half][h][2 * lane]);
+        o.x += x.x;
+        o.y += x.y;
+      }
     }
     float* part = a.ws + (uint64_t)sess * a.ws_sess_stride +
                   (((uint64_t)unit * a.nsplit_total + a.nsplit_fast + run) * gq + h) * (D + 2);
