@@ -378,6 +378,40 @@ def test_batched_sessions_kernel_parity(amd, oracle, bits, batch, qh, n_sess, do
     assert_close(few, got[per:3 * per], "sessions 1..2 alone")
 
 
+def test_session_suffix_run_boundaries_parity(amd, oracle):
+    """GEMM form (8 sessions x 4 heads = 32 rows) with suffixes on both sides of the
+    128-token runs of the suffix kernel, grown by several appends so that each session's
+    device capacity exceeds its length (src/prefix.rs:173-223, 228-289)."""
+    batch, heads, qh, dim, doc = 1, 8, 32, 128, 700
+    rng = np.random.default_rng(4242)
+    k = rng.standard_normal(batch * heads * doc * dim).astype(np.float32)
+    v = rng.standard_normal(batch * heads * doc * dim).astype(np.float32)
+    cfg = KiviConfig(2, 32, 128)
+    ca, co = KiviCache(amd, cfg, batch, heads, dim), KiviCache(oracle, cfg, batch, heads, dim)
+    ca.append(k, v, doc)
+    co.append(k, v, doc)
+    pa, po = ca.share_prefix(), co.share_prefix()
+    lens = (127, 128, 129, 255, 256, 257, 383, 2)
+    sa, so = [pa.session() for _ in lens], [po.session() for _ in lens]
+    for a, o, n in zip(sa, so, lens):
+        done = 0
+        for piece in (n // 3, n - n // 3 - 1, 1):
+            if piece:
+                sk = (rng.standard_normal(batch * heads * piece * dim) * 1.5).astype(np.float32)
+                sv = rng.standard_normal(batch * heads * piece * dim).astype(np.float32)
+                a.append(sk, sv, piece)
+                o.append(sk, sv, piece)
+                done += piece
+        assert done == n
+    per = batch * qh * dim
+    qs = rng.standard_normal(len(lens) * per).astype(np.float32)
+    scale = np.float32(1 / np.sqrt(dim))
+    got = kivi.sessions_attention(amd, sa, qs, qh, scale)
+    for i, o in enumerate(so):
+        assert_close(got[i * per:(i + 1) * per], o.attention(qs[i * per:(i + 1) * per], qh, scale),
+                     f"session {i} (suffix {lens[i]})")
+
+
 @pytest.mark.parametrize("bits", [2, 8])
 def test_shared_prefix_rising_logits_parity(amd, oracle, bits):
     """Batched sessions in the GEMM form over a prefix whose logits climb by ~2 (base 2) per
