@@ -1379,9 +1379,11 @@ __global__ void __launch_bounds__(kThreads) k_attn_suffix(AttnArgs a, SessionTab
 // `parts` waves (2 or 4) that take every parts-th split and meet in LDS. Lane l owns channels
 // l, l + 64, ... (CPL of them); the splits' (m, l) are wave-uniform loads, so each weight
 // exp2(m - max) is computed once per wave, not once per channel. Loads go out in rounds of
-// kMergeBatch / CPL splits, all independent.
+// BATCH / CPL splits, all independent.
 constexpr uint32_t kMergeThreads = 256;  // 4 waves
-constexpr uint32_t kMergeBatch = 32;     // loads per lane in flight per round
+constexpr uint32_t kMergeBatchSmall = 32;  // loads per lane in flight per round: 16 splits at CPL 2
+constexpr uint32_t kMergeBatchLarge = 48;  // 24 splits at CPL 2
+constexpr uint32_t kMergeFewRows = 256;    // below this many rows the merge is latency-bound
 
 // Rows of a decode token the attention launch consumed from its inputs, written to the key
 // residual and the value window once that launch is over (null k: nothing to write).
@@ -1393,12 +1395,12 @@ struct PendRows {
   uint32_t kslot, vslot, R;
 };
 
-template <int CPL>
+template <int CPL, uint32_t BATCH>
 __global__ void __launch_bounds__(kMergeThreads)
     k_attn_merge(const float* ws, uint32_t nsplit, uint32_t parts, uint32_t gq, uint32_t D, uint32_t heads,
                  uint32_t qh, float* out, uint32_t units, uint32_t rows, uint64_t ws_sess_stride,
                  uint64_t out_sess_stride, PendRows pend) {
-  constexpr uint32_t SB = kMergeBatch / CPL;
+  constexpr uint32_t SB = BATCH / CPL;
   __shared__ float xch[4][2 + 64 * CPL];  // per wave: (m, l), then the channel sums
   const uint32_t lane = threadIdx.x % 64;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
@@ -1486,21 +1488,28 @@ __global__ void __launch_bounds__(kMergeThreads)
   }
 }
 
-// Merge launch for `count` sessions of `units` units: parts per row so that a wave takes about
-// one round of loads.
+// Merge launch for `count` sessions of `units` units. Few rows (a latency-bound launch): four
+// waves per row. Otherwise as few waves per row as one round of loads each allows (fewer
+// waves and LDS exchanges for the same bytes).
 hipError_t launch_merge(const float* ws, uint32_t nsplit, uint32_t gq, uint32_t D, uint32_t heads,
                         uint32_t qh, float* out, uint32_t units, uint32_t count,
                         uint64_t ws_sess_stride, uint64_t out_sess_stride, hipStream_t stream,
                         PendRows pend = PendRows{}) {
   const uint32_t cpl = D <= 64 ? 1 : D <= 128 ? 2 : D <= 256 ? 4 : D <= 512 ? 8 : 16;
-  const uint32_t sb = kMergeBatch / cpl;
+  const uint32_t rows = count * units * gq;
+  const uint32_t sb = (rows < kMergeFewRows ? kMergeBatchSmall : kMergeBatchLarge) / cpl;
   const uint32_t want = (nsplit + sb - 1) / sb;
   const uint32_t parts = want <= 1 ? 1 : want <= 2 ? 2 : 4;
-  const uint32_t rows = count * units * gq;
+  // the smaller round when it holds a wave's splits (fewer padded loads), else the larger
+  const bool small = (nsplit + parts - 1) / parts <= kMergeBatchSmall / cpl;
   const uint32_t grid = (rows * parts + 3) / 4;
-#define KIVI_MERGE(C)                                                                                        \
-  k_attn_merge<C><<<grid, kMergeThreads, 0, stream>>>(ws, nsplit, parts, gq, D, heads, qh, out, units, rows, \
-                                                      ws_sess_stride, out_sess_stride, pend)
+#define KIVI_MERGE(C)                                                                          \
+  if (small)                                                                                   \
+    k_attn_merge<C, kMergeBatchSmall><<<grid, kMergeThreads, 0, stream>>>(                     \
+        ws, nsplit, parts, gq, D, heads, qh, out, units, rows, ws_sess_stride, out_sess_stride, pend); \
+  else                                                                                         \
+    k_attn_merge<C, kMergeBatchLarge><<<grid, kMergeThreads, 0, stream>>>(                     \
+        ws, nsplit, parts, gq, D, heads, qh, out, units, rows, ws_sess_stride, out_sess_stride, pend)
   switch (cpl) {
     case 1: KIVI_MERGE(1); break;
     case 2: KIVI_MERGE(2); break;
