@@ -205,6 +205,26 @@ def test_attention_parity_many_rounds(amd, oracle, bits, gqa, batch, heads, seq)
     assert_close(a.attention(q, heads * gqa, scale), o.attention(q, heads * gqa, scale))
 
 
+@pytest.mark.parametrize("bits,qh,seq", [(2, 8, 65536), (4, 2, 98304)])
+def test_merge_several_rounds_parity(amd, oracle, bits, qh, seq):
+    """head_dim 32 (generic splits only) over 65-98k tokens of one unit: hundreds of splits per
+    output row, so each of the merge's four waves per row takes its splits in several rounds
+    of its larger batch (src/attention.rs:18-105 over one long head)."""
+    dim, heads = 32, 1
+    rng = np.random.default_rng(bits * 7 + qh)
+    n = heads * seq * dim
+    k = rng.standard_normal(n, dtype=np.float32)
+    k.reshape(heads, seq, dim)[:, :, 5] *= np.float32(10.0)
+    v = rng.standard_normal(n, dtype=np.float32)
+    cfg = KiviConfig(bits, 32, 128)
+    a, o = KiviCache(amd, cfg, 1, heads, dim), KiviCache(oracle, cfg, 1, heads, dim)
+    a.append(k, v, seq)
+    o.append(k, v, seq)
+    q = (rng.standard_normal(qh * dim) * 2).astype(np.float32)
+    scale = np.float32(1 / np.sqrt(dim))
+    assert_close(a.attention(q, qh, scale), o.attention(q, qh, scale))
+
+
 @pytest.mark.parametrize("bits", [2, 4, 8])
 @pytest.mark.parametrize("dim,group", [(64, 16), (64, 64), (128, 16), (256, 16), (256, 32),
                                        (256, 64)])
