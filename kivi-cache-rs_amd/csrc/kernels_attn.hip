@@ -1311,7 +1311,7 @@ __global__ void __launch_bounds__(kThreads) k_attn_suffix(AttnArgs a, SessionTab
   if (hh == 0) {
 #pragma unroll
     for (uint32_t h = 0; h < kSufMaxHeads; ++h)
-      if (h < gq) sp[h][tk] = tk < n ? dot[h] : -INFINITY;
+      if (h < gq) sp[h][(tk & 1) * 64 + 16 * wave + (lane % 32) / 2] = tk < n ? dot[h] : -INFINITY;
   }
   __syncthreads();
   // softmax per head over the run's tokens (waves take heads w, w + 4)
@@ -1337,16 +1337,26 @@ __global__ void __launch_bounds__(kThreads) k_attn_suffix(AttnArgs a, SessionTab
   float4 acc[kSufMaxHeads];
 #pragma unroll
   for (uint32_t h = 0; h < kSufMaxHeads; ++h) acc[h] = make_float4(0.f, 0.f, 0.f, 0.f);
+  // a half-wave's 16 weights per head are contiguous (the order sp is written in): four rows'
+  // weights per 16-byte read
 #pragma unroll
-  for (int j = 0; j < 16; ++j) {
+  for (int i = 0; i < 4; ++i) {
+    float4 p4[kSufMaxHeads];
 #pragma unroll
-    for (uint32_t h = 0; h < kSufMaxHeads; ++h) {
-      if (h < gq) {
-        const float p = sp[h][32 * wave + 2 * j + hh];  // 0 for tokens past n
-        acc[h].x = fmaf(p, vv[j].x, acc[h].x);
-        acc[h].y = fmaf(p, vv[j].y, acc[h].y);
-        acc[h].z = fmaf(p, vv[j].z, acc[h].z);
-        acc[h].w = fmaf(p, vv[j].w, acc[h].w);
+    for (uint32_t h = 0; h < kSufMaxHeads; ++h)
+      if (h < gq) p4[h] = reinterpret_cast<const float4*>(&sp[h][hh * 64 + 16 * wave])[i];
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const float4 x = vv[4 * i + jj];
+#pragma unroll
+      for (uint32_t h = 0; h < kSufMaxHeads; ++h) {
+        if (h < gq) {
+          const float p = jj == 0 ? p4[h].x : jj == 1 ? p4[h].y : jj == 2 ? p4[h].z : p4[h].w;  // 0 past n
+          acc[h].x = fmaf(p, x.x, acc[h].x);
+          acc[h].y = fmaf(p, x.y, acc[h].y);
+          acc[h].z = fmaf(p, x.z, acc[h].z);
+          acc[h].w = fmaf(p, x.w, acc[h].w);
+        }
       }
     }
   }
