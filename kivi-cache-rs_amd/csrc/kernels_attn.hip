@@ -454,6 +454,14 @@ struct ValueParams {
   float4 sz[Chan<D>::HV];
 };
 
+// Sum of v over each quad, in every lane of it: (v0 + v1) + (v2 + v3) (DPP quad_perm; every
+// lane is active here).
+__device__ __forceinline__ float quad_sum(float v) {
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, true));  // [1,0,3,2]
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, true));  // [2,3,0,1]
+  return v;
+}
+
 // v as held by lane q of each quad (DPP quad_perm broadcast; every lane is active here).
 __device__ __forceinline__ float quad_bcast(float v, int q) {
   const int x = __float_as_int(v);
@@ -1209,10 +1217,11 @@ __global__ void __launch_bounds__(kThreads, BITS == 2 && NRS == 1 ? 3 : 2) k_att
 
 // Session suffixes of the shared-prefix form (fp32 rows, head_dim 128, GQA <= 8): one
 // workgroup per (session, unit, run of kSufTokens suffix tokens) writes one partial per head
-// into split nsplit_fast + run (runs past a session's suffix write empty partials). Keys: lane
-// pair (l, l + 32) of wave w owns token 32w + l%32, 64 channels each; values: half-wave h of
-// wave w owns rows 32w + 2j + h (j < 16), lane l channels 4 (l % 32) .. + 3, and the eight
-// half-waves' sums meet in LDS. Every load of a workgroup is issued before the first wait.
+// into split nsplit_fast + run (runs past a session's suffix write empty partials). Keys:
+// quad l/4 of wave w owns tokens 32w + l/4 and 32w + 16 + l/4, 32 channels per lane, its dot
+// products summed across the quad; values: half-wave h of wave w owns rows 32w + 2j + h
+// (j < 16), lane l channels 4 (l % 32) .. + 3, and the eight half-waves' sums meet in LDS.
+// Every load of a workgroup is issued before the first wait.
 // Raw buffer resource over `floats` floats at p (stride 0, 32-bit data format): loads at byte
 // offsets past the range return zeros.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const float* p, uint32_t floats) {
@@ -1271,11 +1280,17 @@ __global__ void __launch_bounds__(kThreads) k_attn_suffix(AttnArgs a, SessionTab
   __builtin_amdgcn_sched_barrier(0);
   // The run's rows through buffer resources of n rows: a row past n reads as zeros (its weight
   // is 0) without a memory request and without a branch around the load.
-  const uint32_t tk = 32 * wave + lane % 32, hh = lane / 32;
+  // Keys: quad q = l / 4 of wave w owns rows 32w + q (pass 0) and 32w + 16 + q (pass 1); lane
+  // k = l % 4 of the quad holds channels 16i + 4k .. + 3 (i < 8), so each load instruction
+  // reads 64 contiguous bytes of 16 rows.
+  const uint32_t hh = lane / 32, qd4 = lane / 4, kq = lane % 4;
   const __amdgpu_buffer_rsrc_t krs = rows_rsrc(d.k + unit * d.stride + t0 * D, n * D);
   float4 kv[16];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) kv[i] = rsrc_load4(krs, (tk * D + 64 * hh + 4 * i) * 4);
+  for (int p = 0; p < 2; ++p)
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      kv[8 * p + i] = rsrc_load4(krs, ((32 * wave + 16 * p + qd4) * D + 16 * i + 4 * kq) * 4);
   __builtin_amdgcn_sched_barrier(0);
   const __amdgpu_buffer_rsrc_t vrs = rows_rsrc(d.v + unit * d.stride + t0 * D, n * D);
   float4 vv[16];  // row 32w + 2j + hh, channels 4 (l % 32) .. + 3
@@ -1291,27 +1306,35 @@ __global__ void __launch_bounds__(kThreads) k_attn_suffix(AttnArgs a, SessionTab
     qd[3] = q4.w * a.scale2;
   }
   __syncthreads();  // queries in LDS
-  float dot[kSufMaxHeads];
+  float dot[2][kSufMaxHeads];
 #pragma unroll
   for (uint32_t h = 0; h < kSufMaxHeads; ++h) {
-    float acc = 0.f;
+    float acc0 = 0.f, acc1 = 0.f;
     if (h < gq) {
-      const float4* q4 = reinterpret_cast<const float4*>(&qs[h][64 * hh]);
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float4 q = q4[i];
-        acc = fmaf(q.x, kv[i].x, acc);
-        acc = fmaf(q.y, kv[i].y, acc);
-        acc = fmaf(q.z, kv[i].z, acc);
-        acc = fmaf(q.w, kv[i].w, acc);
+      for (int i = 0; i < 8; ++i) {
+        const float4 q = *reinterpret_cast<const float4*>(&qs[h][16 * i + 4 * kq]);
+        acc0 = fmaf(q.x, kv[i].x, acc0);
+        acc0 = fmaf(q.y, kv[i].y, acc0);
+        acc0 = fmaf(q.z, kv[i].z, acc0);
+        acc0 = fmaf(q.w, kv[i].w, acc0);
+        acc1 = fmaf(q.x, kv[8 + i].x, acc1);
+        acc1 = fmaf(q.y, kv[8 + i].y, acc1);
+        acc1 = fmaf(q.z, kv[8 + i].z, acc1);
+        acc1 = fmaf(q.w, kv[8 + i].w, acc1);
       }
     }
-    dot[h] = acc + __shfl_xor(acc, 32);
+    dot[0][h] = quad_sum(acc0);
+    dot[1][h] = quad_sum(acc1);
   }
-  if (hh == 0) {
+  if (kq == 0) {
 #pragma unroll
-    for (uint32_t h = 0; h < kSufMaxHeads; ++h)
-      if (h < gq) sp[h][(tk & 1) * 64 + 16 * wave + (lane % 32) / 2] = tk < n ? dot[h] : -INFINITY;
+    for (int p = 0; p < 2; ++p) {
+      const uint32_t r = 16 * p + qd4;  // row within the wave
+#pragma unroll
+      for (uint32_t h = 0; h < kSufMaxHeads; ++h)
+        if (h < gq) sp[h][(r & 1) * 64 + 16 * wave + r / 2] = 32 * wave + r < n ? dot[p][h] : -INFINITY;
+    }
   }
   __syncthreads();
   // softmax per head over the run's tokens (waves take heads w, w + 4)
