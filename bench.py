@@ -8,11 +8,13 @@ over all 16 sequences (the cache and the queries already resident in HBM); value
 tokens/s = 16 * steps / time.
 
 The default run measures every BASELINE.json workload in the same process and puts the others
-in `configs` (each with its own roofline and CPU baseline): c0 (the reference's CPU-runnable
-case), c1 (streaming decode: a step is RuntimeKv::decode = append one token + attention after
-an 8192-token prefill), c3_4 / c3_8 (4-/8-bit at 131072 tokens, GQA 8), c4 (64 RagSessions over
-one 65536-token prefix, one batched call per step). `--config NAME` measures one workload and
-prints its line alone (the form the rocprof summaries use).
+in `configs` as compact entries (step, throughput, HBM fraction, roofline, CPU baseline): c0
+(the reference's CPU-runnable case), c1 (streaming decode: a step is RuntimeKv::decode = append
+one token + attention after an 8192-token prefill), c3_4 / c3_8 (4-/8-bit at 131072 tokens,
+GQA 8), c4 (64 RagSessions over one 65536-token prefix, one batched call per step). `--config
+NAME` measures one workload and prints its line alone (the form the rocprof summaries use).
+The printed line stays under LINE_LIMIT characters; the full result (per-kernel tables,
+exports, codec, guard) is written to --full-json PATH when asked for.
 
 Per workload: the cache build (prefill quantization) is timed once (`quantize_gbps`, and per
 kernel); the timed region runs `steps` steps twice, plain (the step time) and with the library's
@@ -31,13 +33,13 @@ launch from rocprofv3 FETCH_SIZE + WRITE_SIZE runs calibrated on a plain copy ke
 kernel, workload and algorithmic bytes.
 
 The primary line also carries the device exports (packed streams in the reference order, dense
-reconstruction), the standalone codec (quantize_per_channel / per_token of the C2 tensors), and
-one QualityGuard check per R appended tokens on the c1 shape (median over repetitions).
+reconstruction) and the standalone codec (quantize_per_channel / per_token of the C2 tensors),
+and the c1 entry one QualityGuard check per R appended tokens (median over repetitions).
 `cpu_baseline` is the oracle (C++ restatement of the reference CPU path, one thread) on a
 bounded sample of each workload, on this host.
 
 Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--config NAME] [--no-cpu]
-                       [--copy-calibration MIB]
+                       [--other-shapes] [--full-json PATH] [--copy-calibration MIB]
 """
 
 import argparse
@@ -73,15 +75,18 @@ CONFIGS = {
     "c4": (1, 8, 32, 128, 65536, 2, 32, 128,
            "config 4: one 65536-token 2-bit G=32 R=128 prefix (8 KV heads, head_dim 128) shared by "
            "64 RagSessions with 96-token fp32 suffixes, 32 query heads, batched sessions attention"),
-    # shapes outside the matrix-core path (k_attn_generic), timed on request only
-    "g_d64": (16, 8, 32, 64, 32768, 2, 32, 128, "generic path: batch 16, 32q/8kv heads, head_dim 64, 32768 tokens, 2-bit"),
-    "g_d256": (4, 8, 32, 256, 32768, 2, 32, 128, "generic path: batch 4, 32q/8kv heads, head_dim 256, 32768 tokens, 2-bit"),
-    "g_gqa16": (4, 4, 64, 128, 32768, 2, 32, 128, "generic path: batch 4, 64q/4kv heads (GQA 16), head_dim 128, 32768 tokens, 2-bit"),
-    "g_g64": (16, 8, 32, 128, 32768, 2, 64, 128, "generic path: batch 16, 32q/8kv heads, head_dim 128, 32768 tokens, 2-bit G=64"),
-    "g_d256_b4": (4, 8, 32, 256, 32768, 4, 32, 128, "generic path: batch 4, 32q/8kv heads, head_dim 256, 32768 tokens, 4-bit"),
-    "g_d256_b8": (4, 8, 32, 256, 32768, 8, 32, 128, "generic path: batch 4, 32q/8kv heads, head_dim 256, 32768 tokens, 8-bit"),
+    # shapes beyond head_dim 128 / G 32 / GQA <= 8, timed on request only
+    "g_d64": (16, 8, 32, 64, 32768, 2, 32, 128, "other shape: batch 16, 32q/8kv heads, head_dim 64, 32768 tokens, 2-bit"),
+    "g_d256": (4, 8, 32, 256, 32768, 2, 32, 128, "other shape: batch 4, 32q/8kv heads, head_dim 256, 32768 tokens, 2-bit"),
+    "g_gqa16": (4, 4, 64, 128, 32768, 2, 32, 128, "other shape: batch 4, 64q/4kv heads (GQA 16), head_dim 128, 32768 tokens, 2-bit"),
+    "g_g64": (16, 8, 32, 128, 32768, 2, 64, 128, "other shape: batch 16, 32q/8kv heads, head_dim 128, 32768 tokens, 2-bit G=64"),
+    "g_d256_b4": (4, 8, 32, 256, 32768, 4, 32, 128, "other shape: batch 4, 32q/8kv heads, head_dim 256, 32768 tokens, 4-bit"),
+    "g_d256_b8": (4, 8, 32, 256, 32768, 8, 32, 128, "other shape: batch 4, 32q/8kv heads, head_dim 256, 32768 tokens, 8-bit"),
 }
-SECONDARY = ("c0", "c1", "c3_4", "c3_8", "c4", "g_d64", "g_d256", "g_d256_b4", "g_d256_b8", "g_g64", "g_gqa16")
+SECONDARY = ("c0", "c1", "c3_4", "c3_8", "c4")
+# shapes beyond head_dim 128 / G 32 / GQA <= 8: measured with --other-shapes (stderr and
+# --full-json only) or one at a time with --config
+OTHER_SHAPES = ("g_d64", "g_d256", "g_d256_b4", "g_d256_b8", "g_g64", "g_gqa16")
 # batched-sessions workloads: name -> (sessions, suffix tokens per session)
 SESSIONS = {"c4": (64, 96)}
 # streaming-decode workloads: name -> decode steps the workload allows after the prefill
@@ -709,9 +714,83 @@ def guard_check(kivi, amd, cfg_tuple, reps=5):
                     "alternating"}
 
 
-SUMMARY_KEYS = ("value", "unit", "ms_per_step", "ms_per_step_evented", "effective_hbm_gbps",
-                "hbm_fraction", "quantize_gbps", "cache_copies", "cache_resident", "clock_warmup_calls",
-                "config", "roofline", "kernels", "quantize_kernels", "guard", "cpu_baseline")
+# The driver keeps the tail of stdout, so the line bench.py prints must stay short: the
+# headline workload with its roofline and CPU baseline, and one compact entry per other
+# workload. The full result (per-kernel tables, exports, codec, guard) goes to --full-json.
+LINE_LIMIT = 6000
+PRIMARY_KEYS = ("metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step",
+                "higher_is_better", "scaling", "vs_baseline", "dtype", "data", "config")
+ROOFLINE_KEYS = ("bound", "achieved", "peak", "unit", "frac", "traffic", "kernel",
+                 "mean_launch_us", "algorithmic_bytes_per_launch", "algorithmic_flops_per_launch")
+
+
+def rnd(x, digits=4):
+    """x rounded to `digits` significant digits (ints, None and strings unchanged)."""
+    if isinstance(x, float) and math.isfinite(x) and x != 0.0:
+        return round(x, digits - 1 - int(math.floor(math.log10(abs(x)))))
+    return x
+
+
+def compact_roofline(r, full=True):
+    keys = ROOFLINE_KEYS if full else ROOFLINE_KEYS[:7]
+    counts = ("traffic", "algorithmic_bytes_per_launch", "algorithmic_flops_per_launch")
+    return {k: (int(round(r[k])) if k in counts and r[k] is not None else rnd(r[k]))
+            for k in keys if k in r}
+
+
+def compact_cpu(c, full=True):
+    if c is None:
+        return None
+    out = {"value": rnd(c["value"]), "unit": c["unit"], "ms_per_step": rnd(c["ms_per_step"]),
+           "cores": c["cores"], "kind": c["kind"]}
+    if full:
+        out.update({"sample": c["sample"], "cpu": c.get("cpu"), "nproc": c.get("nproc")})
+        if "quantize_gbps" in c:
+            out["quantize_gbps"] = rnd(c["quantize_gbps"])
+    return out
+
+
+def compact(result, primary):
+    """The short form of one workload's result: the primary line's fields, or a `configs`
+    entry (throughput, step, HBM fraction, roofline and CPU baseline)."""
+    out = {}
+    if primary:
+        out.update({k: rnd(result[k]) for k in PRIMARY_KEYS})
+    else:
+        out.update({"value": rnd(result["value"]), "ms_per_step": rnd(result["ms_per_step"])})
+    out["hbm_fraction"] = rnd(result["hbm_fraction"])
+    out["quantize_gbps"] = rnd(result["quantize_gbps"])
+    if result.get("cache_resident"):
+        out["cache_resident"] = True
+    out["roofline"] = compact_roofline(result["roofline"], primary)
+    out["kernels_us"] = {fam: rnd(r["mean_us"]) for fam, r in result["kernels"].items()}
+    if primary:
+        out["effective_hbm_gbps"] = rnd(result["effective_hbm_gbps"])
+        out["cache_copies"] = result["cache_copies"]
+        if "codec" in result:
+            out["codec_gbps"] = {k: rnd(v["gbps"]) for k, v in result["codec"].items()}
+        if "exports" in result:
+            out["exports_gbps"] = {k: rnd(v["gbps"]) for k, v in result["exports"].items()}
+    if "guard" in result:
+        g = result["guard"]
+        out["guard_ms"] = {"guarded": rnd(g["guarded_ms_median"]),
+                           "plain": rnd(g["plain_append_attention_ms_median"])}
+    out["cpu_baseline"] = compact_cpu(result.get("cpu_baseline"), primary)
+    return out
+
+
+def emit(line_obj, full_obj, path):
+    """Print the one JSON line (refusing one over LINE_LIMIT characters) and write the full
+    result to `path` when given."""
+    if path:
+        Path(path).parent.mkdir(parents=True, exist_ok=True)
+        Path(path).write_text(json.dumps(full_obj, indent=1))
+        log(f"[bench] full result written to {path}")
+    line = json.dumps(line_obj, separators=(",", ":"))
+    if len(line) > LINE_LIMIT:
+        sys.exit(f"bench.py: the result line is {len(line)} characters, over the {LINE_LIMIT} "
+                 f"the driver keeps; shorten compact()")
+    print(line, flush=True)
 
 
 def main():
@@ -723,6 +802,11 @@ def main():
                     help="measure only this workload (default: c2 as the primary line, the others "
                          "in `configs`)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
+    ap.add_argument("--other-shapes", action="store_true",
+                    help="also measure the shapes outside head_dim 128 / G 32 / GQA <= 8 (logged "
+                         "to stderr and --full-json, not in the result line)")
+    ap.add_argument("--full-json", default=None, metavar="PATH",
+                    help="write the full result (per-kernel tables, exports, codec, guard) here")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="after each timed region, copy MIB MiB device-to-device 3 times (a plain "
                          "copy kernel of known size for calibrating rocprofv3 byte counters)")
@@ -743,14 +827,21 @@ def main():
     stream = torch.cuda.Stream()
     with_cpu = not args.no_cpu
     if args.config is not None:
-        print(json.dumps(measure(args.config, args, torch, kivi, amd, stream, with_cpu)), flush=True)
+        result = measure(args.config, args, torch, kivi, amd, stream, with_cpu)
+        emit(compact(result, True), result, args.full_json)
         return
     result = measure("c2", args, torch, kivi, amd, stream, with_cpu)
-    result["configs"] = {}
-    for name in SECONDARY:
+    line = compact(result, True)
+    line["configs"], result["configs"] = {}, {}
+    for name in SECONDARY + (OTHER_SHAPES if args.other_shapes else ()):
         sub = measure(name, args, torch, kivi, amd, stream, with_cpu)
-        result["configs"][name] = {key: sub[key] for key in SUMMARY_KEYS if key in sub}
-    print(json.dumps(result), flush=True)
+        result["configs"][name] = sub
+        if name in SECONDARY:
+            line["configs"][name] = compact(sub, False)
+        else:
+            c = compact(sub, False)
+            log(f"[bench] {name}: " + json.dumps(c, separators=(",", ":")))
+    emit(line, result, args.full_json)
 
 
 if __name__ == "__main__":

@@ -129,3 +129,46 @@ def signed_zero_rows(rng, shape, p=0.25):
     x[z & neg] = np.float32(-0.0)
     x[z & ~neg] = np.float32(0.0)
     return x
+
+
+# ------------------------------------------------------------------ large-magnitude inputs
+# The reference's quiet-channel fixture (tests/quant.rs:170-211, examples/streaming_cache.rs:
+# 10-17): channel 0 of a 32-channel row is 100.0 and channel d >= 1 is d/32, the same for
+# every token. The generators below tile that row across head_dim and add the magnitudes the
+# KIVI observation is about (key channels x100 / x1000, value groups mixing 1e-3 and 1e2).
+
+
+def quiet_channel_rows(tokens, dim, jitter=0.0, rng=None):
+    """[tokens, dim] rows of the quiet-channel fixture tiled over head_dim (channels 0, 32,
+    ... are 100.0; channel d is (d % 32)/32 otherwise). With ``jitter`` > 0, N(0, jitter)
+    noise on the quiet channels and N(0, 1) on the loud ones, so group spans are non-zero."""
+    d = np.arange(dim)
+    row = np.where(d % 32 == 0, np.float32(100.0), (d % 32).astype(np.float32) / np.float32(32.0))
+    x = np.broadcast_to(row.astype(np.float32), (tokens, dim)).copy()
+    if jitter:
+        noise = rng.standard_normal((tokens, dim)).astype(np.float32)
+        x += np.where(d % 32 == 0, np.float32(1.0), np.float32(jitter)) * noise
+    return x.astype(np.float32)
+
+
+def loud_channel_keys(rng, shape, magnitude, per_head=2):
+    """N(0,1) keys [.., heads, T, D] with ``per_head`` channels of every KV head scaled by
+    ``magnitude`` (the same channels for every token)."""
+    k = rng.standard_normal(shape).astype(np.float32)
+    heads, dim = shape[-3], shape[-1]
+    for h in range(heads):
+        chans = rng.choice(dim, size=per_head, replace=False)
+        k[..., h, :, chans] *= np.float32(magnitude)
+    return k
+
+
+def mixed_magnitude_values(rng, shape, group=32):
+    """N(0,1) values [.., T, D] whose 32-channel groups take, per (token, group), one of:
+    every channel ~1e-3; every channel ~1e2; channels alternating 1e-3 / 1e2; ~1."""
+    v = rng.standard_normal(shape).astype(np.float32)
+    lead, dim = shape[:-1], shape[-1]
+    mode = rng.integers(0, 4, size=lead + (dim // group,))
+    alt = np.where(np.arange(group) % 2 == 0, 1e-3, 1e2)
+    table = np.stack([np.full(group, 1e-3), np.full(group, 1e2), alt, np.ones(group)])
+    mag = table[mode].reshape(lead + (dim,)).astype(np.float32)
+    return (v * mag).astype(np.float32)
