@@ -182,8 +182,12 @@ kivi_status kivi_cache_attention_device(const kivi_cache* cache, const float* qu
  * floats, about 1.26 M for batch 16 x 8 KV heads x 32768 tokens with 32 query heads). It calls
  * no hipMalloc, hipFree or memset (an empty cache's zeros come from a fill kernel) and does not
  * wait for the device. Larger calls return KIVI_ERR_CAPACITY (a = floats needed, b = the
- * limit). Every call on one device shares that device's workspace: calls that overlap on the
- * device race (calls on one stream are ordered). */
+ * limit). Every call on one device shares that device's workspace. Calls on one stream are
+ * ordered by the stream; a call on another stream than the previous call waits (on the device,
+ * through an event the library creates once per device at its first call there) for the work
+ * enqueued on that stream so far. A call made under stream capture is ordered only by the
+ * stream its graph is launched on: graph launches that overlap other calls on the device
+ * race, and ordering them is the caller's part. */
 kivi_status kivi_cache_attention_device_noalloc(const kivi_cache* cache, const float* query,
                                                 size_t query_len, size_t num_q_heads, float scale,
                                                 float* out, size_t out_len, void* stream,

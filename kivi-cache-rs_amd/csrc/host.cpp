@@ -789,10 +789,42 @@ Status cache_attention(const kivi_cache* c, const float* query, size_t query_len
   return sync(s, "attention");
 }
 
+// Ordering of the calls that share one device's static workspace. Calls on one stream are
+// ordered by the stream. An eager call on another stream than the previous eager call first
+// waits for an event recorded on that stream at this moment (as AttnSync does for a cache's
+// own workspace). The event is created once per device, with the workspace's address, at the
+// first call there. A call enqueued under stream capture is ordered only by the stream its
+// graph is later launched on, and leaves the eager ordering state alone.
+struct StaticWorkspaceSlot {
+  std::mutex mu;
+  float* ws = nullptr;
+  hipEvent_t done = nullptr;
+  hipStream_t last = nullptr;
+  bool used = false;
+};
+constexpr int kMaxStaticDevices = 64;
+std::mutex g_static_mu;
+StaticWorkspaceSlot g_static_slots[kMaxStaticDevices];
+
+Status static_workspace_slot(int device, StaticWorkspaceSlot** out) {
+  if (device < 0 || device >= kMaxStaticDevices)
+    return Err(KIVI_ERR_UNSUPPORTED, static_cast<size_t>(device), kMaxStaticDevices, "device index");
+  std::lock_guard<std::mutex> lock(g_static_mu);
+  StaticWorkspaceSlot& slot = g_static_slots[device];
+  if (slot.ws == nullptr) {
+    float* ws = nullptr;
+    HIP_TRY(static_workspace(&ws), "static attention workspace");
+    HIP_TRY(hipEventCreateWithFlags(&slot.done, hipEventDisableTiming), "static workspace event");
+    slot.ws = ws;
+  }
+  *out = &slot;
+  return Status{};
+}
+
 // KiviCache::attention on device pointers with the split partials in the library's static
 // per-device workspace: no allocation, no memset (an empty cache's zeros come from a fill
-// kernel), no host-side wait. Checks as cache_attention, then the workspace size. Calls that
-// overlap on one device share the workspace and race; calls on one stream are ordered.
+// kernel), no host-side wait. Checks as cache_attention, then the workspace size. Eager calls
+// on different streams are ordered by StaticWorkspaceSlot; calls on one stream by the stream.
 Status cache_attention_noalloc(const kivi_cache* c, const float* query, size_t query_len,
                                size_t num_q_heads, float scale, float* out, size_t out_len,
                                hipStream_t stream) {
@@ -811,9 +843,21 @@ Status cache_attention_noalloc(const kivi_cache* c, const float* query, size_t q
   const size_t floats = attention_workspace_floats(p);
   if (floats > kStaticWorkspaceFloats)
     return Err(KIVI_ERR_CAPACITY, floats, kStaticWorkspaceFloats, "attention workspace floats");
-  float* ws = nullptr;
-  HIP_TRY(static_workspace(&ws), "static attention workspace");
-  HIP_TRY(launch_attention(p, ws, stream), "attention");
+  StaticWorkspaceSlot* slot = nullptr;
+  KIVI_TRY(static_workspace_slot(core.device, &slot));
+  std::lock_guard<std::mutex> lock(slot->mu);
+  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+  HIP_TRY(hipStreamIsCapturing(stream, &capture), "attention capture status");
+  const bool eager = capture == hipStreamCaptureStatusNone;
+  if (eager && slot->used && slot->last != stream) {
+    HIP_TRY(hipEventRecord(slot->done, slot->last), "static workspace ordering");
+    HIP_TRY(hipStreamWaitEvent(stream, slot->done, 0), "static workspace ordering");
+  }
+  HIP_TRY(launch_attention(p, slot->ws, stream), "attention");
+  if (eager) {
+    slot->used = true;
+    slot->last = stream;
+  }
   return Status{};
 }
 
