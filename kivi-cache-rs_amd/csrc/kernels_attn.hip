@@ -1240,7 +1240,55 @@ __device__ __forceinline__ float2 rsrc_load2(__amdgpu_buffer_rsrc_t r, uint32_t 
 
 constexpr uint32_t kSufTokens = 128;
 constexpr uint32_t kSufMaxHeads = 8;
+constexpr uint32_t kSufMergeRound = 16;  // GEMM split partials a wave loads per round
 
+// Output row (sess, unit, h) of the shared-prefix form: the GEMM splits' partials [0,
+// nsplit_fast) merged by log-sum-exp with the suffix partial (m, l, o) the wave holds (lane l:
+// channels 2l, 2l + 1), in rounds of kSufMergeRound independent loads; the (m, l) pairs are
+// wave-uniform.
+__device__ __forceinline__ void merge_suffix_row(const AttnArgs& a, uint32_t sess, uint32_t unit, uint32_t h,
+                                                 uint32_t lane, float m, float l, float2 o) {
+  constexpr uint32_t D = 128, RB = kSufMergeRound;
+  const uint32_t gq = a.gq, ns = a.nsplit_fast;
+  const uint64_t stride = (uint64_t)gq * (D + 2);
+  const float* base = a.ws + (uint64_t)sess * a.ws_sess_stride + ((uint64_t)unit * a.nsplit_total * gq + h) * (D + 2);
+  for (uint32_t s0 = 0; s0 < ns; s0 += RB) {
+    float2 v[RB];
+    float ms[RB], ls[RB];
+#pragma unroll
+    for (uint32_t j = 0; j < RB; ++j) {
+      const float* ps = base + (uint64_t)std::min(s0 + j, ns - 1) * stride;
+      ms[j] = s0 + j < ns ? ps[D] : -INFINITY;
+      ls[j] = ps[D + 1];
+      v[j] = *reinterpret_cast<const float2*>(ps + 2 * lane);
+    }
+    float bm = m;
+#pragma unroll
+    for (uint32_t j = 0; j < RB; ++j) bm = fmaxf(bm, ms[j]);
+    if (bm != -INFINITY) {
+      const float r = __builtin_amdgcn_exp2f(m - bm);  // 0 while m is -inf
+      l *= r;
+      o.x *= r;
+      o.y *= r;
+#pragma unroll
+      for (uint32_t j = 0; j < RB; ++j) {
+        const float f = ms[j] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms[j] - bm);
+        l = fmaf(ls[j], f, l);
+        o.x = fmaf(v[j].x, f, o.x);
+        o.y = fmaf(v[j].y, f, o.y);
+      }
+      m = bm;
+    }
+  }
+  const uint32_t b = unit / a.heads, kvh = unit % a.heads;
+  float* out = a.out + (uint64_t)sess * a.q_sess_stride + ((uint64_t)b * a.qh + kvh * gq + h) * D;
+  *reinterpret_cast<float2*>(out + 2 * lane) = make_float2(o.x / l, o.y / l);
+}
+
+// MERGED (a launch group whose suffixes fit one run, after k_attn_shared): one workgroup per
+// (session, unit) computes its suffix partial and merges it with the GEMM splits' partials
+// into the output (merge_suffix_row), in place of writing a partial for k_attn_merge.
+template <bool MERGED>
 __global__ void __launch_bounds__(kThreads) k_attn_suffix(AttnArgs a, SessionTable t) {
   constexpr uint32_t D = 128;
   __shared__ float qs[kSufMaxHeads][D];
@@ -1249,14 +1297,19 @@ __global__ void __launch_bounds__(kThreads) k_attn_suffix(AttnArgs a, SessionTab
   __shared__ float red[4][2][kSufMaxHeads][D];  // [wave][half-wave][head][channel]
   const uint32_t lane = threadIdx.x % 64, wave = threadIdx.x / 64;
   const uint32_t gq = a.gq;
-  const uint32_t per_sess = a.units * a.nsplit_win;
+  const uint32_t runs = MERGED ? 1u : a.nsplit_win;
+  const uint32_t per_sess = a.units * runs;
   const uint32_t sess = blockIdx.x / per_sess, rem = blockIdx.x % per_sess;
-  const uint32_t unit = rem / a.nsplit_win, run = rem % a.nsplit_win;
+  const uint32_t unit = rem / runs, run = rem % runs;
   const SessionDesc d = t.d[sess];
   const uint64_t t0 = (uint64_t)run * kSufTokens;
   const uint32_t n = d.len > t0 ? static_cast<uint32_t>(std::min<uint64_t>(kSufTokens, d.len - t0)) : 0u;
   const uint32_t b = unit / a.heads, kvh = unit % a.heads;
   if (n == 0) {
+    if constexpr (MERGED) {
+      for (uint32_t h = wave; h < gq; h += 4) merge_suffix_row(a, sess, unit, h, lane, -INFINITY, 0.f, make_float2(0.f, 0.f));
+      return;
+    }
     // no token of this session in the run (its suffix arrays may be absent): empty partials
     for (uint32_t h = wave; h < gq; h += 4) {
       float* part = a.ws + (uint64_t)sess * a.ws_sess_stride +
@@ -1398,12 +1451,16 @@ __global__ void __launch_bounds__(kThreads) k_attn_suffix(AttnArgs a, SessionTab
         o.y += x.y;
       }
     }
-    float* part = a.ws + (uint64_t)sess * a.ws_sess_stride +
-                  (((uint64_t)unit * a.nsplit_total + a.nsplit_fast + run) * gq + h) * (D + 2);
-    *reinterpret_cast<float2*>(part + 2 * lane) = o;
-    if (lane == 0) {
-      part[D] = ml[h][0];
-      part[D + 1] = ml[h][1];
+    if constexpr (MERGED) {
+      merge_suffix_row(a, sess, unit, h, lane, ml[h][0], ml[h][1], o);
+    } else {
+      float* part = a.ws + (uint64_t)sess * a.ws_sess_stride +
+                    (((uint64_t)unit * a.nsplit_total + a.nsplit_fast + run) * gq + h) * (D + 2);
+      *reinterpret_cast<float2*>(part + 2 * lane) = o;
+      if (lane == 0) {
+        part[D] = ml[h][0];
+        part[D + 1] = ml[h][1];
+      }
     }
   }
 }
@@ -2407,14 +2464,19 @@ hipError_t launch_sessions(const AttnArgs& a, const SessionTable& t, const Group
   return hipGetLastError();
 }
 
+// A launch group of the GEMM form whose suffixes fit one run (at most kSufTokens tokens each):
+// its suffix kernel runs after k_attn_shared and merges every output row itself.
+bool shared_merges_in_suffix(const AttnArgs& a) { return a.nsplit_fast > 0 && a.nsplit_win <= 1; }
+
 template <int BITS, int NRS>
 hipError_t launch_shared(const AttnArgs& a, const SessionTable& t, const GroupBytes& by,
                          hipStream_t stream) {
-  // window / suffix chunks per session: the window workgroups of the per-session kernel
+  const bool merged = shared_merges_in_suffix(a);
+  // window / suffix chunks per session: one workgroup per (session, unit, run of suffix tokens)
   const uint32_t nwin = a.nsess * a.units * a.nsplit_win;
-  if (nwin > 0) {
+  if (nwin > 0 && !merged) {
     TimedLaunch timed(KIVI_KERNEL_ATTN_SESSIONS, stream, by.suffixes + by.queries);
-    k_attn_suffix<<<nwin, kThreads, 0, stream>>>(a, t);
+    k_attn_suffix<false><<<nwin, kThreads, 0, stream>>>(a, t);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
@@ -2428,8 +2490,18 @@ hipError_t launch_shared(const AttnArgs& a, const SessionTable& t, const GroupBy
   });
   if (configured != hipSuccess) return configured;
   const uint32_t rblocks = (a.nsess * a.gq + kShRows - 1) / kShRows;
-  TimedLaunch timed(KIVI_KERNEL_ATTN_SHARED, stream, by.prefix + by.queries);
-  k_attn_shared<BITS><<<a.units * rblocks * a.nsplit_fast, kShThreads, kShLdsBytes, stream>>>(a);
+  {
+    TimedLaunch timed(KIVI_KERNEL_ATTN_SHARED, stream, by.prefix + by.queries);
+    k_attn_shared<BITS><<<a.units * rblocks * a.nsplit_fast, kShThreads, kShLdsBytes, stream>>>(a);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess || !merged) return e;
+  }
+  // the suffixes and the merge of every row: the suffix rows and queries, the GEMM partials
+  // read back, the outputs written
+  const double rows = (double)a.nsess * a.units * a.gq;
+  TimedLaunch timed(KIVI_KERNEL_ATTN_SESSIONS, stream,
+                    by.suffixes + by.queries + rows * ((double)a.nsplit_fast * (a.c.geo.D + 2) + a.c.geo.D) * 4.0);
+  k_attn_suffix<true><<<a.nsess * a.units, kThreads, 0, stream>>>(a, t);
   return hipGetLastError();
 }
 
@@ -2496,6 +2568,7 @@ hipError_t launch_sessions_attention(const SessionsProblem& p, float* workspace,
       default: e = hipErrorInvalidValue; break;
     }
     if (e != hipSuccess) return e;
+    if (shared && shared_merges_in_suffix(a)) continue;  // the suffix kernel wrote the outputs
     const double bytes = (double)count * g.units * a.gq * ((double)a.nsplit_total * (g.D + 2) + g.D) * 4.0;
     TimedLaunch timed(KIVI_KERNEL_ATTN_MERGE, stream, bytes);
     e = launch_merge(workspace, a.nsplit_total, a.gq, g.D, p.heads, p.qh, a.out, g.units, count,
