@@ -718,15 +718,23 @@ __device__ __forceinline__ void key_fp32(const AttnArgs& a, uint64_t t0, uint32_
 }
 
 // The quarter's fp32 value rows for channels lane and 64+lane (tokens 16*quarter .. +15, all
-// 32 values requested at once).
+// 32 values requested at once). Lane r of each 16 computes row r's address once (vector
+// work), and each row's address reaches the wave by readlane, in place of 16 scalar address
+// computations with their branches.
 struct ValueRows {
   float b[16][2];
 };
 __device__ __forceinline__ void load_value_rows(const AttnArgs& a, uint32_t unit, uint64_t t0,
                                                 uint32_t quarter, uint32_t lane, ValueRows& vr) {
+  const uint64_t mine = reinterpret_cast<uint64_t>(value_row(a, unit, t0 + 16 * quarter + lane % 16));
+  const uint32_t lo = static_cast<uint32_t>(mine), hi = static_cast<uint32_t>(mine >> 32);
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
-    const float* row = value_row(a, unit, t0 + 16 * quarter + r);
+    // readlane returns int: each word is taken as uint32_t before widening, or a low word with
+    // its top bit set would sign-extend over the high word
+    const uint64_t p = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane(hi, r) << 32) |
+                       (uint64_t)(uint32_t)__builtin_amdgcn_readlane(lo, r);
+    const float* row = reinterpret_cast<const float*>(p);
     vr.b[r][0] = row[lane];
     vr.b[r][1] = row[lane + 64];
   }
@@ -811,16 +819,22 @@ __device__ __forceinline__ void evict_groups(EvictRow& e, float levels, float& s
 // unit (chunks whose 64 keys and 64 values are all packed). D = 128, G = 32. Per chunk the
 // operands are prepared from the (scale, zero) registers first, then the next chunk's data
 // is requested into the same registers while this chunk's MFMAs run (code words are
-// double-buffered).
-template <int BITS, int NRS, int CPW, bool MIXED, int D>
+// double-buffered). EARLY (one chunk per wave, launches of a few hundred workgroups such as a
+// decode step, where every memory round trip is on the critical path): the chunk's value
+// data and fp32 rows are requested with its key data at the start, so the wave waits for
+// memory once.
+template <int BITS, int NRS, int CPW, bool MIXED, int D, bool EARLY = false>
 __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uint32_t split,
                                            uint32_t hg, float* lds) {
   static_assert(!MIXED || D == 128, "window / suffix chunks are taken at head_dim 128 only");
+  static_assert(!EARLY || CPW == 1, "early requests cover one chunk per wave");
   constexpr int KS = Chan<D>::KS, HV = Chan<D>::HV;
   constexpr int ROW = CPW * 64 + kRowPad;  // logits row stride (floats)
   constexpr int NH = 4 * NRS;              // padded heads per unit
   const uint32_t b = unit / a.heads, kvh = unit % a.heads;
-  const uint32_t lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+  // the wave index as a wave-uniform value: the chunk, quarter and row addresses derived from
+  // it are then scalar (a MIXED wave's fp32 row addresses otherwise take divergent branches)
+  const uint32_t lane = threadIdx.x % 64, wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
   const uint32_t la = (lane % 32) / 4;  // block within a half-wave
   const uint32_t li = lane % 4;         // MFMA row = head within the row set
   const uint32_t lc = lane / 32;        // half-wave: key group / value channel group parity
@@ -862,6 +876,19 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
   const bool value_rows = MIXED && nch > 0 && tw + 16 * quarter + 16 > vq && tw + 16 * quarter < total;
   KeyRows krw;
   ValueRows vrw;
+  ValueParams<D> vp;
+  ValueWords<BITS, D> vw0, vw1;
+  if constexpr (EARLY) {
+    if (nch > 0) {
+      const int32_t v0 = std::min(chunk_of(0), lastv);
+      load_value_params<D>(a, unit, v0, la, lc, li, vp);
+      load_value_words<BITS, D>(a, unit, v0, lane, vw0);
+    }
+    if constexpr (MIXED) {
+      if (key_rows) load_key_rows(a, unit, tw, quarter, lane, krw);
+      if (value_rows) load_value_rows(a, unit, tw, quarter, lane, vrw);
+    }
+  }
 
   // a decode token appended by this launch evicts token vq-1 from the window: its row
   EvictRow er{};
@@ -899,18 +926,11 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
   // operand |w * scale| * 2^ev (w <= 1) stays below 2^15, from the unit's largest scales.
   qmax = warp_max(qmax);
   const float kmax = __uint_as_float(a.c.smax[4 * unit]);
-  float vmax = __uint_as_float(a.c.smax[4 * unit + 1]);
   constexpr float kLevels = static_cast<float>((1 << BITS) - 1);
-  float ev_scale = 0.f, ev_amax = 0.f;  // the evicted row's largest scale and |x|
-  if (D == 128 && a.pend_evict) {
-    evict_groups(er, kLevels, ev_scale, ev_amax);
-    vmax = fmaxf(vmax, ev_scale);  // the maximum its quantization raises (as the append would)
-  }
   const int ek = std::min(60, std::max(-100, 15 - __builtin_amdgcn_frexp_expf(qmax * kmax)));
-  const int ev = std::min(60, std::max(-100, 15 - __builtin_amdgcn_frexp_expf(vmax)));
   constexpr int kExp = CodeUnit<BITS>::kExp;
-  const float kfac = ldexpf(1.f, ek), vfac = ldexpf(1.f, ev);
-  const float kout = ldexpf(1.f, -ek - kExp), vout = ldexpf(1.f, -ev - kExp);
+  const float kfac = ldexpf(1.f, ek);
+  const float kout = ldexpf(1.f, -ek - kExp);
 #pragma unroll
   for (int rs = 0; rs < NRS; ++rs)
 #pragma unroll
@@ -948,7 +968,7 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
       if (packed) key_mfma<BITS, NRS, D>(cur, A, lg);
       if constexpr (MIXED) {
         if (key_rows) {  // t0 == tw
-          load_key_rows(a, unit, tw, quarter, lane, krw);
+          if constexpr (!EARLY) load_key_rows(a, unit, tw, quarter, lane, krw);
           key_fp32<NRS>(a, t0, quarter, lane, qv, krw, kUnit, lg);
         }
       }
@@ -968,7 +988,7 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
     }
   }
   // wave max per head; each lane keeps the max of its own MFMA row (true base-2 units)
-  if constexpr (MIXED) {
+  if constexpr (MIXED && !EARLY) {
     if (value_rows) load_value_rows(a, unit, tw, quarter, lane, vrw);
   }
   float mrow[NRS];
@@ -979,6 +999,18 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
     for (int i = 0; i < 4; ++i) mall[i] = warp_max(mx[rs][i]) * kout;
     mrow[rs] = li == 0 ? mall[0] : li == 1 ? mall[1] : li == 2 ? mall[2] : mall[3];
   }
+  // the value operands' range: the unit's largest value scale, raised by the evicted row's
+  // quantization when a decode token is appended by this launch (as the append would have);
+  // taken after the logits, so the evicted row's load is not waited for before them
+  float vmax = __uint_as_float(a.c.smax[4 * unit + 1]);
+  float ev_scale = 0.f, ev_amax = 0.f;  // the evicted row's largest scale and |x|
+  if (D == 128 && a.pend_evict) {
+    evict_groups(er, kLevels, ev_scale, ev_amax);
+    vmax = fmaxf(vmax, ev_scale);
+  }
+  const int ev = std::min(60, std::max(-100, 15 - __builtin_amdgcn_frexp_expf(vmax)));
+  const float vfac = ldexpf(1.f, ev);
+  const float vout = ldexpf(1.f, -ev - kExp);
   // exponent offset: the row max, or 0 when every logit of the row is -inf (a MIXED wave whose
   // quarter lies past `total`), so the weights are 0 rather than NaN
   float moff[NRS];
@@ -1004,8 +1036,6 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
     lsum[rs] = 0.f;
   }
   {
-    ValueParams<D> vp;
-    ValueWords<BITS, D> vw0, vw1;
     ValueA<NRS, D> A;
     auto step = [&](int k, ValueWords<BITS, D>& cur, ValueWords<BITS, D>& next) {
       const uint64_t t0 = (uint64_t)chunk_of(k) * 64;
@@ -1072,7 +1102,7 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
         if (value_rows) value_fp32<NRS>(a, t0, quarter, la, wl + li * ROW, moff, kout, vfac * kUnit, vrw, vacc);
       }
     };
-    if (nch > 0) {
+    if (!EARLY && nch > 0) {
       const int32_t v0 = std::min(chunk_of(0), lastv);
       load_value_params<D>(a, unit, v0, la, lc, li, vp);
       load_value_words<BITS, D>(a, unit, v0, lane, vw0);
@@ -1113,23 +1143,57 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
   // the head group's rows hg*NH .. (the unit's heads gq)
   const uint32_t hrows = std::min<uint32_t>(NH, gq - hg * NH);
   float* part = a.ws + (((uint64_t)unit * a.nsplit_total + split_base + split) * gq + hg * NH) * (D + 2);
-  for (uint32_t idx = threadIdx.x; idx < hrows * (D + 2); idx += blockDim.x) {
-    const uint32_t h = idx / (D + 2), d = idx % (D + 2);
-    float M = -INFINITY;
-#pragma unroll
-    for (int wv = 0; wv < 4; ++wv) M = fmaxf(M, lds[wv * NH * (D + 2) + h * (D + 2) + D]);
-    float v = 0.f;
-    if (d == D) {
-      v = M;
-    } else {
+  if constexpr (EARLY) {
+    // wave w writes rows w, w + 4: lane l channels l + 64k, lanes 0 and 1 the row's (m, l),
+    // each wave's weight exp2(m_w - M) computed once per row (fewer dependent LDS reads on
+    // the critical path of a short launch)
+    for (uint32_t h = wave; h < hrows; h += 4) {
+      float mw[4], f[4];
+      float M = -INFINITY;
 #pragma unroll
       for (int wv = 0; wv < 4; ++wv) {
-        const float* c = lds + wv * NH * (D + 2) + h * (D + 2);
-        const float f = c[D] == -INFINITY ? 0.f : exp2f(c[D] - M);
-        v += (d == D + 1 ? c[D + 1] : c[d]) * f;
+        mw[wv] = lds[wv * NH * (D + 2) + h * (D + 2) + D];
+        M = fmaxf(M, mw[wv]);
+      }
+#pragma unroll
+      for (int wv = 0; wv < 4; ++wv) f[wv] = mw[wv] == -INFINITY ? 0.f : exp2f(mw[wv] - M);
+#pragma unroll
+      for (int k = 0; k < HV; ++k) {
+        const uint32_t d = lane + 64 * k;
+        float v = 0.f;
+#pragma unroll
+        for (int wv = 0; wv < 4; ++wv) v += lds[wv * NH * (D + 2) + h * (D + 2) + d] * f[wv];
+        part[h * (D + 2) + d] = v;
+      }
+      if (lane < 2) {
+        float v = M;
+        if (lane == 1) {
+          v = 0.f;
+#pragma unroll
+          for (int wv = 0; wv < 4; ++wv) v += lds[wv * NH * (D + 2) + h * (D + 2) + D + 1] * f[wv];
+        }
+        part[h * (D + 2) + D + lane] = v;
       }
     }
-    part[h * (D + 2) + d] = v;
+  } else {
+    for (uint32_t idx = threadIdx.x; idx < hrows * (D + 2); idx += blockDim.x) {
+      const uint32_t h = idx / (D + 2), d = idx % (D + 2);
+      float M = -INFINITY;
+#pragma unroll
+      for (int wv = 0; wv < 4; ++wv) M = fmaxf(M, lds[wv * NH * (D + 2) + h * (D + 2) + D]);
+      float v = 0.f;
+      if (d == D) {
+        v = M;
+      } else {
+#pragma unroll
+        for (int wv = 0; wv < 4; ++wv) {
+          const float* c = lds + wv * NH * (D + 2) + h * (D + 2);
+          const float f = c[D] == -INFINITY ? 0.f : exp2f(c[D] - M);
+          v += (d == D + 1 ? c[D + 1] : c[d]) * f;
+        }
+      }
+      part[h * (D + 2) + d] = v;
+    }
   }
 }
 
@@ -1144,8 +1208,10 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
 constexpr int fast_min_groups(int bits, int nrs, int d) {
   return d > 128 ? (bits == 2 ? 3 : 2) : (nrs == 1 && bits <= 4) ? 4 : (bits == 8 && nrs == 2) ? 2 : 3;
 }
-template <int BITS, int NRS, int D>
-__global__ void __launch_bounds__(kThreads, fast_min_groups(BITS, NRS, D))
+// SMALL: every wave owns at most one chunk (decode-sized launches): EARLY requests, one
+// chunk's logits of LDS; its register use does not set the occupancy of long launches.
+template <int BITS, int NRS, int D, bool SMALL = false>
+__global__ void __launch_bounds__(kThreads, SMALL ? 2 : fast_min_groups(BITS, NRS, D))
     k_attn_mfma(AttnArgs a) {
   extern __shared__ float lds[];
   // workgroups of (unit, head group) pairs: vu = unit * hgroups + hg. First in the grid, so
@@ -1157,7 +1223,7 @@ __global__ void __launch_bounds__(kThreads, fast_min_groups(BITS, NRS, D))
   if constexpr (D == 128) {
     if (blockIdx.x < nwin) {
       const uint32_t vu = blockIdx.x / a.nsplit_win;
-      mfma_split<BITS, NRS, 1, true, D>(a, vu / a.hgroups, blockIdx.x % a.nsplit_win, vu % a.hgroups, lds);
+      mfma_split<BITS, NRS, 1, true, D, SMALL>(a, vu / a.hgroups, blockIdx.x % a.nsplit_win, vu % a.hgroups, lds);
       return;
     }
   } else {
@@ -1167,7 +1233,11 @@ __global__ void __launch_bounds__(kThreads, fast_min_groups(BITS, NRS, D))
     }
   }
   const uint32_t blk = blockIdx.x - nwin - ngen, vu = blk / a.nsplit_fast;
-  mfma_split<BITS, NRS, fast_cpw(BITS, NRS), false, D>(a, vu / a.hgroups, blk % a.nsplit_fast, vu % a.hgroups, lds);
+  if constexpr (SMALL) {
+    mfma_split<BITS, NRS, 1, false, D, true>(a, vu / a.hgroups, blk % a.nsplit_fast, vu % a.hgroups, lds);
+  } else {
+    mfma_split<BITS, NRS, fast_cpw(BITS, NRS), false, D>(a, vu / a.hgroups, blk % a.nsplit_fast, vu % a.hgroups, lds);
+  }
 }
 
 // Arguments of session s of a batched call: its queries, partials and suffix.
@@ -2234,15 +2304,28 @@ AttnArgs make_args(const AttnProblem& p, float* ws) {
   return a;
 }
 
+// A launch whose waves own at most one packed chunk each (at head_dim 128, where the window
+// chunks are MIXED workgroups of one chunk anyway) takes the SMALL instantiation.
+bool small_launch(const AttnArgs& a) {
+  return a.c.geo.D == 128 && a.gq <= 4 && (uint64_t)a.nsplit_fast * 4 >= a.chunk_end - a.chunk_begin;
+}
+
 template <int BITS, int NRS, int D>
 hipError_t launch_fast(const AttnArgs& a, double bytes, hipStream_t stream) {
   constexpr int NH = 4 * NRS;
-  const size_t logits = (size_t)4 * NH * ((a.nsplit_fast > 0 ? fast_cpw(BITS, NRS) : 1) * 64 + kRowPad);
+  const bool small = D == 128 && NRS == 1 && small_launch(a);
+  const size_t logits = (size_t)4 * NH * ((a.nsplit_fast > 0 && !small ? fast_cpw(BITS, NRS) : 1) * 64 + kRowPad);
   const size_t combine = (size_t)4 * NH * (D + 2);
   const size_t gen = a.nsplit_gen > 0 ? (size_t)a.gq * (D + a.S) : 0;  // generic splits' q and weights
   const size_t lds = std::max(std::max(logits, combine), gen) * sizeof(float);
   TimedLaunch timed(KIVI_KERNEL_ATTN_PACKED, stream, bytes);
   const uint32_t grid = a.units * (a.hgroups * (a.nsplit_win + a.nsplit_fast) + a.nsplit_gen);
+  if constexpr (D == 128 && NRS == 1) {
+    if (small) {
+      k_attn_mfma<BITS, NRS, D, true><<<grid, kThreads, lds, stream>>>(a);
+      return hipGetLastError();
+    }
+  }
   k_attn_mfma<BITS, NRS, D><<<grid, kThreads, lds, stream>>>(a);
   return hipGetLastError();
 }
