@@ -163,9 +163,29 @@ __device__ __forceinline__ float value_at(const AttnArgs& a, uint32_t unit, uint
   return fmaf(fmaf(code, sz.x, sz.y), m, dense * (1.f - m));  // exact for m in {0, 1}
 }
 
-__device__ __forceinline__ float warp_max(float v) {
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+// DPP exchanges inside rows of 16 lanes (every lane active): quad_perm xor 1 and xor 2, then
+// the mirrors that pair each lane with the other half of its 8- and 16-lane group.
+template <int CTRL>
+__device__ __forceinline__ float dpp_row(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+// max (MAX) or min over each 16-lane row, in every lane of the row
+template <bool MAX>
+__device__ __forceinline__ float row_reduce(float v) {
+  v = MAX ? fmaxf(v, dpp_row<0xB1>(v)) : fminf(v, dpp_row<0xB1>(v));
+  v = MAX ? fmaxf(v, dpp_row<0x4E>(v)) : fminf(v, dpp_row<0x4E>(v));
+  v = MAX ? fmaxf(v, dpp_row<0x141>(v)) : fminf(v, dpp_row<0x141>(v));
+  v = MAX ? fmaxf(v, dpp_row<0x140>(v)) : fminf(v, dpp_row<0x140>(v));
   return v;
+}
+__device__ __forceinline__ float lane_value(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+// max over the wave (every lane active): rows by DPP, then the four rows' maxima by readlane,
+// in place of six dependent LDS-path shuffles
+__device__ __forceinline__ float warp_max(float v) {
+  v = row_reduce<true>(v);
+  return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
 }
 __device__ __forceinline__ float warp_sum(float v) {
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
@@ -795,14 +815,13 @@ __device__ __forceinline__ uint32_t evict_code(float x, float zero, float scale,
 __device__ __forceinline__ void evict_groups(EvictRow& e, float levels, float& smax, float& amax) {
   smax = 0.f;
   amax = 0.f;
+  const bool low = __lane_id() < 32;
 #pragma unroll
   for (int hv = 0; hv < 2; ++hv) {
-    float mn = e.x[hv], mx = e.x[hv];
-#pragma unroll
-    for (int o = 1; o < 32; o <<= 1) {
-      mn = fminf(mn, __shfl_xor(mn, o));
-      mx = fmaxf(mx, __shfl_xor(mx, o));
-    }
+    // min and max over each half-wave: rows by DPP, then the half's two rows by readlane
+    float mn = row_reduce<false>(e.x[hv]), mx = row_reduce<true>(e.x[hv]);
+    mn = low ? fminf(lane_value(mn, 0), lane_value(mn, 16)) : fminf(lane_value(mn, 32), lane_value(mn, 48));
+    mx = low ? fmaxf(lane_value(mx, 0), lane_value(mx, 16)) : fmaxf(lane_value(mx, 32), lane_value(mx, 48));
     const float fz = lane_group_first_zero(e.x[hv], 32);  // a zero minimum: the first zero's sign
     if (mn == 0.f) mn = fz;
     const float span = mx - mn;
@@ -811,8 +830,8 @@ __device__ __forceinline__ void evict_groups(EvictRow& e, float levels, float& s
     smax = fmaxf(smax, e.sc[hv]);
     amax = fmaxf(amax, fmaxf(fabsf(mn), fabsf(mx)));
   }
-  smax = fmaxf(smax, __shfl_xor(smax, 32));
-  amax = fmaxf(amax, __shfl_xor(amax, 32));
+  smax = fmaxf(lane_value(smax, 0), lane_value(smax, 32));
+  amax = fmaxf(lane_value(amax, 0), lane_value(amax, 32));
 }
 
 // One workgroup = 4 waves; wave w of split s owns packed chunks [s*4*CPW + w*CPW, +CPW) of its
