@@ -261,18 +261,24 @@ def run_cpu_baseline(kivi, name):
 # ------------------------------------------------------------------ GPU measurement helpers
 
 
+TRAFFIC_MATCH = 0.02  # relative difference of algorithmic bytes a traffic record still covers
+
+
 def recorded_traffic(kernel, workload, bytes_per_launch):
     """HBM bytes per launch of `kernel` on `workload` from profiles/traffic.json, if that
-    record was measured at the same algorithmic bytes per launch."""
+    record was measured at the same algorithmic bytes per launch, within TRAFFIC_MATCH (a
+    decode workload's mean bytes per launch move with the number of steps), scaled by the
+    ratio of the two."""
     path = ROOT / "profiles" / "traffic.json"
     try:
         records = json.loads(path.read_text())
     except (OSError, ValueError):
         return None
     for r in records.get("records", []):
-        if (r.get("kernel") == kernel and r.get("workload") == workload
-                and abs(r.get("algorithmic_bytes_per_launch", -1) - bytes_per_launch) < 1.0):
-            return r
+        algo = r.get("algorithmic_bytes_per_launch", -1)
+        if (r.get("kernel") == kernel and r.get("workload") == workload and algo > 0
+                and abs(algo - bytes_per_launch) <= TRAFFIC_MATCH * algo):
+            return dict(r, hbm_bytes_per_launch=r["hbm_bytes_per_launch"] * bytes_per_launch / algo)
     return None
 
 
