@@ -24,10 +24,11 @@ its clocks have ramped up (`clock_warmup_calls`). Caches smaller than three time
 Infinity Cache rotate over identical copies between steps (`cache_copies`), so each step reads
 HBM; C0 and C1 are too small for that and report `cache_resident: true`.
 
-`roofline` is for the dominant kernel: the packed-chunk attention kernel (k_attn_mfma, HBM
-bound: algorithmic bytes per launch over its mean launch duration), or for c4 the shared-prefix
-GEMM kernel (k_attn_shared, matrix-core bound: 4*D flops per (session row, prefix token) over
-its mean duration, against the dense f16 MFMA peak). `traffic` is that kernel's HBM bytes per
+`roofline` is for the dominant kernel: the packed-chunk attention kernel (k_attn_mfma, or
+k_attn_wide for the eight-head units of c3; HBM bound: algorithmic bytes per launch over its
+mean launch duration), or for c4 the shared-prefix GEMM kernel (k_attn_shared, matrix-core
+bound: 4*D flops per (session row, prefix token) over its mean duration, against the dense
+f16 MFMA peak). `traffic` is that kernel's HBM bytes per
 launch from rocprofv3 FETCH_SIZE + WRITE_SIZE runs calibrated on a plain copy kernel
 (--copy-calibration), as recorded in profiles/traffic.json; null when no record matches the
 kernel, workload and algorithmic bytes.
@@ -532,7 +533,10 @@ def measure(name, args, torch, kivi, amd, stream, with_cpu):
     if sessions_cfg and "attn_shared" in kernels:
         dom_fam, dom_name = "attn_shared", "k_attn_shared"
     elif "attn_packed" in kernels:
-        dom_fam, dom_name = "attn_packed", "k_attn_mfma"
+        # eight-head units (GQA 5..8 and head groups of 8) at head_dim 128, G = 32 run their
+        # packed chunks on the 16x16x32 kernel
+        wide = dim == 128 and G == 32 and qh // heads > 4
+        dom_fam, dom_name = "attn_packed", "k_attn_wide" if wide else "k_attn_mfma"
     elif "attn_sessions" in kernels:
         dom_fam, dom_name = "attn_sessions", "k_attn_sessions"
     else:

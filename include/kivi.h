@@ -319,8 +319,10 @@ kivi_status kivi_runtime_decode(kivi_runtime* rt, const float* key, size_t key_l
                                 size_t query_len, size_t num_q_heads, float scale, float* out,
                                 size_t out_len, kivi_error* err);
 /* The same on device pointers, enqueued on `stream` (inputs read by the enqueued work). A step
-   without a key flush due runs as one attention launch that carries the append, plus the
-   merge launch; the result is bit for bit that of append then attention. */
+   without a key flush due runs, at head_dim 128, G = 32 and up to four query heads per KV head,
+   as one attention launch that carries the append, plus the merge launch; other steps run as
+   the append and then the attention. Either way the result is bit for bit that of append then
+   attention. */
 kivi_status kivi_runtime_decode_device(kivi_runtime* rt, const float* key, size_t key_len,
                                        const float* value, size_t value_len, const float* query,
                                        size_t query_len, size_t num_q_heads, float scale,

@@ -81,6 +81,7 @@ struct AttnArgs {
   // (unit, head group, split), each writing its group's partial rows
   uint32_t hgroups;
   uint32_t gshift;         // log2(G) on the matrix-core path (G = 32, 64 or 128 there)
+  uint32_t wide;           // packed splits on the eight-head 16x16x32 kernel (k_attn_wide)
   float* ws;               // [units][nsplit_total][gq][D+2]
   // batched sessions (0 otherwise): session count and the strides between consecutive
   // sessions' queries, partials and outputs
@@ -1259,6 +1260,377 @@ __global__ void __launch_bounds__(kThreads, SMALL ? 2 : fast_min_groups(BITS, NR
   }
 }
 
+// ------------------------------------------------------------------ eight-head 16x16x32 path
+// Packed chunks of eight-head units (GQA 5..8, and head groups of 8 above) at head_dim 128,
+// G = 32, on v_mfma_f32_16x16x32_f16. Per issue cycle it does four times the multiply-adds of
+// the 4x4x4 broadcast form, and vector instructions of other waves issue while it runs (the
+// 4x4x4 form holds them off); the decode kernels are bound by the two streams together.
+//
+// Lane l = 16g + n; D (4 VGPRs) holds rows 4g .. 4g+3 of column n of a 16x16 tile.
+// Keys: rows = 16 tokens (tile mt: tokens 16mt .. +15), columns = (head n%8, key group n/8 of
+// the chunk), K = channels with hi and lo halves: K-tile kt gives lane group g the channels
+// 32g + 4kt .. +3, its eight K slots the hi then the lo halves of q*scale (B operand) against
+// the same four codes twice (A operand). A tile's tokens lie in one key group: the other
+// group's columns are computed and dropped.
+// Values: rows = 16 channels (tile mt: channels 16mt .. +15, value group mt/2), columns =
+// (head n%8, parity n/8 of the value group), K = tokens with hi and lo halves: K-tile kt gives
+// lane group g the tokens 16g + 4kt .. +3; the other parity's columns are dropped.
+// A chunk's (scale, zero) pairs are staged in LDS, from which the eight lanes of a head
+// column set read them as broadcasts (no cross-lane moves on the vector ALU).
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+
+constexpr int kWideCpw = 8;       // chunks per wave (LDS: two workgroups per CU)
+constexpr int kWideHeads = 8;     // heads per workgroup (one head group)
+// One chunk's (scale, zero) pairs staged per wave, as stored: keys [group][channel][2],
+// values [group][token][2]. (A layout padded so that the eight addresses of a broadcast read
+// fall in disjoint banks measured no faster.)
+constexpr int kWideStage = 512;   // floats per wave
+
+__device__ __forceinline__ v4f mfma_wide(h8 a, h8 b, v4f c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ h8 twice(h4 x) { return h8{x[0], x[1], x[2], x[3], x[0], x[1], x[2], x[3]}; }
+__device__ __forceinline__ h8 join(h4 x, h4 y) { return h8{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]}; }
+
+// One chunk's code words for the lane. Keys: tile mt's token 16mt + n, words BITS*g .. +BITS-1
+// of its row (channels 32g .. 32g+31). Values: tile mt's channel 16mt + n, words
+// (BITS/2)*g .. of its 64-token block (tokens 16g .. 16g+15).
+template <int BITS>
+struct WideKeyWords {
+  uint32_t w[4][BITS];
+};
+template <int BITS>
+struct WideValueWords {
+  uint32_t w[8][BITS / 2];
+};
+
+template <int BITS>
+__device__ __forceinline__ void wide_load_keys(const AttnArgs& a, uint32_t unit, uint32_t ch, uint32_t g,
+                                               uint32_t n, WideKeyWords<BITS>& kw) {
+  constexpr int KW = 4 * BITS;  // words per token at head_dim 128
+  const uint32_t* base = a.c.kcodes + unit * a.c.geo.kcodes_unit() + ((uint64_t)ch * 64 + n) * KW + BITS * g;
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+    const uint32_t* p = base + 16 * mt * KW;
+    if constexpr (BITS == 2) {
+      const uint2 x = *reinterpret_cast<const uint2*>(p);
+      kw.w[mt][0] = x.x;
+      kw.w[mt][1] = x.y;
+    } else {
+      load_words<BITS>(p, kw.w[mt]);
+    }
+  }
+}
+template <int BITS>
+__device__ __forceinline__ void wide_load_values(const AttnArgs& a, uint32_t unit, uint32_t tb, uint32_t g,
+                                                 uint32_t n, WideValueWords<BITS>& vw) {
+  constexpr int VW = 2 * BITS, VG = BITS / 2;  // words per channel per block; the lane's share
+  const uint32_t* base = a.c.vcodes + unit * a.c.geo.vcodes_unit() + ((uint64_t)tb * 128 + n) * VW + VG * g;
+#pragma unroll
+  for (int mt = 0; mt < 8; ++mt) {
+    const uint32_t* p = base + 16 * mt * VW;
+    if constexpr (VG == 1) {
+      vw.w[mt][0] = p[0];
+    } else if constexpr (VG == 2) {
+      const uint2 x = *reinterpret_cast<const uint2*>(p);
+      vw.w[mt][0] = x.x;
+      vw.w[mt][1] = x.y;
+    } else {
+      load_words<VG>(p, vw.w[mt]);
+    }
+  }
+}
+// the lane's share of a chunk's (scale, zero) pairs, as stored: keys, group lane/32 of the
+// chunk, channels 4*(lane%32) .. +3; values, group lane/16, tokens 4*(lane%16) .. +3
+__device__ __forceinline__ void wide_load_key_params(const AttnArgs& a, uint32_t unit, uint32_t ch, uint32_t lane,
+                                                     float4& p0, float4& p1) {
+  const float4* p = reinterpret_cast<const float4*>(
+      a.c.kparams + unit * a.c.geo.kparams_unit() + ((uint64_t)(2 * ch + lane / 32) * 128 + 4 * (lane % 32)) * 2);
+  p0 = p[0];
+  p1 = p[1];
+}
+__device__ __forceinline__ void wide_load_value_params(const AttnArgs& a, uint32_t unit, uint32_t tb,
+                                                       uint32_t lane, float4& p0, float4& p1) {
+  const float4* p = reinterpret_cast<const float4*>(
+      a.c.vparams + unit * a.c.geo.vparams_unit() + (((uint64_t)tb * 4 + lane / 16) * 64 + 4 * (lane % 16)) * 2);
+  p0 = p[0];
+  p1 = p[1];
+}
+// The lane's eight floats (four (scale, zero) pairs, as loaded) at 8*lane.
+__device__ __forceinline__ void wide_stage(float* stage, uint32_t lane, float4 p0, float4 p1) {
+  float4* s = reinterpret_cast<float4*>(stage + 8 * lane);
+  s[0] = p0;
+  s[1] = p1;
+}
+
+// A operand of tile mt, K-tile kt: the four codes of the lane's K slots, twice.
+template <int BITS>
+__device__ __forceinline__ h8 wide_key_codes(const WideKeyWords<BITS>& kw, int mt, int kt) {
+  // channels 32g + 4kt .. +3: word (32g + 4kt) / PPW of the token, elements 4*(kt % (PPW/4)) ..
+  if constexpr (BITS == 2) return twice(codes4<2>(kw.w[mt][kt / 4], kt % 4));
+  else if constexpr (BITS == 4) return twice(codes4<4>(kw.w[mt][kt / 2], kt % 2));
+  else return twice(codes4<8>(kw.w[mt][kt], 0));
+}
+template <int BITS>
+__device__ __forceinline__ h8 wide_value_codes(const WideValueWords<BITS>& vw, int mt, int kt) {
+  // tokens 16g + 4kt .. +3 of the channel: word (16g + 4kt) / PPW of the block
+  if constexpr (BITS == 2) return twice(codes4<2>(vw.w[mt][0], kt));
+  else if constexpr (BITS == 4) return twice(codes4<4>(vw.w[mt][kt / 2], kt % 2));
+  else return twice(codes4<8>(vw.w[mt][kt], 0));
+}
+
+// B operand from four products: hi halves then lo halves (x below 2^15 in magnitude)
+__device__ __forceinline__ h8 wide_split4(const float (&x)[4]) {
+  h4 hi, lo;
+  split4(x, hi, lo);
+  return join(hi, lo);
+}
+
+template <int BITS>
+__device__ __forceinline__ void wide_split(const AttnArgs& a, uint32_t unit, uint32_t split, uint32_t hg,
+                                           float* lds) {
+  constexpr int CPW = kWideCpw, NH = kWideHeads, D = 128;
+  constexpr int ROW = CPW * 64 + kRowPad;
+  constexpr int kExp = CodeUnit<BITS>::kExp;
+  constexpr float kUnit = kExp == 0 ? 1.0f : kExp == -1 ? 0.5f : 0.001953125f;
+  const uint32_t b = unit / a.heads, kvh = unit % a.heads;
+  const uint32_t lane = threadIdx.x % 64, wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+  const uint32_t g = lane / 16, n = lane % 16;
+  const uint32_t hq = n % 8;   // head of the lane's column
+  const uint32_t sel = n / 8;  // key group of the chunk (keys) / value group parity (values)
+  const uint32_t gq = a.gq;
+  float* wl = lds + wave * (NH * ROW + kWideStage);  // this wave's logits [NH][ROW]
+  float* stage = wl + NH * ROW;                       // and (scale, zero) staging
+
+  // chunks dealt round-robin over the unit's waves, as in the 4x4x4 path
+  const int32_t slots = static_cast<int32_t>(a.nsplit_fast * 4);
+  const int32_t slot = static_cast<int32_t>(split * 4 + wave);
+  const int32_t span = static_cast<int32_t>(a.chunk_end - a.chunk_begin);
+  const int32_t nch = std::min<int32_t>(CPW, std::max<int32_t>(0, (span - slot + slots - 1) / slots));
+  // (every owned chunk is packed in keys and values: chunk_end <= min(kq, vq) / 64)
+  auto chunk_of = [&](int32_t k) { return static_cast<int32_t>(a.chunk_begin) + slot + k * slots; };
+
+  // one chunk ahead (two ahead measured slower): two buffers of code words; one of (scale,
+  // zero) pairs, staged to LDS before the next chunk's are requested into it
+  WideKeyWords<BITS> kw0, kw1;
+  float4 kp0, kp1;
+  if (nch > 0) {
+    wide_load_key_params(a, unit, chunk_of(0), lane, kp0, kp1);
+    wide_load_keys<BITS>(a, unit, chunk_of(0), g, n, kw0);
+  }
+  // q in base-2 logit units: head hg*8 + hq, channels 32g .. 32g+31 (0 for padded heads)
+  float qv[32];
+  float qmax = 0.f;
+  {
+    const uint32_t h = hg * NH + hq;
+    const float s = h < gq ? a.scale2 : 0.f;
+    const float* qp = a.query + ((uint64_t)b * a.qh + kvh * gq + min(h, gq - 1)) * D + 32 * g;
+#pragma unroll
+    for (int r = 0; r < 32; r += 4) {
+      const float4 v = *reinterpret_cast<const float4*>(qp + r);
+      qv[r] = v.x * s;
+      qv[r + 1] = v.y * s;
+      qv[r + 2] = v.z * s;
+      qv[r + 3] = v.w * s;
+    }
+#pragma unroll
+    for (int r = 0; r < 32; ++r) qmax = fmaxf(qmax, fabsf(qv[r]));
+  }
+  // power-of-two operand ranges from the unit's largest scales, as in the 4x4x4 path
+  qmax = warp_max(qmax);
+  const float kmax = __uint_as_float(a.c.smax[4 * unit]);
+  const int ek = std::min(60, std::max(-100, 15 - __builtin_amdgcn_frexp_expf(qmax * kmax)));
+  const float kfac = ldexpf(1.f, ek);
+  const float kout = ldexpf(1.f, -ek - kExp);
+#pragma unroll
+  for (int r = 0; r < 32; ++r) qv[r] *= kfac;
+
+  // ---------------- phase 1: logits of every owned chunk into LDS (scaled by 2^(ek+kExp))
+  float mx = -INFINITY;
+  {
+    auto step = [&](int k, const WideKeyWords<BITS>& cur, WideKeyWords<BITS>& next) {
+      // this chunk's (scale, zero) pairs to LDS (after the previous chunk's reads of them),
+      // then the next chunk's requested (the last step re-reads an L2-resident chunk)
+      wide_stage(stage, lane, kp0, kp1);
+      const int32_t kn = chunk_of(std::min(k + 1, nch - 1));
+      wide_load_key_params(a, unit, kn, lane, kp0, kp1);
+      wide_load_keys<BITS>(a, unit, kn, g, n, next);
+      v4f acc[4];
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) acc[mt] = v4f{0.f, 0.f, 0.f, 0.f};
+      float bias = 0.f;
+#pragma unroll
+      for (int kt = 0; kt < 8; ++kt) {
+        const float4* sp = reinterpret_cast<const float4*>(stage + (sel * 128 + 32 * g + 4 * kt) * 2);
+        const float4 s01 = sp[0], s23 = sp[1];
+        const float p[4] = {qv[4 * kt] * s01.x, qv[4 * kt + 1] * s01.z, qv[4 * kt + 2] * s23.x,
+                            qv[4 * kt + 3] * s23.z};
+        bias = fmaf(qv[4 * kt], s01.y, bias);
+        bias = fmaf(qv[4 * kt + 1], s01.w, bias);
+        bias = fmaf(qv[4 * kt + 2], s23.y, bias);
+        bias = fmaf(qv[4 * kt + 3], s23.w, bias);
+        const h8 B = wide_split4(p);
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) acc[mt] = mfma_wide(wide_key_codes<BITS>(cur, mt, kt), B, acc[mt]);
+      }
+      // the zero term of the lane's column over all 128 channels (lane groups g)
+      bias += __shfl_xor(bias, 16);
+      bias += __shfl_xor(bias, 32);
+      const float bu = bias * kUnit;
+      // the lane's column is live for the two tiles of its key group: tokens 32*sel + 16*m2 + 4g ..
+#pragma unroll
+      for (int m2 = 0; m2 < 2; ++m2) {
+        const v4f v = sel ? acc[2 + m2] : acc[m2];
+        const float4 o = make_float4(v[0] + bu, v[1] + bu, v[2] + bu, v[3] + bu);
+        *reinterpret_cast<float4*>(wl + hq * ROW + k * 64 + 32 * sel + 16 * m2 + 4 * g) = o;
+        mx = fmaxf(mx, fmaxf(fmaxf(o.x, o.y), fmaxf(o.z, o.w)));
+      }
+    };
+    for (int k = 0; k < nch; k += 2) {
+      step(k, kw0, kw1);
+      if (k + 1 < nch) step(k + 1, kw1, kw0);
+    }
+  }
+  // wave max per head: the lanes of head hq (both key groups, four lane groups)
+  mx = fmaxf(mx, __shfl_xor(mx, 8));
+  mx = fmaxf(mx, __shfl_xor(mx, 16));
+  mx = fmaxf(mx, __shfl_xor(mx, 32));
+  const float mrow = mx * kout;
+
+  const float vmax = __uint_as_float(a.c.smax[4 * unit + 1]);
+  const int ev = std::min(60, std::max(-100, 15 - __builtin_amdgcn_frexp_expf(vmax)));
+  const float vout = ldexpf(1.f, -ev - kExp);
+  const float moff = mrow == -INFINITY ? 0.f : mrow;
+  const float evoff = static_cast<float>(ev) - moff;  // weights times 2^ev from the exponential
+  const float vinv = ldexpf(1.f, -ev);
+
+  // ---------------- phase 2: value mix
+  v4f vacc[8];
+#pragma unroll
+  for (int mt = 0; mt < 8; ++mt) vacc[mt] = v4f{0.f, 0.f, 0.f, 0.f};
+  float zacc[2] = {0.f, 0.f};  // zero terms of value groups sel, 2 + sel
+  float lsum = 0.f;
+  {
+    WideValueWords<BITS> vw0, vw1;
+    float4 vp0, vp1;
+    if (nch > 0) {
+      wide_load_value_params(a, unit, chunk_of(0), lane, vp0, vp1);
+      wide_load_values<BITS>(a, unit, chunk_of(0), g, n, vw0);
+    }
+    auto step = [&](int k, const WideValueWords<BITS>& cur, WideValueWords<BITS>& next) {
+      wide_stage(stage, lane, vp0, vp1);
+      const int32_t kn = chunk_of(std::min(k + 1, nch - 1));
+      wide_load_value_params(a, unit, kn, lane, vp0, vp1);
+      wide_load_values<BITS>(a, unit, kn, g, n, next);
+      // weights (times 2^ev) of head hq, tokens 16g .. 16g+15
+      float w[16];
+      {
+        const float4* lp = reinterpret_cast<const float4*>(wl + hq * ROW + k * 64 + 16 * g);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float4 x = lp[r];
+          w[4 * r] = __builtin_amdgcn_exp2f(fmaf(x.x, kout, evoff));
+          w[4 * r + 1] = __builtin_amdgcn_exp2f(fmaf(x.y, kout, evoff));
+          w[4 * r + 2] = __builtin_amdgcn_exp2f(fmaf(x.z, kout, evoff));
+          w[4 * r + 3] = __builtin_amdgcn_exp2f(fmaf(x.w, kout, evoff));
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) lsum += w[r];
+      }
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+#pragma unroll
+        for (int pr = 0; pr < 2; ++pr) {
+          // value group 2*pr + sel, tokens 16g + 4kt .. +3
+          const float4* sp = reinterpret_cast<const float4*>(stage + ((2 * pr + sel) * 64 + 16 * g + 4 * kt) * 2);
+          const float4 s01 = sp[0], s23 = sp[1];
+          const float p[4] = {w[4 * kt] * s01.x, w[4 * kt + 1] * s01.z, w[4 * kt + 2] * s23.x,
+                              w[4 * kt + 3] * s23.z};
+          zacc[pr] = fmaf(w[4 * kt], s01.y, zacc[pr]);
+          zacc[pr] = fmaf(w[4 * kt + 1], s01.w, zacc[pr]);
+          zacc[pr] = fmaf(w[4 * kt + 2], s23.y, zacc[pr]);
+          zacc[pr] = fmaf(w[4 * kt + 3], s23.w, zacc[pr]);
+          const h8 B = wide_split4(p);
+#pragma unroll
+          for (int mm = 0; mm < 4; ++mm)
+            vacc[4 * pr + mm] = mfma_wide(wide_value_codes<BITS>(cur, 4 * pr + mm, kt), B, vacc[4 * pr + mm]);
+        }
+      }
+    };
+    for (int k = 0; k < nch; k += 2) {
+      step(k, vw0, vw1);
+      if (k + 1 < nch) step(k + 1, vw1, vw0);
+    }
+  }
+
+  // ---------------- wave partial: sums over the lane groups, then the output rows
+  lsum += __shfl_xor(lsum, 16);
+  lsum += __shfl_xor(lsum, 32);
+#pragma unroll
+  for (int pr = 0; pr < 2; ++pr) {
+    zacc[pr] += __shfl_xor(zacc[pr], 16);
+    zacc[pr] += __shfl_xor(zacc[pr], 32);
+  }
+  __syncthreads();  // every wave is done with its logits; reuse LDS for the combine
+  float* cw = lds + wave * NH * (D + 2);
+  // the lane's column is live for the tiles of parity sel: tiles 4*pr + 2*sel + m2, channels
+  // 16 * tile + 4g .. +3
+#pragma unroll
+  for (int pr = 0; pr < 2; ++pr) {
+    const float z = zacc[pr] * vinv;
+#pragma unroll
+    for (int m2 = 0; m2 < 2; ++m2) {
+      const v4f v = sel ? vacc[4 * pr + 2 + m2] : vacc[4 * pr + m2];
+      const uint32_t c0 = 16 * (4 * pr + 2 * sel + m2) + 4 * g;
+      float2* o = reinterpret_cast<float2*>(cw + hq * (D + 2) + c0);
+      o[0] = make_float2(fmaf(v[0], vout, z), fmaf(v[1], vout, z));
+      o[1] = make_float2(fmaf(v[2], vout, z), fmaf(v[3], vout, z));
+    }
+  }
+  if (g == 0 && sel == 0) {
+    cw[hq * (D + 2) + D] = nch > 0 ? mrow : -INFINITY;
+    cw[hq * (D + 2) + D + 1] = nch > 0 ? lsum * vinv : 0.f;
+  }
+  __syncthreads();
+  const uint32_t hrows = std::min<uint32_t>(NH, gq - hg * NH);
+  float* part = a.ws + (((uint64_t)unit * a.nsplit_total + split) * gq + hg * NH) * (D + 2);
+  for (uint32_t idx = threadIdx.x; idx < hrows * (D + 2); idx += blockDim.x) {
+    const uint32_t h = idx / (D + 2), d = idx % (D + 2);
+    float M = -INFINITY;
+#pragma unroll
+    for (int wv = 0; wv < 4; ++wv) M = fmaxf(M, lds[wv * NH * (D + 2) + h * (D + 2) + D]);
+    float v = 0.f;
+    if (d == D) {
+      v = M;
+    } else {
+#pragma unroll
+      for (int wv = 0; wv < 4; ++wv) {
+        const float* c = lds + wv * NH * (D + 2) + h * (D + 2);
+        const float f = c[D] == -INFINITY ? 0.f : exp2f(c[D] - M);
+        v += (d == D + 1 ? c[D + 1] : c[d]) * f;
+      }
+    }
+    part[h * (D + 2) + d] = v;
+  }
+}
+
+// Eight-head launch at head_dim 128, G = 32: the window / suffix chunk workgroups first (the
+// 4x4x4 MIXED path), then the packed splits on the 16x16x32 path. Two workgroups per CU fit
+// the LDS of eight chunks' logits; the register budget of three (168 VGPRs, no spills) measured
+// faster than that of two, and requests two chunks ahead slower than one.
+template <int BITS>
+__global__ void __launch_bounds__(kThreads, 3) k_attn_wide(AttnArgs a) {
+  extern __shared__ float lds[];
+  const uint32_t nwin = a.units * a.hgroups * a.nsplit_win;
+  if (blockIdx.x < nwin) {
+    const uint32_t vu = blockIdx.x / a.nsplit_win;
+    mfma_split<BITS, 2, 1, true, 128>(a, vu / a.hgroups, blockIdx.x % a.nsplit_win, vu % a.hgroups, lds);
+    return;
+  }
+  const uint32_t blk = blockIdx.x - nwin, vu = blk / a.nsplit_fast;
+  wide_split<BITS>(a, vu / a.hgroups, blk % a.nsplit_fast, vu % a.hgroups, lds);
+}
+
 // Arguments of session s of a batched call: its queries, partials and suffix.
 __device__ __forceinline__ AttnArgs session_args(const AttnArgs& a, const SessionTable& t,
                                                  uint32_t s) {
@@ -2253,6 +2625,11 @@ bool fast_eligible(const AttnProblem& p) {
 }
 // MFMA row sets (4 heads each) per workgroup, and the head groups of a unit
 int fast_nrs(uint32_t D, uint32_t gq) { return D > 128 || gq <= 4 ? 1 : 2; }
+// Eight-head groups at head_dim 128 and G = 32 take the 16x16x32 kernel for their packed chunks.
+bool wide_shape(const AttnProblem& p) {
+  const uint32_t gq = p.qh / p.heads;
+  return fast_eligible(p) && p.cache.geo.D == 128 && p.cache.geo.G == 32 && fast_nrs(128, gq) == 2;
+}
 uint32_t head_groups(uint32_t D, uint32_t gq) {
   const uint32_t per = 4u * static_cast<uint32_t>(fast_nrs(D, gq));
   return (gq + per - 1) / per;
@@ -2294,11 +2671,15 @@ AttnArgs make_args(const AttnProblem& p, float* ws) {
   a.win_end = fast_win ? static_cast<uint32_t>((a.total + 63) / 64) : a.chunk_end;
   a.hgroups = fast ? head_groups(p.cache.geo.D, a.gq) : 1u;
   a.gshift = fast ? static_cast<uint32_t>(__builtin_ctz(p.cache.geo.G)) : 5u;
-  // packed splits per unit: at most kFastCpw chunks per wave, at least one, and at least
-  // kFastGroups workgroups (over units and head groups) when the chunks allow
+  // a launch that also appends a decode token keeps the 4x4x4 kernel (it quantizes the
+  // evicted window row); such launches are not made for these shapes (attention_fuses_decode)
+  a.wide = fast && wide_shape(p) && a.pend_evict == 0 ? 1u : 0u;
+  // packed splits per unit: at most kFastCpw (kWideCpw) chunks per wave, at least one, and at
+  // least kFastGroups workgroups (over units and head groups) when the chunks allow
   {
     const uint32_t units = p.cache.geo.units * a.hgroups;
-    const uint32_t cpw = static_cast<uint32_t>(fast_cpw(static_cast<int>(p.cache.geo.bits), fast_nrs(p.cache.geo.D, a.gq)));
+    const uint32_t cpw = a.wide ? static_cast<uint32_t>(kWideCpw)
+                                : static_cast<uint32_t>(fast_cpw(static_cast<int>(p.cache.geo.bits), fast_nrs(p.cache.geo.D, a.gq)));
     const uint32_t fewest = (a.chunk_end + 4 * cpw - 1) / (4 * cpw);
     const uint32_t most = (a.chunk_end + 3) / 4;
     a.nsplit_fast = std::min(most, std::max(fewest, (kFastGroups + units - 1) / units));
@@ -2339,6 +2720,15 @@ hipError_t launch_fast(const AttnArgs& a, double bytes, hipStream_t stream) {
   const size_t lds = std::max(std::max(logits, combine), gen) * sizeof(float);
   TimedLaunch timed(KIVI_KERNEL_ATTN_PACKED, stream, bytes);
   const uint32_t grid = a.units * (a.hgroups * (a.nsplit_win + a.nsplit_fast) + a.nsplit_gen);
+  if constexpr (D == 128 && NRS == 2) {
+    if (a.wide) {
+      const size_t wide = (size_t)4 * (kWideHeads * (kWideCpw * 64 + kRowPad) + kWideStage);
+      const size_t mixed = (size_t)4 * NH * (64 + kRowPad);
+      const size_t wlds = std::max(std::max(wide, mixed), combine) * sizeof(float);
+      k_attn_wide<BITS><<<grid, kThreads, wlds, stream>>>(a);
+      return hipGetLastError();
+    }
+  }
   if constexpr (D == 128 && NRS == 1) {
     if (small) {
       k_attn_mfma<BITS, NRS, D, true><<<grid, kThreads, lds, stream>>>(a);
@@ -2425,11 +2815,13 @@ hipError_t launch_fill_zero(float* out, size_t n, hipStream_t stream) {
 }
 
 // The decode fused into the attention launch quantizes the evicted window token with the
-// 32-channel value groups of one half-wave, once per chunk workgroup: G = 32, one head group.
+// 32-channel value groups of one half-wave, once per chunk workgroup: G = 32, one head group
+// of up to four heads (eight-head units take the 16x16x32 kernel, which does not append: their
+// decode is an append launch and an attention launch, bit for bit the same as those calls).
 bool attention_fuses_decode(const AttnProblem& p) {
   const AttnArgs a = make_args(p, nullptr);
   return a.total > 0 && a.nsplit_gen == 0 && (a.nsplit_fast > 0 || a.nsplit_win > 0) &&
-         p.cache.geo.D == 128 && p.cache.geo.G == 32 && a.hgroups == 1;
+         p.cache.geo.D == 128 && p.cache.geo.G == 32 && a.hgroups == 1 && !wide_shape(p);
 }
 
 size_t attention_workspace_floats(const AttnProblem& p) {

@@ -126,6 +126,33 @@ def test_other_shapes_attention_parity(amd, oracle, dim, group, gqa, bits):
     assert max_abs(got, dense_attend(kh, vh, q, batch, heads, heads * gqa, seq, dim, scale)) < 1e-4
 
 
+@pytest.mark.parametrize("bits,gqa,batch,heads,seq", [
+    (2, 5, 1, 2, 200), (4, 6, 2, 1, 777), (8, 7, 1, 2, 2600), (4, 8, 1, 3, 4321), (2, 8, 2, 2, 9000),
+    (8, 12, 1, 2, 5000), (4, 16, 1, 1, 3000)])
+def test_eight_head_units_attention_parity(amd, oracle, bits, gqa, batch, heads, seq):
+    """Eight-head units at head_dim 128 and G = 32 (GQA 5..8, and head groups of eight above)
+    take the 16x16x32 kernel for their packed chunks: padded heads (GQA 5..7), a short last
+    head group (GQA 12), waves that own fewer chunks than they hold or none (seq 200: one
+    packed chunk for four waves), the window chunks in the same launch, and many splits;
+    against the oracle and f64 dense attention on the dequantized cache."""
+    dim = 128
+    rng = np.random.default_rng(4200 + 10 * gqa + bits)
+    k = rng.standard_normal(batch * heads * seq * dim).astype(np.float32)
+    k.reshape(batch, heads, seq, dim)[:, :, :, 7] *= np.float32(10.0)
+    v = rng.standard_normal(batch * heads * seq * dim).astype(np.float32)
+    cfg = KiviConfig(bits, 32, 128)
+    a = KiviCache(amd, cfg, batch, heads, dim)
+    o = KiviCache(oracle, cfg, batch, heads, dim)
+    a.append(k, v, seq)
+    o.append(k, v, seq)
+    q = rng.standard_normal(batch * heads * gqa * dim).astype(np.float32)
+    scale = np.float32(1 / np.sqrt(dim))
+    got = a.attention(q, heads * gqa, scale)
+    assert_close(got, o.attention(q, heads * gqa, scale))
+    kh, vh = a.dequantize()
+    assert max_abs(got, dense_attend(kh, vh, q, batch, heads, heads * gqa, seq, dim, scale)) < 1e-4
+
+
 @pytest.mark.parametrize("bits", [2, 4, 8])
 @pytest.mark.parametrize("gqa", [1, 4, 8])
 def test_attention_parity_long(amd, oracle, bits, gqa):
@@ -496,8 +523,9 @@ def test_runtime_decode_parity(amd, oracle):
     (4, 128, 16, 128, 128), (4, 64, 4, 32, 64), (2, 128, 8, 64, 256)])
 def test_runtime_decode_device_parity(amd, oracle, bits, residual, gqa, group, dim):
     """RuntimeKv::decode on device pointers, which runs append + attention in one attention
-    launch (the token the window evicts quantized inside it) for G = 32 and GQA <= 8 when no
-    key flush is due, and as an append then an attention launch otherwise: bit for bit equal to
+    launch (the token the window evicts quantized inside it) for G = 32 and GQA <= 4 when no
+    key flush is due, and as an append then an attention launch otherwise (GQA 8 here: the
+    eight-head kernel does not append): bit for bit equal to
     a cache taking append_device then attention_device (tests/runtime.rs:13-52), and within
     tolerance of the oracle's decode, streams bit-exact, across evictions and flushes."""
     heads, prefill, steps = 2, 3 * residual + 17, 2 * residual + 5
