@@ -1268,13 +1268,15 @@ __global__ void __launch_bounds__(kThreads, SMALL ? 2 : fast_min_groups(BITS, NR
 //
 // Lane l = 16g + n; D (4 VGPRs) holds rows 4g .. 4g+3 of column n of a 16x16 tile.
 // Keys: rows = 16 tokens (tile mt: tokens 16mt .. +15), columns = (head n%8, key group n/8 of
-// the chunk), K = channels with hi and lo halves: K-tile kt gives lane group g the channels
-// 32g + 4kt .. +3, its eight K slots the hi then the lo halves of q*scale (B operand) against
-// the same four codes twice (A operand). A tile's tokens lie in one key group: the other
-// group's columns are computed and dropped.
+// the chunk), K = 32 channels per K-tile (lane group g: channels 32g + 8kt .. +7), each K-tile
+// taken twice into one accumulator, against the hi and then the lo halves of q*scale (B
+// operand) with the same eight codes (A operand). A tile's tokens lie in one key group: the
+// other group's columns are computed and dropped.
 // Values: rows = 16 channels (tile mt: channels 16mt .. +15, value group mt/2), columns =
-// (head n%8, parity n/8 of the value group), K = tokens with hi and lo halves: K-tile kt gives
-// lane group g the tokens 16g + 4kt .. +3; the other parity's columns are dropped.
+// (head n%8, parity n/8 of the value group), K = 32 tokens per K-tile (lane group g: tokens
+// 16g + 8kt .. +7), hi and lo halves of w*scale as for the keys; the other parity's columns
+// are dropped. (Four codes twice in one K-tile against hi-then-lo K slots measured slower:
+// the duplicated operand costs a copy per MFMA.)
 // A chunk's (scale, zero) pairs are staged in LDS, from which the eight lanes of a head
 // column set read them as broadcasts (no cross-lane moves on the vector ALU).
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
@@ -1289,7 +1291,6 @@ constexpr int kWideStage = 512;   // floats per wave
 __device__ __forceinline__ v4f mfma_wide(h8 a, h8 b, v4f c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
-__device__ __forceinline__ h8 twice(h4 x) { return h8{x[0], x[1], x[2], x[3], x[0], x[1], x[2], x[3]}; }
 __device__ __forceinline__ h8 join(h4 x, h4 y) { return h8{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]}; }
 
 // One chunk's code words for the lane. Keys: tile mt's token 16mt + n, words BITS*g .. +BITS-1
@@ -1363,27 +1364,32 @@ __device__ __forceinline__ void wide_stage(float* stage, uint32_t lane, float4 p
   s[1] = p1;
 }
 
-// A operand of tile mt, K-tile kt: the four codes of the lane's K slots, twice.
+// A operand of tile mt, K-tile kt: the eight codes of the lane's K slots, in element order.
 template <int BITS>
 __device__ __forceinline__ h8 wide_key_codes(const WideKeyWords<BITS>& kw, int mt, int kt) {
-  // channels 32g + 4kt .. +3: word (32g + 4kt) / PPW of the token, elements 4*(kt % (PPW/4)) ..
-  if constexpr (BITS == 2) return twice(codes4<2>(kw.w[mt][kt / 4], kt % 4));
-  else if constexpr (BITS == 4) return twice(codes4<4>(kw.w[mt][kt / 2], kt % 2));
-  else return twice(codes4<8>(kw.w[mt][kt], 0));
+  // channels 32g + 8kt .. +7: 2-bit word 2g + kt/2, elements 8*(kt%2) ..; 4-bit word 4g + kt;
+  // 8-bit words 8g + 2kt, +1
+  if constexpr (BITS == 2) return join(codes4<2>(kw.w[mt][kt / 2], 2 * (kt % 2)), codes4<2>(kw.w[mt][kt / 2], 2 * (kt % 2) + 1));
+  else if constexpr (BITS == 4) return join(codes4<4>(kw.w[mt][kt], 0), codes4<4>(kw.w[mt][kt], 1));
+  else return join(codes4<8>(kw.w[mt][2 * kt], 0), codes4<8>(kw.w[mt][2 * kt + 1], 0));
 }
 template <int BITS>
 __device__ __forceinline__ h8 wide_value_codes(const WideValueWords<BITS>& vw, int mt, int kt) {
-  // tokens 16g + 4kt .. +3 of the channel: word (16g + 4kt) / PPW of the block
-  if constexpr (BITS == 2) return twice(codes4<2>(vw.w[mt][0], kt));
-  else if constexpr (BITS == 4) return twice(codes4<4>(vw.w[mt][kt / 2], kt % 2));
-  else return twice(codes4<8>(vw.w[mt][kt], 0));
+  // tokens 16g + 8kt .. +7 of the channel: 2-bit word g, elements 8kt ..; 4-bit word 2g + kt;
+  // 8-bit words 4g + 2kt, +1
+  if constexpr (BITS == 2) return join(codes4<2>(vw.w[mt][0], 2 * kt), codes4<2>(vw.w[mt][0], 2 * kt + 1));
+  else if constexpr (BITS == 4) return join(codes4<4>(vw.w[mt][kt], 0), codes4<4>(vw.w[mt][kt], 1));
+  else return join(codes4<8>(vw.w[mt][2 * kt], 0), codes4<8>(vw.w[mt][2 * kt + 1], 0));
 }
 
-// B operand from four products: hi halves then lo halves (x below 2^15 in magnitude)
-__device__ __forceinline__ h8 wide_split4(const float (&x)[4]) {
-  h4 hi, lo;
-  split4(x, hi, lo);
-  return join(hi, lo);
+// B operands from eight products: their hi halves and their lo halves (x below 2^15 in
+// magnitude)
+__device__ __forceinline__ void wide_split8(const float (&x)[8], h8& hi, h8& lo) {
+  h4 h0, l0, h1, l1;
+  split4(x, h0, l0);
+  split4(x + 4, h1, l1);
+  hi = join(h0, h1);
+  lo = join(l0, l1);
 }
 
 template <int BITS>
@@ -1460,18 +1466,27 @@ __device__ __forceinline__ void wide_split(const AttnArgs& a, uint32_t unit, uin
       for (int mt = 0; mt < 4; ++mt) acc[mt] = v4f{0.f, 0.f, 0.f, 0.f};
       float bias = 0.f;
 #pragma unroll
-      for (int kt = 0; kt < 8; ++kt) {
-        const float4* sp = reinterpret_cast<const float4*>(stage + (sel * 128 + 32 * g + 4 * kt) * 2);
-        const float4 s01 = sp[0], s23 = sp[1];
-        const float p[4] = {qv[4 * kt] * s01.x, qv[4 * kt + 1] * s01.z, qv[4 * kt + 2] * s23.x,
-                            qv[4 * kt + 3] * s23.z};
-        bias = fmaf(qv[4 * kt], s01.y, bias);
-        bias = fmaf(qv[4 * kt + 1], s01.w, bias);
-        bias = fmaf(qv[4 * kt + 2], s23.y, bias);
-        bias = fmaf(qv[4 * kt + 3], s23.w, bias);
-        const h8 B = wide_split4(p);
+      for (int kt = 0; kt < 4; ++kt) {
+        // channels 32g + 8kt .. +7 of key group sel: four (scale, zero) pairs per float4 pair
+        const float4* sp = reinterpret_cast<const float4*>(stage + (sel * 128 + 32 * g + 8 * kt) * 2);
+        const float4 s[4] = {sp[0], sp[1], sp[2], sp[3]};
+        float p[8];
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) acc[mt] = mfma_wide(wide_key_codes<BITS>(cur, mt, kt), B, acc[mt]);
+        for (int j = 0; j < 4; ++j) {
+          p[2 * j] = qv[8 * kt + 2 * j] * s[j].x;
+          p[2 * j + 1] = qv[8 * kt + 2 * j + 1] * s[j].z;
+          bias = fmaf(qv[8 * kt + 2 * j], s[j].y, bias);
+          bias = fmaf(qv[8 * kt + 2 * j + 1], s[j].w, bias);
+        }
+        h8 bhi, blo;
+        wide_split8(p, bhi, blo);
+        h8 A[4];
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) A[mt] = wide_key_codes<BITS>(cur, mt, kt);
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) acc[mt] = mfma_wide(A[mt], bhi, acc[mt]);
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) acc[mt] = mfma_wide(A[mt], blo, acc[mt]);
       }
       // the zero term of the lane's column over all 128 channels (lane groups g)
       bias += __shfl_xor(bias, 16);
@@ -1538,22 +1553,29 @@ __device__ __forceinline__ void wide_split(const AttnArgs& a, uint32_t unit, uin
         for (int r = 0; r < 16; ++r) lsum += w[r];
       }
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
+      for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
         for (int pr = 0; pr < 2; ++pr) {
-          // value group 2*pr + sel, tokens 16g + 4kt .. +3
-          const float4* sp = reinterpret_cast<const float4*>(stage + ((2 * pr + sel) * 64 + 16 * g + 4 * kt) * 2);
-          const float4 s01 = sp[0], s23 = sp[1];
-          const float p[4] = {w[4 * kt] * s01.x, w[4 * kt + 1] * s01.z, w[4 * kt + 2] * s23.x,
-                              w[4 * kt + 3] * s23.z};
-          zacc[pr] = fmaf(w[4 * kt], s01.y, zacc[pr]);
-          zacc[pr] = fmaf(w[4 * kt + 1], s01.w, zacc[pr]);
-          zacc[pr] = fmaf(w[4 * kt + 2], s23.y, zacc[pr]);
-          zacc[pr] = fmaf(w[4 * kt + 3], s23.w, zacc[pr]);
-          const h8 B = wide_split4(p);
+          h8 A[4];
 #pragma unroll
-          for (int mm = 0; mm < 4; ++mm)
-            vacc[4 * pr + mm] = mfma_wide(wide_value_codes<BITS>(cur, 4 * pr + mm, kt), B, vacc[4 * pr + mm]);
+          for (int mm = 0; mm < 4; ++mm) A[mm] = wide_value_codes<BITS>(cur, 4 * pr + mm, kt);
+          // value group 2*pr + sel, tokens 16g + 8kt .. +7
+          const float4* sp = reinterpret_cast<const float4*>(stage + ((2 * pr + sel) * 64 + 16 * g + 8 * kt) * 2);
+          const float4 s[4] = {sp[0], sp[1], sp[2], sp[3]};
+          float p[8];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            p[2 * j] = w[8 * kt + 2 * j] * s[j].x;
+            p[2 * j + 1] = w[8 * kt + 2 * j + 1] * s[j].z;
+            zacc[pr] = fmaf(w[8 * kt + 2 * j], s[j].y, zacc[pr]);
+            zacc[pr] = fmaf(w[8 * kt + 2 * j + 1], s[j].w, zacc[pr]);
+          }
+          h8 bhi, blo;
+          wide_split8(p, bhi, blo);
+#pragma unroll
+          for (int mm = 0; mm < 4; ++mm) vacc[4 * pr + mm] = mfma_wide(A[mm], bhi, vacc[4 * pr + mm]);
+#pragma unroll
+          for (int mm = 0; mm < 4; ++mm) vacc[4 * pr + mm] = mfma_wide(A[mm], blo, vacc[4 * pr + mm]);
         }
       }
     };
@@ -1616,10 +1638,10 @@ __device__ __forceinline__ void wide_split(const AttnArgs& a, uint32_t unit, uin
 
 // Eight-head launch at head_dim 128, G = 32: the window / suffix chunk workgroups first (the
 // 4x4x4 MIXED path), then the packed splits on the 16x16x32 path. Two workgroups per CU fit
-// the LDS of eight chunks' logits; the register budget of three (168 VGPRs, no spills) measured
-// faster than that of two, and requests two chunks ahead slower than one.
+// the LDS of eight chunks' logits, and so the register budget of two (up to 256 VGPRs);
+// requests two chunks ahead measured slower than one.
 template <int BITS>
-__global__ void __launch_bounds__(kThreads, 3) k_attn_wide(AttnArgs a) {
+__global__ void __launch_bounds__(kThreads, 2) k_attn_wide(AttnArgs a) {
   extern __shared__ float lds[];
   const uint32_t nwin = a.units * a.hgroups * a.nsplit_win;
   if (blockIdx.x < nwin) {
