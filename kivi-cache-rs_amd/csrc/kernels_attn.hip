@@ -1281,12 +1281,20 @@ __global__ void __launch_bounds__(kThreads, SMALL ? 2 : fast_min_groups(BITS, NR
 // column set read them as broadcasts (no cross-lane moves on the vector ALU).
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 
-constexpr int kWideCpw = 8;       // chunks per wave (LDS: two workgroups per CU)
 constexpr int kWideHeads = 8;     // heads per workgroup (one head group)
-// One chunk's (scale, zero) pairs staged per wave, as stored: keys [group][channel][2],
-// values [group][token][2]. (A layout padded so that the eight addresses of a broadcast read
-// fall in disjoint banks measured no faster.)
-constexpr int kWideStage = 512;   // floats per wave
+// Chunks per wave and workgroups per CU: 2- and 4-bit take 6 chunks and three workgroups per
+// CU (the LDS of six chunks' logits, 168 VGPRs); 8-bit, whose code words take more registers,
+// 8 chunks and two (up to 256 VGPRs).
+constexpr int wide_cpw(int bits) { return bits == 8 ? 8 : 6; }
+constexpr int wide_blocks(int bits) { return bits == 8 ? 2 : 3; }
+// One chunk's (scale, zero) pairs (512 floats, as stored: keys [group][channel][2], values
+// [group][token][2]) are staged in the LDS of the chunk's own logits slot, eight row segments
+// of 64 floats: stage float i at row i/64, column 64k + i%64. A key step reads them before it
+// writes the slot's logits; a value step writes them after it has read the slot's logits.
+// (A separate, bank-padded staging buffer measured no faster and cost a workgroup per CU.)
+__device__ __forceinline__ float* wide_stage_at(float* wl, int row, int k, uint32_t i) {
+  return wl + (i / 64) * row + k * 64 + (i % 64);
+}
 
 __device__ __forceinline__ v4f mfma_wide(h8 a, h8 b, v4f c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
@@ -1357,9 +1365,9 @@ __device__ __forceinline__ void wide_load_value_params(const AttnArgs& a, uint32
   p0 = p[0];
   p1 = p[1];
 }
-// The lane's eight floats (four (scale, zero) pairs, as loaded) at 8*lane.
-__device__ __forceinline__ void wide_stage(float* stage, uint32_t lane, float4 p0, float4 p1) {
-  float4* s = reinterpret_cast<float4*>(stage + 8 * lane);
+// The lane's eight floats (four (scale, zero) pairs, as loaded) at stage floats 8*lane ..
+__device__ __forceinline__ void wide_stage(float* wl, int row, int k, uint32_t lane, float4 p0, float4 p1) {
+  float4* s = reinterpret_cast<float4*>(wide_stage_at(wl, row, k, 8 * lane));
   s[0] = p0;
   s[1] = p1;
 }
@@ -1395,7 +1403,7 @@ __device__ __forceinline__ void wide_split8(const float (&x)[8], h8& hi, h8& lo)
 template <int BITS>
 __device__ __forceinline__ void wide_split(const AttnArgs& a, uint32_t unit, uint32_t split, uint32_t hg,
                                            float* lds) {
-  constexpr int CPW = kWideCpw, NH = kWideHeads, D = 128;
+  constexpr int CPW = wide_cpw(BITS), NH = kWideHeads, D = 128;
   constexpr int ROW = CPW * 64 + kRowPad;
   constexpr int kExp = CodeUnit<BITS>::kExp;
   constexpr float kUnit = kExp == 0 ? 1.0f : kExp == -1 ? 0.5f : 0.001953125f;
@@ -1405,8 +1413,7 @@ __device__ __forceinline__ void wide_split(const AttnArgs& a, uint32_t unit, uin
   const uint32_t hq = n % 8;   // head of the lane's column
   const uint32_t sel = n / 8;  // key group of the chunk (keys) / value group parity (values)
   const uint32_t gq = a.gq;
-  float* wl = lds + wave * (NH * ROW + kWideStage);  // this wave's logits [NH][ROW]
-  float* stage = wl + NH * ROW;                       // and (scale, zero) staging
+  float* wl = lds + wave * NH * ROW;  // this wave's logits [NH][ROW] (and staging)
 
   // chunks dealt round-robin over the unit's waves, as in the 4x4x4 path
   const int32_t slots = static_cast<int32_t>(a.nsplit_fast * 4);
@@ -1457,7 +1464,7 @@ __device__ __forceinline__ void wide_split(const AttnArgs& a, uint32_t unit, uin
     auto step = [&](int k, const WideKeyWords<BITS>& cur, WideKeyWords<BITS>& next) {
       // this chunk's (scale, zero) pairs to LDS (after the previous chunk's reads of them),
       // then the next chunk's requested (the last step re-reads an L2-resident chunk)
-      wide_stage(stage, lane, kp0, kp1);
+      wide_stage(wl, ROW, k, lane, kp0, kp1);
       const int32_t kn = chunk_of(std::min(k + 1, nch - 1));
       wide_load_key_params(a, unit, kn, lane, kp0, kp1);
       wide_load_keys<BITS>(a, unit, kn, g, n, next);
@@ -1468,7 +1475,7 @@ __device__ __forceinline__ void wide_split(const AttnArgs& a, uint32_t unit, uin
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) {
         // channels 32g + 8kt .. +7 of key group sel: four (scale, zero) pairs per float4 pair
-        const float4* sp = reinterpret_cast<const float4*>(stage + (sel * 128 + 32 * g + 8 * kt) * 2);
+        const float4* sp = reinterpret_cast<const float4*>(wide_stage_at(wl, ROW, k, (sel * 128 + 32 * g + 8 * kt) * 2));
         const float4 s[4] = {sp[0], sp[1], sp[2], sp[3]};
         float p[8];
 #pragma unroll
@@ -1480,13 +1487,15 @@ __device__ __forceinline__ void wide_split(const AttnArgs& a, uint32_t unit, uin
         }
         h8 bhi, blo;
         wide_split8(p, bhi, blo);
-        h8 A[4];
+        // two tiles' codes live at a time; each tile's hi and lo products one MFMA apart
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) A[mt] = wide_key_codes<BITS>(cur, mt, kt);
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) acc[mt] = mfma_wide(A[mt], bhi, acc[mt]);
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) acc[mt] = mfma_wide(A[mt], blo, acc[mt]);
+        for (int m2 = 0; m2 < 4; m2 += 2) {
+          const h8 A0 = wide_key_codes<BITS>(cur, m2, kt), A1 = wide_key_codes<BITS>(cur, m2 + 1, kt);
+          acc[m2] = mfma_wide(A0, bhi, acc[m2]);
+          acc[m2 + 1] = mfma_wide(A1, bhi, acc[m2 + 1]);
+          acc[m2] = mfma_wide(A0, blo, acc[m2]);
+          acc[m2 + 1] = mfma_wide(A1, blo, acc[m2 + 1]);
+        }
       }
       // the zero term of the lane's column over all 128 channels (lane groups g)
       bias += __shfl_xor(bias, 16);
@@ -1533,17 +1542,23 @@ __device__ __forceinline__ void wide_split(const AttnArgs& a, uint32_t unit, uin
       wide_load_values<BITS>(a, unit, chunk_of(0), g, n, vw0);
     }
     auto step = [&](int k, const WideValueWords<BITS>& cur, WideValueWords<BITS>& next) {
-      wide_stage(stage, lane, vp0, vp1);
-      const int32_t kn = chunk_of(std::min(k + 1, nch - 1));
-      wide_load_value_params(a, unit, kn, lane, vp0, vp1);
-      wide_load_values<BITS>(a, unit, kn, g, n, next);
-      // weights (times 2^ev) of head hq, tokens 16g .. 16g+15
-      float w[16];
+      // weights (times 2^ev) of head hq, tokens 16g .. 16g+15, read from the slot before the
+      // chunk's (scale, zero) pairs are staged over it
+      float4 lg[4];
       {
         const float4* lp = reinterpret_cast<const float4*>(wl + hq * ROW + k * 64 + 16 * g);
 #pragma unroll
+        for (int r = 0; r < 4; ++r) lg[r] = lp[r];
+      }
+      wide_stage(wl, ROW, k, lane, vp0, vp1);
+      const int32_t kn = chunk_of(std::min(k + 1, nch - 1));
+      wide_load_value_params(a, unit, kn, lane, vp0, vp1);
+      wide_load_values<BITS>(a, unit, kn, g, n, next);
+      float w[16];
+      {
+#pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float4 x = lp[r];
+          const float4 x = lg[r];
           w[4 * r] = __builtin_amdgcn_exp2f(fmaf(x.x, kout, evoff));
           w[4 * r + 1] = __builtin_amdgcn_exp2f(fmaf(x.y, kout, evoff));
           w[4 * r + 2] = __builtin_amdgcn_exp2f(fmaf(x.z, kout, evoff));
@@ -1556,11 +1571,10 @@ __device__ __forceinline__ void wide_split(const AttnArgs& a, uint32_t unit, uin
       for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
         for (int pr = 0; pr < 2; ++pr) {
-          h8 A[4];
-#pragma unroll
-          for (int mm = 0; mm < 4; ++mm) A[mm] = wide_value_codes<BITS>(cur, 4 * pr + mm, kt);
+
           // value group 2*pr + sel, tokens 16g + 8kt .. +7
-          const float4* sp = reinterpret_cast<const float4*>(stage + ((2 * pr + sel) * 64 + 16 * g + 8 * kt) * 2);
+          const float4* sp =
+              reinterpret_cast<const float4*>(wide_stage_at(wl, ROW, k, ((2 * pr + sel) * 64 + 16 * g + 8 * kt) * 2));
           const float4 s[4] = {sp[0], sp[1], sp[2], sp[3]};
           float p[8];
 #pragma unroll
@@ -1573,9 +1587,14 @@ __device__ __forceinline__ void wide_split(const AttnArgs& a, uint32_t unit, uin
           h8 bhi, blo;
           wide_split8(p, bhi, blo);
 #pragma unroll
-          for (int mm = 0; mm < 4; ++mm) vacc[4 * pr + mm] = mfma_wide(A[mm], bhi, vacc[4 * pr + mm]);
-#pragma unroll
-          for (int mm = 0; mm < 4; ++mm) vacc[4 * pr + mm] = mfma_wide(A[mm], blo, vacc[4 * pr + mm]);
+          for (int m2 = 0; m2 < 4; m2 += 2) {
+            const int t0 = 4 * pr + m2;
+            const h8 A0 = wide_value_codes<BITS>(cur, t0, kt), A1 = wide_value_codes<BITS>(cur, t0 + 1, kt);
+            vacc[t0] = mfma_wide(A0, bhi, vacc[t0]);
+            vacc[t0 + 1] = mfma_wide(A1, bhi, vacc[t0 + 1]);
+            vacc[t0] = mfma_wide(A0, blo, vacc[t0]);
+            vacc[t0 + 1] = mfma_wide(A1, blo, vacc[t0 + 1]);
+          }
         }
       }
     };
@@ -1637,11 +1656,10 @@ __device__ __forceinline__ void wide_split(const AttnArgs& a, uint32_t unit, uin
 }
 
 // Eight-head launch at head_dim 128, G = 32: the window / suffix chunk workgroups first (the
-// 4x4x4 MIXED path), then the packed splits on the 16x16x32 path. Two workgroups per CU fit
-// the LDS of eight chunks' logits, and so the register budget of two (up to 256 VGPRs);
-// requests two chunks ahead measured slower than one.
+// 4x4x4 MIXED path), then the packed splits on the 16x16x32 path, wide_blocks(BITS)
+// workgroups per CU. Requests two chunks ahead measured slower than one.
 template <int BITS>
-__global__ void __launch_bounds__(kThreads, 2) k_attn_wide(AttnArgs a) {
+__global__ void __launch_bounds__(kThreads, wide_blocks(BITS)) k_attn_wide(AttnArgs a) {
   extern __shared__ float lds[];
   const uint32_t nwin = a.units * a.hgroups * a.nsplit_win;
   if (blockIdx.x < nwin) {
@@ -2696,11 +2714,11 @@ AttnArgs make_args(const AttnProblem& p, float* ws) {
   // a launch that also appends a decode token keeps the 4x4x4 kernel (it quantizes the
   // evicted window row); such launches are not made for these shapes (attention_fuses_decode)
   a.wide = fast && wide_shape(p) && a.pend_evict == 0 ? 1u : 0u;
-  // packed splits per unit: at most kFastCpw (kWideCpw) chunks per wave, at least one, and at
+  // packed splits per unit: at most kFastCpw (wide_cpw) chunks per wave, at least one, and at
   // least kFastGroups workgroups (over units and head groups) when the chunks allow
   {
     const uint32_t units = p.cache.geo.units * a.hgroups;
-    const uint32_t cpw = a.wide ? static_cast<uint32_t>(kWideCpw)
+    const uint32_t cpw = a.wide ? static_cast<uint32_t>(wide_cpw(static_cast<int>(p.cache.geo.bits)))
                                 : static_cast<uint32_t>(fast_cpw(static_cast<int>(p.cache.geo.bits), fast_nrs(p.cache.geo.D, a.gq)));
     const uint32_t fewest = (a.chunk_end + 4 * cpw - 1) / (4 * cpw);
     const uint32_t most = (a.chunk_end + 3) / 4;
@@ -2744,7 +2762,7 @@ hipError_t launch_fast(const AttnArgs& a, double bytes, hipStream_t stream) {
   const uint32_t grid = a.units * (a.hgroups * (a.nsplit_win + a.nsplit_fast) + a.nsplit_gen);
   if constexpr (D == 128 && NRS == 2) {
     if (a.wide) {
-      const size_t wide = (size_t)4 * (kWideHeads * (kWideCpw * 64 + kRowPad) + kWideStage);
+      const size_t wide = (size_t)4 * kWideHeads * (wide_cpw(BITS) * 64 + kRowPad);
       const size_t mixed = (size_t)4 * NH * (64 + kRowPad);
       const size_t wlds = std::max(std::max(wide, mixed), combine) * sizeof(float);
       k_attn_wide<BITS><<<grid, kThreads, wlds, stream>>>(a);
