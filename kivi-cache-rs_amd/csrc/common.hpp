@@ -20,8 +20,8 @@
 // offset 2*(i/8) of that nibble). One shift-and-mask then leaves four (4-bit) or eight
 // (2-bit) consecutive elements one per byte or nibble, which the attention kernels convert
 // into MFMA operands with the packed fp8 / fp4 converters and no further shuffling.
-// Per unit, smax[4] holds the largest key and value scale and the largest key and value
-// magnitude quantized so far (see CacheView).
+// Per unit, smax holds the largest key and value scale and the largest key and value
+// magnitude quantized so far, in kMaxSlots records (see CacheView and unit_max).
 //
 // fp32 state per unit: key residual [R][D] (linear, token kq+i in slot i) and the value
 // window [R][D] as a ring (token vq+i in slot (vhead+i) % R), so a decode step evicts one
@@ -97,12 +97,36 @@ struct CacheView {
   float* vparams;
   float* kres;   // [units][R][D]
   float* vring;  // [units][R][D]
-  // [units][4]: running maxima of the key scales, the value scales, the key |x| and the
-  // value |x| ever quantized into each unit (f32 bit patterns of values >= 0, so unsigned
-  // order is float order). The attention kernels derive power-of-two operand ranges from
-  // them; |x| bounds every dequantized element (up to rounding).
+  // [units][kMaxSlots][kMaxStride]: running maxima of the key scales, the value scales, the
+  // key |x| and the value |x| ever quantized into each unit (words kMaxKeyScale ..
+  // kMaxValueAbs of a slot record; f32 bit patterns of values >= 0, so unsigned order is float
+  // order). A writer raises the record its workgroup index selects (max_slot), a reader takes
+  // the maximum over the records (unit_max). The attention kernels derive power-of-two operand
+  // ranges from them; |x| bounds every dequantized element (up to rounding).
   uint32_t* smax;
 };
+
+// The maxima records of a unit sit on their own 128-byte lines, so the atomics of one launch
+// spread over kMaxSlots lines per unit. With one record per unit, the records of eight units
+// shared one line and every quantize workgroup's atomics queued on it (batch 1 x 8 heads).
+constexpr uint32_t kMaxSlots = 8;
+constexpr uint32_t kMaxStride = 32;  // words per record
+constexpr uint32_t kMaxUnitWords = kMaxSlots * kMaxStride;
+constexpr uint32_t kMaxKeyScale = 0, kMaxValueScale = 1, kMaxKeyAbs = 2, kMaxValueAbs = 3;
+
+// Record `slot` (mod kMaxSlots) of a unit's maxima.
+__device__ __forceinline__ uint32_t* max_slot(uint32_t* smax, uint32_t unit, uint32_t slot) {
+  return smax + (uint64_t)unit * kMaxUnitWords + (slot % kMaxSlots) * kMaxStride;
+}
+
+// Maximum `which` (kMaxKeyScale .. kMaxValueAbs) of a unit over its records.
+__device__ __forceinline__ float unit_max(const uint32_t* smax, uint32_t unit, uint32_t which) {
+  const uint32_t* p = smax + (uint64_t)unit * kMaxUnitWords + which;
+  uint32_t m = p[0];
+#pragma unroll
+  for (uint32_t s = 1; s < kMaxSlots; ++s) m = m > p[s * kMaxStride] ? m : p[s * kMaxStride];
+  return __uint_as_float(m);
+}
 
 // Sequence state of a cache at one instant.
 struct SeqState {

@@ -353,7 +353,7 @@ struct CacheCore {
     const size_t rbytes = (size_t)geo.units * geo.R * geo.D * sizeof(float);
     KIVI_TRY(kres.alloc_zero(rbytes, s, "key residual"));
     KIVI_TRY(vring.alloc_zero(rbytes, s, "value window"));
-    KIVI_TRY(smax.alloc_zero((size_t)geo.units * 4 * sizeof(uint32_t), s, "scale maxima"));
+    KIVI_TRY(smax.alloc_zero((size_t)geo.units * kMaxUnitWords * sizeof(uint32_t), s, "scale maxima"));
     return Status{};
   }
 

@@ -945,7 +945,7 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
   // Power-of-two operand ranges: every key A operand |q * scale| * 2^ek and every value A
   // operand |w * scale| * 2^ev (w <= 1) stays below 2^15, from the unit's largest scales.
   qmax = warp_max(qmax);
-  const float kmax = __uint_as_float(a.c.smax[4 * unit]);
+  const float kmax = unit_max(a.c.smax, unit, kMaxKeyScale);
   constexpr float kLevels = static_cast<float>((1 << BITS) - 1);
   const int ek = std::min(60, std::max(-100, 15 - __builtin_amdgcn_frexp_expf(qmax * kmax)));
   constexpr int kExp = CodeUnit<BITS>::kExp;
@@ -1022,7 +1022,7 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
   // the value operands' range: the unit's largest value scale, raised by the evicted row's
   // quantization when a decode token is appended by this launch (as the append would have);
   // taken after the logits, so the evicted row's load is not waited for before them
-  float vmax = __uint_as_float(a.c.smax[4 * unit + 1]);
+  float vmax = unit_max(a.c.smax, unit, kMaxValueScale);
   float ev_scale = 0.f, ev_amax = 0.f;  // the evicted row's largest scale and |x|
   if (D == 128 && a.pend_evict) {
     evict_groups(er, kLevels, ev_scale, ev_amax);
@@ -1094,8 +1094,8 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
           }
         }
         if (lane == 0) {
-          atomicMax(a.c.smax + 4 * unit + 1, __float_as_uint(ev_scale));
-          atomicMax(a.c.smax + 4 * unit + 3, __float_as_uint(ev_amax));
+          atomicMax(max_slot(a.c.smax, unit, 0) + kMaxValueScale, __float_as_uint(ev_scale));
+          atomicMax(max_slot(a.c.smax, unit, 0) + kMaxValueAbs, __float_as_uint(ev_amax));
         }
       }
       }  // D == 128 (the decode is fused into the launch at head_dim 128 only)
@@ -1451,7 +1451,7 @@ __device__ __forceinline__ void wide_split(const AttnArgs& a, uint32_t unit, uin
   }
   // power-of-two operand ranges from the unit's largest scales, as in the 4x4x4 path
   qmax = warp_max(qmax);
-  const float kmax = __uint_as_float(a.c.smax[4 * unit]);
+  const float kmax = unit_max(a.c.smax, unit, kMaxKeyScale);
   const int ek = std::min(60, std::max(-100, 15 - __builtin_amdgcn_frexp_expf(qmax * kmax)));
   const float kfac = ldexpf(1.f, ek);
   const float kout = ldexpf(1.f, -ek - kExp);
@@ -1521,7 +1521,7 @@ __device__ __forceinline__ void wide_split(const AttnArgs& a, uint32_t unit, uin
   mx = fmaxf(mx, __shfl_xor(mx, 32));
   const float mrow = mx * kout;
 
-  const float vmax = __uint_as_float(a.c.smax[4 * unit + 1]);
+  const float vmax = unit_max(a.c.smax, unit, kMaxValueScale);
   const int ev = std::min(60, std::max(-100, 15 - __builtin_amdgcn_frexp_expf(vmax)));
   const float vout = ldexpf(1.f, -ev - kExp);
   const float moff = mrow == -INFINITY ? 0.f : mrow;
@@ -2548,8 +2548,8 @@ __device__ __forceinline__ void shared_split(const AttnArgs& a, uint32_t unit, u
     qhi[s] = __builtin_bit_cast(hx8, hi);
     qlo[s] = __builtin_bit_cast(hx8, lo);
   }
-  const int ek = range_exp(__uint_as_float(a.c.smax[4 * unit + 2]));
-  const int ev = range_exp(__uint_as_float(a.c.smax[4 * unit + 3]));
+  const int ek = range_exp(unit_max(a.c.smax, unit, kMaxKeyAbs));
+  const int ev = range_exp(unit_max(a.c.smax, unit, kMaxValueAbs));
   const float kf = ldexpf(1.f, ek), vf = ldexpf(1.f, ev);
   const float s_unscale = ldexpf(1.f, -ek - eq);
   const float o_unscale = ldexpf(1.f, -ev) / kShPScale;  // O and l carry the P operand scale
