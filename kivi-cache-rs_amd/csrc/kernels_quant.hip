@@ -459,8 +459,8 @@ __device__ __forceinline__ void wave_raise_max(uint32_t* m, float scale, float a
 // per-channel min/max (src/quant.rs:296-311). Codes are packed in registers: the LPW lanes
 // whose channels share a token-major word OR their parts together (DPP), lane m of the group
 // keeps the words of tokens t = m (mod LPW), and each store writes 64 consecutive words. The
-// unit's running maxima are raised once per workgroup (a few units' maxima are hot addresses).
-constexpr uint32_t kKeySpan = 16;
+// unit's running maxima are raised once per workgroup, in the maxima record its index selects.
+constexpr uint32_t kKeySpan = 4;  // one group per wave
 template <int BITS, int CPL, int GG>
 __global__ void __launch_bounds__(kThreads)
     k_quant_keys_wave(CacheView c, RowSource src, uint64_t g0, uint32_t ngroups, uint32_t spans) {
@@ -540,8 +540,8 @@ __global__ void __launch_bounds__(kThreads)
 // (16/PPW words per channel). The four waves' words meet in LDS (two buffers, one barrier per
 // block) so each block's words are stored contiguously; words that already hold earlier tokens
 // of the block are read and OR-ed (blocks fill across appends). The unit's running maxima are
-// raised once per workgroup.
-constexpr uint32_t kValueSpan = 4;
+// raised once per workgroup, in the maxima record its index selects.
+constexpr uint32_t kValueSpan = 1;  // one block per workgroup
 template <int BITS, int CPL, int GG>
 __global__ void __launch_bounds__(kThreads)
     k_quant_values_wave(CacheView c, RowSource ring, uint32_t n_ring, RowSource in, uint64_t vq0,
