@@ -319,7 +319,7 @@ kivi_status kivi_runtime_decode(kivi_runtime* rt, const float* key, size_t key_l
                                 size_t query_len, size_t num_q_heads, float scale, float* out,
                                 size_t out_len, kivi_error* err);
 /* The same on device pointers, enqueued on `stream` (inputs read by the enqueued work). A step
-   without a key flush due runs, at head_dim 128, G = 32 and up to four query heads per KV head,
+   without a key flush due runs, at head_dim 128, G = 32 and up to eight query heads per KV head,
    as one attention launch that carries the append, plus the merge launch; other steps run as
    the append and then the attention. Either way the result is bit for bit that of append then
    attention. */

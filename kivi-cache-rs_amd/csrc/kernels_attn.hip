@@ -1400,7 +1400,78 @@ __device__ __forceinline__ void wide_split8(const float (&x)[8], h8& hi, h8& lo)
   lo = join(l0, l1);
 }
 
+// A decode token appended by this launch evicted token vq-1 into the chunk at token t0 (t0 <=
+// vq-1 < t0 + 64): the token's codes and (scale, zero) pairs join the wave's registers of the
+// chunk (value words vw, the lane's pairs p0 / p1 as wide_load_value_params holds them) and go
+// to memory (the only reader of those words in this launch is this wave), and the unit's
+// maxima take the row's largest scale and |x|, as the value quantizer would have
+// (src/quant.rs:349-375). er is the row in the quantizer's layout (lane holds channels lane and
+// 64 + lane, after evict_groups).
 template <int BITS>
+__device__ __forceinline__ void wide_evict(const AttnArgs& a, uint32_t unit, const EvictRow& er, uint64_t t0,
+                                           uint32_t lane, WideValueWords<BITS>& vw, float4& p0, float4& p1,
+                                           float ev_scale, float ev_amax) {
+  constexpr int PPW = 32 / BITS, VW = 2 * BITS, VG = BITS / 2;
+  constexpr float kLevels = static_cast<float>((1 << BITS) - 1);
+  const uint32_t g = lane / 16, n = lane % 16;
+  const uint32_t tt = static_cast<uint32_t>(a.st.vq - 1 - t0);  // the token within the chunk
+  const uint64_t tb = t0 / 64;
+  const uint32_t c0 = evict_code(er.x[0], er.mn[0], er.sc[0], kLevels);  // channel lane
+  const uint32_t c1 = evict_code(er.x[1], er.mn[1], er.sc[1], kLevels);  // channel 64 + lane
+  // lane group tt/16 holds the token's word (tt % 16) / PPW of its share, for channel 16mt + n
+  const uint32_t wi = (tt % 16) / PPW, sh = code_shift(BITS, tt % PPW);
+#pragma unroll
+  for (int mt = 0; mt < 8; ++mt) {
+    const uint32_t code = static_cast<uint32_t>(__shfl(static_cast<int>(mt < 4 ? c0 : c1), (16 * mt + n) % 64));
+    if (g == tt / 16) {
+#pragma unroll
+      for (int i = 0; i < VG; ++i) {
+        if (i == (int)wi) {
+          vw.w[mt][i] |= code << sh;
+          a.c.vcodes[unit * a.c.geo.vcodes_unit() + ((uint64_t)tb * 128 + 16 * mt + n) * VW + VG * g + i] = vw.w[mt][i];
+        }
+      }
+    }
+  }
+  // the pair of group g (channels 32g .. +31: the quantizer's half-wave g % 2 of hv = g / 2) for
+  // token tt, held by the lane of group g with n == tt / 4 (pairs of tokens 4n .. 4n + 3)
+  float sc = 0.f, mn = 0.f;
+#pragma unroll
+  for (int cg = 0; cg < 4; ++cg) {
+    const float s = lane_value(er.sc[cg / 2], 32 * (cg % 2));
+    const float m = lane_value(er.mn[cg / 2], 32 * (cg % 2));
+    if (g == (uint32_t)cg) {
+      sc = s;
+      mn = m;
+    }
+  }
+  if (n == tt / 4) {
+    const uint32_t j = tt % 4;
+    if (j == 0) {
+      p0.x = sc;
+      p0.y = mn;
+    } else if (j == 1) {
+      p0.z = sc;
+      p0.w = mn;
+    } else if (j == 2) {
+      p1.x = sc;
+      p1.y = mn;
+    } else {
+      p1.z = sc;
+      p1.w = mn;
+    }
+    *reinterpret_cast<float2*>(a.c.vparams + unit * a.c.geo.vparams_unit() + (((uint64_t)tb * 4 + g) * 64 + tt) * 2) =
+        make_float2(sc, mn);
+  }
+  if (lane == 0) {
+    atomicMax(max_slot(a.c.smax, unit, 0) + kMaxValueScale, __float_as_uint(ev_scale));
+    atomicMax(max_slot(a.c.smax, unit, 0) + kMaxValueAbs, __float_as_uint(ev_amax));
+  }
+}
+
+// EVICT: the launch also appends a decode token whose window eviction lands in the packed
+// range (a separate instantiation, so the plain attention keeps its register budget).
+template <int BITS, bool EVICT>
 __device__ __forceinline__ void wide_split(const AttnArgs& a, uint32_t unit, uint32_t split, uint32_t hg,
                                            float* lds) {
   constexpr int CPW = wide_cpw(BITS), NH = kWideHeads, D = 128;
@@ -1430,6 +1501,14 @@ __device__ __forceinline__ void wide_split(const AttnArgs& a, uint32_t unit, uin
   if (nch > 0) {
     wide_load_key_params(a, unit, chunk_of(0), lane, kp0, kp1);
     wide_load_keys<BITS>(a, unit, chunk_of(0), g, n, kw0);
+  }
+  // a decode token appended by this launch evicts token vq-1 from the window: its row, in the
+  // value quantizer's layout (channels lane and 64 + lane)
+  EvictRow er{};
+  if constexpr (EVICT) {
+    const float* row = a.c.vring + ((uint64_t)unit * a.c.geo.R + a.pend_vslot) * D;
+    er.x[0] = row[lane];
+    er.x[1] = row[lane + 64];
   }
   // q in base-2 logit units: head hg*8 + hq, channels 32g .. 32g+31 (0 for padded heads)
   float qv[32];
@@ -1521,7 +1600,14 @@ __device__ __forceinline__ void wide_split(const AttnArgs& a, uint32_t unit, uin
   mx = fmaxf(mx, __shfl_xor(mx, 32));
   const float mrow = mx * kout;
 
-  const float vmax = unit_max(a.c.smax, unit, kMaxValueScale);
+  // the value operands' range: the unit's largest value scale, raised by the evicted row's (as
+  // the append would have raised it)
+  float vmax = unit_max(a.c.smax, unit, kMaxValueScale);
+  float ev_scale = 0.f, ev_amax = 0.f;
+  if constexpr (EVICT) {
+    evict_groups(er, static_cast<float>((1 << BITS) - 1), ev_scale, ev_amax);
+    vmax = fmaxf(vmax, ev_scale);
+  }
   const int ev = std::min(60, std::max(-100, 15 - __builtin_amdgcn_frexp_expf(vmax)));
   const float vout = ldexpf(1.f, -ev - kExp);
   const float moff = mrow == -INFINITY ? 0.f : mrow;
@@ -1541,7 +1627,7 @@ __device__ __forceinline__ void wide_split(const AttnArgs& a, uint32_t unit, uin
       wide_load_value_params(a, unit, chunk_of(0), lane, vp0, vp1);
       wide_load_values<BITS>(a, unit, chunk_of(0), g, n, vw0);
     }
-    auto step = [&](int k, const WideValueWords<BITS>& cur, WideValueWords<BITS>& next) {
+    auto step = [&](int k, WideValueWords<BITS>& cur, WideValueWords<BITS>& next) {
       // weights (times 2^ev) of head hq, tokens 16g .. 16g+15, read from the slot before the
       // chunk's (scale, zero) pairs are staged over it
       float4 lg[4];
@@ -1549,6 +1635,10 @@ __device__ __forceinline__ void wide_split(const AttnArgs& a, uint32_t unit, uin
         const float4* lp = reinterpret_cast<const float4*>(wl + hq * ROW + k * 64 + 16 * g);
 #pragma unroll
         for (int r = 0; r < 4; ++r) lg[r] = lp[r];
+      }
+      if constexpr (EVICT) {
+        const uint64_t t0 = (uint64_t)chunk_of(k) * 64;
+        if (t0 < a.st.vq && t0 + 64 >= a.st.vq) wide_evict<BITS>(a, unit, er, t0, lane, cur, vp0, vp1, ev_scale, ev_amax);
       }
       wide_stage(wl, ROW, k, lane, vp0, vp1);
       const int32_t kn = chunk_of(std::min(k + 1, nch - 1));
@@ -1657,9 +1747,11 @@ __device__ __forceinline__ void wide_split(const AttnArgs& a, uint32_t unit, uin
 
 // Eight-head launch at head_dim 128, G = 32: the window / suffix chunk workgroups first (the
 // 4x4x4 MIXED path), then the packed splits on the 16x16x32 path, wide_blocks(BITS)
-// workgroups per CU. Requests two chunks ahead measured slower than one.
-template <int BITS>
-__global__ void __launch_bounds__(kThreads, wide_blocks(BITS)) k_attn_wide(AttnArgs a) {
+// workgroups per CU. Requests two chunks ahead measured slower than one. A launch that also
+// appends a decode token (EVICT) takes the register budget of two workgroups per CU, so the
+// eviction's registers spill nothing (a decode launch is latency-bound).
+template <int BITS, bool EVICT>
+__global__ void __launch_bounds__(kThreads, EVICT ? 2 : wide_blocks(BITS)) k_attn_wide(AttnArgs a) {
   extern __shared__ float lds[];
   const uint32_t nwin = a.units * a.hgroups * a.nsplit_win;
   if (blockIdx.x < nwin) {
@@ -1668,7 +1760,7 @@ __global__ void __launch_bounds__(kThreads, wide_blocks(BITS)) k_attn_wide(AttnA
     return;
   }
   const uint32_t blk = blockIdx.x - nwin, vu = blk / a.nsplit_fast;
-  wide_split<BITS>(a, vu / a.hgroups, blk % a.nsplit_fast, vu % a.hgroups, lds);
+  wide_split<BITS, EVICT>(a, vu / a.hgroups, blk % a.nsplit_fast, vu % a.hgroups, lds);
 }
 
 // Arguments of session s of a batched call: its queries, partials and suffix.
@@ -2711,9 +2803,7 @@ AttnArgs make_args(const AttnProblem& p, float* ws) {
   a.win_end = fast_win ? static_cast<uint32_t>((a.total + 63) / 64) : a.chunk_end;
   a.hgroups = fast ? head_groups(p.cache.geo.D, a.gq) : 1u;
   a.gshift = fast ? static_cast<uint32_t>(__builtin_ctz(p.cache.geo.G)) : 5u;
-  // a launch that also appends a decode token keeps the 4x4x4 kernel (it quantizes the
-  // evicted window row); such launches are not made for these shapes (attention_fuses_decode)
-  a.wide = fast && wide_shape(p) && a.pend_evict == 0 ? 1u : 0u;
+  a.wide = fast && wide_shape(p) ? 1u : 0u;
   // packed splits per unit: at most kFastCpw (wide_cpw) chunks per wave, at least one, and at
   // least kFastGroups workgroups (over units and head groups) when the chunks allow
   {
@@ -2765,7 +2855,10 @@ hipError_t launch_fast(const AttnArgs& a, double bytes, hipStream_t stream) {
       const size_t wide = (size_t)4 * kWideHeads * (wide_cpw(BITS) * 64 + kRowPad);
       const size_t mixed = (size_t)4 * NH * (64 + kRowPad);
       const size_t wlds = std::max(std::max(wide, mixed), combine) * sizeof(float);
-      k_attn_wide<BITS><<<grid, kThreads, wlds, stream>>>(a);
+      if (a.pend_evict)
+        k_attn_wide<BITS, true><<<grid, kThreads, wlds, stream>>>(a);
+      else
+        k_attn_wide<BITS, false><<<grid, kThreads, wlds, stream>>>(a);
       return hipGetLastError();
     }
   }
@@ -2856,12 +2949,11 @@ hipError_t launch_fill_zero(float* out, size_t n, hipStream_t stream) {
 
 // The decode fused into the attention launch quantizes the evicted window token with the
 // 32-channel value groups of one half-wave, once per chunk workgroup: G = 32, one head group
-// of up to four heads (eight-head units take the 16x16x32 kernel, which does not append: their
-// decode is an append launch and an attention launch, bit for bit the same as those calls).
+// (up to four heads on the 4x4x4 kernel, five to eight on the 16x16x32 one).
 bool attention_fuses_decode(const AttnProblem& p) {
   const AttnArgs a = make_args(p, nullptr);
   return a.total > 0 && a.nsplit_gen == 0 && (a.nsplit_fast > 0 || a.nsplit_win > 0) &&
-         p.cache.geo.D == 128 && p.cache.geo.G == 32 && a.hgroups == 1 && !wide_shape(p);
+         p.cache.geo.D == 128 && p.cache.geo.G == 32 && a.hgroups == 1;
 }
 
 size_t attention_workspace_floats(const AttnProblem& p) {

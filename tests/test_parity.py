@@ -520,12 +520,13 @@ def test_runtime_decode_parity(amd, oracle):
 
 @pytest.mark.parametrize("bits,residual,gqa,group,dim", [
     (2, 64, 4, 32, 128), (4, 64, 8, 32, 128), (8, 128, 4, 32, 128), (2, 128, 1, 32, 128), (2, 128, 4, 64, 128),
-    (4, 128, 16, 128, 128), (4, 64, 4, 32, 64), (2, 128, 8, 64, 256)])
+    (4, 128, 16, 128, 128), (4, 64, 4, 32, 64), (2, 128, 8, 64, 256), (2, 128, 8, 32, 128), (8, 64, 6, 32, 128),
+    (2, 64, 5, 32, 128)])
 def test_runtime_decode_device_parity(amd, oracle, bits, residual, gqa, group, dim):
     """RuntimeKv::decode on device pointers, which runs append + attention in one attention
-    launch (the token the window evicts quantized inside it) for G = 32 and GQA <= 4 when no
-    key flush is due, and as an append then an attention launch otherwise (GQA 8 here: the
-    eight-head kernel does not append): bit for bit equal to
+    launch (the token the window evicts quantized inside it) for head_dim 128, G = 32 and GQA
+    <= 8 (GQA 5-8 on the eight-head kernel) when no key flush is due, and as an append then an
+    attention launch otherwise (GQA 16, G 64/128, head_dim 64/256 here): bit for bit equal to
     a cache taking append_device then attention_device (tests/runtime.rs:13-52), and within
     tolerance of the oracle's decode, streams bit-exact, across evictions and flushes."""
     heads, prefill, steps = 2, 3 * residual + 17, 2 * residual + 5
@@ -561,13 +562,14 @@ def test_runtime_decode_device_parity(amd, oracle, bits, residual, gqa, group, d
     mem.free()
 
 
-@pytest.mark.parametrize("bits", [2, 8])
-def test_decode_device_zero_minima_parity(amd, oracle, bits):
+@pytest.mark.parametrize("bits,gqa", [(2, 4), (8, 4), (4, 8), (8, 7)])
+def test_decode_device_zero_minima_parity(amd, oracle, bits, gqa):
     """RuntimeKv::decode on device pointers with window rows whose channel groups have zero
     minima and zeros of both signs: the token each step evicts is quantized inside the
-    attention launch, and its stored zeros must be each group's first zero, as the oracle's
-    decode stores them (src/quant.rs:356)."""
-    heads, dim, residual, gqa = 2, 128, 64, 4
+    attention launch (the 4x4x4 kernel at GQA 4, the eight-head kernel at GQA 7-8), and its
+    stored zeros must be each group's first zero, as the oracle's decode stores them
+    (src/quant.rs:356)."""
+    heads, dim, residual = 2, 128, 64
     prefill, steps = 3 * residual + 17, 2 * residual + 5
     qh = heads * gqa
     cfg = KiviConfig(bits, 32, residual)
