@@ -345,7 +345,7 @@ struct CacheCore {
     const size_t arenas = (geo.kcodes_unit() + geo.kparams_unit() + geo.vcodes_unit() +
                            geo.vparams_unit()) * geo.units * 4;
     return arenas + 2 * (size_t)geo.units * geo.R * geo.D * sizeof(float) +
-           (size_t)geo.units * 4 * sizeof(uint32_t);
+           (size_t)geo.units * kMaxUnitWords * sizeof(uint32_t);
   }
 
   Status init(hipStream_t s) {
