@@ -25,8 +25,9 @@ Infinity Cache rotate over identical copies between steps (`cache_copies`), so e
 HBM; C0 and C1 are too small for that and report `cache_resident: true`.
 
 `roofline` is for the dominant kernel: the packed-chunk attention kernel (k_attn_mfma, or
-k_attn_wide for the eight-head units of c3; HBM bound: algorithmic bytes per launch over its
-mean launch duration), or for c4 the shared-prefix GEMM kernel (k_attn_shared, matrix-core
+k_attn_wide for the eight-head units of c3, k_attn_wide16 for GQA 16; HBM bound: algorithmic
+bytes per launch over its mean launch duration), or for c4 the shared-prefix GEMM kernel
+(k_attn_shared, matrix-core
 bound: 4*D flops per (session row, prefix token) over its mean duration, against the dense
 f16 MFMA peak). `traffic` is that kernel's HBM bytes per
 launch from rocprofv3 FETCH_SIZE + WRITE_SIZE runs calibrated on a plain copy kernel
@@ -533,10 +534,12 @@ def measure(name, args, torch, kivi, amd, stream, with_cpu):
     if sessions_cfg and "attn_shared" in kernels:
         dom_fam, dom_name = "attn_shared", "k_attn_shared"
     elif "attn_packed" in kernels:
-        # eight-head units (GQA 5..8 and head groups of 8) at head_dim 128, G = 32 run their
-        # packed chunks on the 16x16x32 kernel
-        wide = dim == 128 and G == 32 and qh // heads > 4
-        dom_fam, dom_name = "attn_packed", "k_attn_wide" if wide else "k_attn_mfma"
+        # units of five or more heads at head_dim 128, G = 32 run their packed chunks on the
+        # 16x16x32 kernels: sixteen-head groups for GQA a multiple of 16, eight-head otherwise
+        gqa = qh // heads
+        wide = dim == 128 and G == 32 and gqa > 4
+        dom_name = ("k_attn_wide16" if gqa % 16 == 0 else "k_attn_wide") if wide else "k_attn_mfma"
+        dom_fam = "attn_packed"
     elif "attn_sessions" in kernels:
         dom_fam, dom_name = "attn_sessions", "k_attn_sessions"
     else:

@@ -78,10 +78,13 @@ struct AttnArgs {
   uint32_t nsplit_win;
   uint32_t nsplit_total;   // splits per unit in the workspace
   // query heads in groups of up to 8 (GQA > 8 on the matrix-core path): one workgroup per
-  // (unit, head group, split), each writing its group's partial rows
-  uint32_t hgroups;
+  // (unit, head group, split), each writing its group's partial rows. hgroups_fast: the head
+  // groups of the packed splits (groups of 16 on the sixteen-head kernel, hgroups otherwise)
+  uint32_t hgroups, hgroups_fast;
   uint32_t gshift;         // log2(G) on the matrix-core path (G = 32, 64 or 128 there)
-  uint32_t wide;           // packed splits on the eight-head 16x16x32 kernel (k_attn_wide)
+  // packed splits on the 16x16x32 kernels: 1 eight-head (k_attn_wide), 2 sixteen-head
+  // (k_attn_wide16)
+  uint32_t wide;
   float* ws;               // [units][nsplit_total][gq][D+2]
   // batched sessions (0 otherwise): session count and the strides between consecutive
   // sessions' queries, partials and outputs
@@ -1763,6 +1766,269 @@ __global__ void __launch_bounds__(kThreads, EVICT ? 2 : wide_blocks(BITS)) k_att
   wide_split<BITS, EVICT>(a, vu / a.hgroups, blk % a.nsplit_fast, vu % a.hgroups, lds);
 }
 
+// ------------------------------------------------------------------ sixteen-head 16x16x32 path
+// GQA 16 (or a multiple of 16) at head_dim 128, G = 32: the MFMA's 16 columns are the 16 heads
+// of a head group, so the two key groups of a chunk (and its four value groups) take B
+// operands of their own and no column is spent on another group's scales. Each chunk is read
+// once for the 16 heads; the eight-head form reads it once per eight. Layout and chunk
+// dealing as in wide_split: lane (g, n) holds column n (head 16*hg + n) and K slots 8g .. 8g+7.
+constexpr int kWide16Heads = 16;
+constexpr int kWide16Cpw = 4;     // chunks per wave: four chunks of 16 heads' logits, 16.6 KB
+constexpr int kWide16Blocks = 2;  // workgroups per CU (66.6 KB of LDS each)
+
+template <int BITS>
+__device__ __forceinline__ void wide16_split(const AttnArgs& a, uint32_t unit, uint32_t split, uint32_t hg,
+                                             float* lds) {
+  constexpr int CPW = kWide16Cpw, NH = kWide16Heads, D = 128;
+  constexpr int ROW = CPW * 64 + kRowPad;
+  constexpr int kExp = CodeUnit<BITS>::kExp;
+  constexpr float kUnit = kExp == 0 ? 1.0f : kExp == -1 ? 0.5f : 0.001953125f;
+  const uint32_t b = unit / a.heads, kvh = unit % a.heads;
+  const uint32_t lane = threadIdx.x % 64, wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+  const uint32_t g = lane / 16, n = lane % 16;  // n: the lane's column (head)
+  const uint32_t gq = a.gq;
+  float* wl = lds + wave * NH * ROW;  // this wave's logits [NH][ROW] (and staging)
+
+  const int32_t slots = static_cast<int32_t>(a.nsplit_fast * 4);
+  const int32_t slot = static_cast<int32_t>(split * 4 + wave);
+  const int32_t span = static_cast<int32_t>(a.chunk_end - a.chunk_begin);
+  const int32_t nch = std::min<int32_t>(CPW, std::max<int32_t>(0, (span - slot + slots - 1) / slots));
+  auto chunk_of = [&](int32_t k) { return static_cast<int32_t>(a.chunk_begin) + slot + k * slots; };
+
+  WideKeyWords<BITS> kw0, kw1;
+  float4 kp0, kp1;
+  if (nch > 0) {
+    wide_load_key_params(a, unit, chunk_of(0), lane, kp0, kp1);
+    wide_load_keys<BITS>(a, unit, chunk_of(0), g, n, kw0);
+  }
+  // q in base-2 logit units: head hg*16 + n, channels 32g .. 32g+31 (0 for padded heads)
+  float qv[32];
+  float qmax = 0.f;
+  {
+    const uint32_t h = hg * NH + n;
+    const float s = h < gq ? a.scale2 : 0.f;
+    const float* qp = a.query + ((uint64_t)b * a.qh + kvh * gq + min(h, gq - 1)) * D + 32 * g;
+#pragma unroll
+    for (int r = 0; r < 32; r += 4) {
+      const float4 v = *reinterpret_cast<const float4*>(qp + r);
+      qv[r] = v.x * s;
+      qv[r + 1] = v.y * s;
+      qv[r + 2] = v.z * s;
+      qv[r + 3] = v.w * s;
+    }
+#pragma unroll
+    for (int r = 0; r < 32; ++r) qmax = fmaxf(qmax, fabsf(qv[r]));
+  }
+  qmax = warp_max(qmax);
+  const float kmax = unit_max(a.c.smax, unit, kMaxKeyScale);
+  const int ek = std::min(60, std::max(-100, 15 - __builtin_amdgcn_frexp_expf(qmax * kmax)));
+  const float kfac = ldexpf(1.f, ek);
+  const float kout = ldexpf(1.f, -ek - kExp);
+#pragma unroll
+  for (int r = 0; r < 32; ++r) qv[r] *= kfac;
+
+  // ---------------- phase 1: logits of every owned chunk into LDS (scaled by 2^(ek+kExp))
+  float mx = -INFINITY;
+  {
+    auto step = [&](int k, const WideKeyWords<BITS>& cur, WideKeyWords<BITS>& next) {
+      wide_stage(wl, ROW, k, lane, kp0, kp1);
+      const int32_t kn = chunk_of(std::min(k + 1, nch - 1));
+      wide_load_key_params(a, unit, kn, lane, kp0, kp1);
+      wide_load_keys<BITS>(a, unit, kn, g, n, next);
+      v4f acc[4];
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) acc[mt] = v4f{0.f, 0.f, 0.f, 0.f};
+      float bias[2] = {0.f, 0.f};
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+        // channels 32g + 8kt .. +7: one B per key group (tiles 0, 1 take group 0; 2, 3 group 1)
+        h8 bhi[2], blo[2];
+#pragma unroll
+        for (int grp = 0; grp < 2; ++grp) {
+          const float4* sp = reinterpret_cast<const float4*>(wide_stage_at(wl, ROW, k, (grp * 128 + 32 * g + 8 * kt) * 2));
+          const float4 sv[4] = {sp[0], sp[1], sp[2], sp[3]};
+          float p[8];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            p[2 * j] = qv[8 * kt + 2 * j] * sv[j].x;
+            p[2 * j + 1] = qv[8 * kt + 2 * j + 1] * sv[j].z;
+            bias[grp] = fmaf(qv[8 * kt + 2 * j], sv[j].y, bias[grp]);
+            bias[grp] = fmaf(qv[8 * kt + 2 * j + 1], sv[j].w, bias[grp]);
+          }
+          wide_split8(p, bhi[grp], blo[grp]);
+        }
+#pragma unroll
+        for (int m2 = 0; m2 < 4; m2 += 2) {
+          const h8 A0 = wide_key_codes<BITS>(cur, m2, kt), A1 = wide_key_codes<BITS>(cur, m2 + 1, kt);
+          acc[m2] = mfma_wide(A0, bhi[m2 / 2], acc[m2]);
+          acc[m2 + 1] = mfma_wide(A1, bhi[m2 / 2], acc[m2 + 1]);
+          acc[m2] = mfma_wide(A0, blo[m2 / 2], acc[m2]);
+          acc[m2 + 1] = mfma_wide(A1, blo[m2 / 2], acc[m2 + 1]);
+        }
+      }
+      // each key group's zero term of the lane's column over all 128 channels (lane groups g)
+#pragma unroll
+      for (int grp = 0; grp < 2; ++grp) {
+        bias[grp] += __shfl_xor(bias[grp], 16);
+        bias[grp] += __shfl_xor(bias[grp], 32);
+      }
+      // tile mt: tokens 16mt + 4g .. +3 of key group mt / 2
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+        const float bu = bias[mt / 2] * kUnit;
+        const v4f v = acc[mt];
+        const float4 o = make_float4(v[0] + bu, v[1] + bu, v[2] + bu, v[3] + bu);
+        *reinterpret_cast<float4*>(wl + n * ROW + k * 64 + 16 * mt + 4 * g) = o;
+        mx = fmaxf(mx, fmaxf(fmaxf(o.x, o.y), fmaxf(o.z, o.w)));
+      }
+    };
+    for (int k = 0; k < nch; k += 2) {
+      step(k, kw0, kw1);
+      if (k + 1 < nch) step(k + 1, kw1, kw0);
+    }
+  }
+  // wave max per head: the four lane groups of column n
+  mx = fmaxf(mx, __shfl_xor(mx, 16));
+  mx = fmaxf(mx, __shfl_xor(mx, 32));
+  const float mrow = mx * kout;
+
+  const float vmax = unit_max(a.c.smax, unit, kMaxValueScale);
+  const int ev = std::min(60, std::max(-100, 15 - __builtin_amdgcn_frexp_expf(vmax)));
+  const float vout = ldexpf(1.f, -ev - kExp);
+  const float moff = mrow == -INFINITY ? 0.f : mrow;
+  const float evoff = static_cast<float>(ev) - moff;  // weights times 2^ev from the exponential
+  const float vinv = ldexpf(1.f, -ev);
+
+  // ---------------- phase 2: value mix
+  v4f vacc[8];
+#pragma unroll
+  for (int mt = 0; mt < 8; ++mt) vacc[mt] = v4f{0.f, 0.f, 0.f, 0.f};
+  float zacc[4] = {0.f, 0.f, 0.f, 0.f};  // zero terms of the four value groups
+  float lsum = 0.f;
+  {
+    WideValueWords<BITS> vw0, vw1;
+    float4 vp0, vp1;
+    if (nch > 0) {
+      wide_load_value_params(a, unit, chunk_of(0), lane, vp0, vp1);
+      wide_load_values<BITS>(a, unit, chunk_of(0), g, n, vw0);
+    }
+    auto step = [&](int k, const WideValueWords<BITS>& cur, WideValueWords<BITS>& next) {
+      // weights (times 2^ev) of head n, tokens 16g .. 16g+15, read from the slot before the
+      // chunk's (scale, zero) pairs are staged over it
+      float4 lg[4];
+      {
+        const float4* lp = reinterpret_cast<const float4*>(wl + n * ROW + k * 64 + 16 * g);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) lg[r] = lp[r];
+      }
+      wide_stage(wl, ROW, k, lane, vp0, vp1);
+      const int32_t kn = chunk_of(std::min(k + 1, nch - 1));
+      wide_load_value_params(a, unit, kn, lane, vp0, vp1);
+      wide_load_values<BITS>(a, unit, kn, g, n, next);
+      float w[16];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float4 x = lg[r];
+        w[4 * r] = __builtin_amdgcn_exp2f(fmaf(x.x, kout, evoff));
+        w[4 * r + 1] = __builtin_amdgcn_exp2f(fmaf(x.y, kout, evoff));
+        w[4 * r + 2] = __builtin_amdgcn_exp2f(fmaf(x.z, kout, evoff));
+        w[4 * r + 3] = __builtin_amdgcn_exp2f(fmaf(x.w, kout, evoff));
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) lsum += w[r];
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+        for (int cg = 0; cg < 4; ++cg) {
+          // value group cg (channel tiles 2cg, 2cg+1), tokens 16g + 8kt .. +7
+          const float4* sp = reinterpret_cast<const float4*>(wide_stage_at(wl, ROW, k, (cg * 64 + 16 * g + 8 * kt) * 2));
+          const float4 sv[4] = {sp[0], sp[1], sp[2], sp[3]};
+          float p[8];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            p[2 * j] = w[8 * kt + 2 * j] * sv[j].x;
+            p[2 * j + 1] = w[8 * kt + 2 * j + 1] * sv[j].z;
+            zacc[cg] = fmaf(w[8 * kt + 2 * j], sv[j].y, zacc[cg]);
+            zacc[cg] = fmaf(w[8 * kt + 2 * j + 1], sv[j].w, zacc[cg]);
+          }
+          h8 bhi, blo;
+          wide_split8(p, bhi, blo);
+          const h8 A0 = wide_value_codes<BITS>(cur, 2 * cg, kt), A1 = wide_value_codes<BITS>(cur, 2 * cg + 1, kt);
+          vacc[2 * cg] = mfma_wide(A0, bhi, vacc[2 * cg]);
+          vacc[2 * cg + 1] = mfma_wide(A1, bhi, vacc[2 * cg + 1]);
+          vacc[2 * cg] = mfma_wide(A0, blo, vacc[2 * cg]);
+          vacc[2 * cg + 1] = mfma_wide(A1, blo, vacc[2 * cg + 1]);
+        }
+      }
+    };
+    for (int k = 0; k < nch; k += 2) {
+      step(k, vw0, vw1);
+      if (k + 1 < nch) step(k + 1, vw1, vw0);
+    }
+  }
+
+  // ---------------- wave partial: sums over the lane groups, then the output rows
+  lsum += __shfl_xor(lsum, 16);
+  lsum += __shfl_xor(lsum, 32);
+#pragma unroll
+  for (int cg = 0; cg < 4; ++cg) {
+    zacc[cg] += __shfl_xor(zacc[cg], 16);
+    zacc[cg] += __shfl_xor(zacc[cg], 32);
+  }
+  __syncthreads();  // every wave is done with its logits; reuse LDS for the combine
+  float* cw = lds + wave * NH * (D + 2);
+  // tile mt: channels 16mt + 4g .. +3 of head n (value group mt / 2)
+#pragma unroll
+  for (int mt = 0; mt < 8; ++mt) {
+    const float z = zacc[mt / 2] * vinv;
+    const v4f v = vacc[mt];
+    float2* o = reinterpret_cast<float2*>(cw + n * (D + 2) + 16 * mt + 4 * g);
+    o[0] = make_float2(fmaf(v[0], vout, z), fmaf(v[1], vout, z));
+    o[1] = make_float2(fmaf(v[2], vout, z), fmaf(v[3], vout, z));
+  }
+  if (g == 0) {
+    cw[n * (D + 2) + D] = nch > 0 ? mrow : -INFINITY;
+    cw[n * (D + 2) + D + 1] = nch > 0 ? lsum * vinv : 0.f;
+  }
+  __syncthreads();
+  const uint32_t hrows = std::min<uint32_t>(NH, gq - hg * NH);
+  float* part = a.ws + (((uint64_t)unit * a.nsplit_total + split) * gq + hg * NH) * (D + 2);
+  for (uint32_t idx = threadIdx.x; idx < hrows * (D + 2); idx += blockDim.x) {
+    const uint32_t h = idx / (D + 2), d = idx % (D + 2);
+    float M = -INFINITY;
+#pragma unroll
+    for (int wv = 0; wv < 4; ++wv) M = fmaxf(M, lds[wv * NH * (D + 2) + h * (D + 2) + D]);
+    float v = 0.f;
+    if (d == D) {
+      v = M;
+    } else {
+#pragma unroll
+      for (int wv = 0; wv < 4; ++wv) {
+        const float* c = lds + wv * NH * (D + 2) + h * (D + 2);
+        const float f = c[D] == -INFINITY ? 0.f : exp2f(c[D] - M);
+        v += (d == D + 1 ? c[D + 1] : c[d]) * f;
+      }
+    }
+    part[h * (D + 2) + d] = v;
+  }
+}
+
+// Sixteen-head launch at head_dim 128, G = 32, GQA a multiple of 16: the window / suffix chunk
+// workgroups first (the 4x4x4 MIXED path, in head groups of eight), then the packed splits on
+// the sixteen-head 16x16x32 path (head groups of sixteen), two workgroups per CU.
+template <int BITS>
+__global__ void __launch_bounds__(kThreads, kWide16Blocks) k_attn_wide16(AttnArgs a) {
+  extern __shared__ float lds[];
+  const uint32_t nwin = a.units * a.hgroups * a.nsplit_win;
+  if (blockIdx.x < nwin) {
+    const uint32_t vu = blockIdx.x / a.nsplit_win;
+    mfma_split<BITS, 2, 1, true, 128>(a, vu / a.hgroups, blockIdx.x % a.nsplit_win, vu % a.hgroups, lds);
+    return;
+  }
+  const uint32_t blk = blockIdx.x - nwin, vu = blk / a.nsplit_fast;
+  wide16_split<BITS>(a, vu / a.hgroups_fast, blk % a.nsplit_fast, vu % a.hgroups_fast, lds);
+}
+
 // Arguments of session s of a batched call: its queries, partials and suffix.
 __device__ __forceinline__ AttnArgs session_args(const AttnArgs& a, const SessionTable& t,
                                                  uint32_t s) {
@@ -2762,6 +3028,11 @@ bool wide_shape(const AttnProblem& p) {
   const uint32_t gq = p.qh / p.heads;
   return fast_eligible(p) && p.cache.geo.D == 128 && p.cache.geo.G == 32 && fast_nrs(128, gq) == 2;
 }
+// GQA a multiple of 16 at head_dim 128 and G = 32: packed splits on the sixteen-head kernel.
+bool wide16_shape(const AttnProblem& p) {
+  const uint32_t gq = p.qh / p.heads;
+  return fast_eligible(p) && p.cache.geo.D == 128 && p.cache.geo.G == 32 && gq % 16 == 0;
+}
 uint32_t head_groups(uint32_t D, uint32_t gq) {
   const uint32_t per = 4u * static_cast<uint32_t>(fast_nrs(D, gq));
   return (gq + per - 1) / per;
@@ -2803,13 +3074,15 @@ AttnArgs make_args(const AttnProblem& p, float* ws) {
   a.win_end = fast_win ? static_cast<uint32_t>((a.total + 63) / 64) : a.chunk_end;
   a.hgroups = fast ? head_groups(p.cache.geo.D, a.gq) : 1u;
   a.gshift = fast ? static_cast<uint32_t>(__builtin_ctz(p.cache.geo.G)) : 5u;
-  a.wide = fast && wide_shape(p) ? 1u : 0u;
+  a.wide = !(fast && wide_shape(p)) ? 0u : wide16_shape(p) ? 2u : 1u;
+  a.hgroups_fast = a.wide == 2 ? a.gq / kWide16Heads : a.hgroups;
   // packed splits per unit: at most kFastCpw (wide_cpw) chunks per wave, at least one, and at
   // least kFastGroups workgroups (over units and head groups) when the chunks allow
   {
-    const uint32_t units = p.cache.geo.units * a.hgroups;
-    const uint32_t cpw = a.wide ? static_cast<uint32_t>(wide_cpw(static_cast<int>(p.cache.geo.bits)))
-                                : static_cast<uint32_t>(fast_cpw(static_cast<int>(p.cache.geo.bits), fast_nrs(p.cache.geo.D, a.gq)));
+    const uint32_t units = p.cache.geo.units * a.hgroups_fast;
+    const uint32_t cpw = a.wide == 2 ? static_cast<uint32_t>(kWide16Cpw)
+                         : a.wide ? static_cast<uint32_t>(wide_cpw(static_cast<int>(p.cache.geo.bits)))
+                                  : static_cast<uint32_t>(fast_cpw(static_cast<int>(p.cache.geo.bits), fast_nrs(p.cache.geo.D, a.gq)));
     const uint32_t fewest = (a.chunk_end + 4 * cpw - 1) / (4 * cpw);
     const uint32_t most = (a.chunk_end + 3) / 4;
     a.nsplit_fast = std::min(most, std::max(fewest, (kFastGroups + units - 1) / units));
@@ -2849,8 +3122,16 @@ hipError_t launch_fast(const AttnArgs& a, double bytes, hipStream_t stream) {
   const size_t gen = a.nsplit_gen > 0 ? (size_t)a.gq * (D + a.S) : 0;  // generic splits' q and weights
   const size_t lds = std::max(std::max(logits, combine), gen) * sizeof(float);
   TimedLaunch timed(KIVI_KERNEL_ATTN_PACKED, stream, bytes);
-  const uint32_t grid = a.units * (a.hgroups * (a.nsplit_win + a.nsplit_fast) + a.nsplit_gen);
+  const uint32_t grid = a.units * (a.hgroups * a.nsplit_win + a.hgroups_fast * a.nsplit_fast + a.nsplit_gen);
   if constexpr (D == 128 && NRS == 2) {
+    if (a.wide == 2) {
+      const size_t wide = (size_t)4 * kWide16Heads * (kWide16Cpw * 64 + kRowPad);
+      const size_t mixed = (size_t)4 * NH * (64 + kRowPad);
+      const size_t comb16 = (size_t)4 * kWide16Heads * (D + 2);
+      const size_t wlds = std::max(std::max(wide, mixed), comb16) * sizeof(float);
+      k_attn_wide16<BITS><<<grid, kThreads, wlds, stream>>>(a);
+      return hipGetLastError();
+    }
     if (a.wide) {
       const size_t wide = (size_t)4 * kWideHeads * (wide_cpw(BITS) * 64 + kRowPad);
       const size_t mixed = (size_t)4 * NH * (64 + kRowPad);

@@ -128,13 +128,15 @@ def test_other_shapes_attention_parity(amd, oracle, dim, group, gqa, bits):
 
 @pytest.mark.parametrize("bits,gqa,batch,heads,seq", [
     (2, 5, 1, 2, 200), (4, 6, 2, 1, 777), (8, 7, 1, 2, 2600), (4, 8, 1, 3, 4321), (2, 8, 2, 2, 9000),
-    (8, 12, 1, 2, 5000), (4, 16, 1, 1, 3000)])
+    (8, 12, 1, 2, 5000), (4, 16, 1, 1, 3000), (2, 16, 2, 2, 9000), (8, 16, 1, 2, 5000), (4, 32, 1, 1, 6000),
+    (2, 48, 1, 1, 2000), (4, 16, 1, 3, 70), (2, 16, 1, 1, 200)])
 def test_eight_head_units_attention_parity(amd, oracle, bits, gqa, batch, heads, seq):
-    """Eight-head units at head_dim 128 and G = 32 (GQA 5..8, and head groups of eight above)
-    take the 16x16x32 kernel for their packed chunks: padded heads (GQA 5..7), a short last
-    head group (GQA 12), waves that own fewer chunks than they hold or none (seq 200: one
-    packed chunk for four waves), the window chunks in the same launch, and many splits;
-    against the oracle and f64 dense attention on the dequantized cache."""
+    """Units of five or more query heads at head_dim 128 and G = 32 take the 16x16x32
+    kernels for their packed chunks: eight-head groups for GQA 5..8 and 12, sixteen-head groups
+    for GQA 16, 32, 48. Padded heads (GQA 5..7), a short last head group (GQA 12), waves that
+    own fewer chunks than they hold or none (seq 200: one packed chunk for four waves; seq 70:
+    one packed chunk), the window chunks in the same launch (head groups of eight there), and
+    many splits; against the oracle and f64 dense attention on the dequantized cache."""
     dim = 128
     rng = np.random.default_rng(4200 + 10 * gqa + bits)
     k = rng.standard_normal(batch * heads * seq * dim).astype(np.float32)
