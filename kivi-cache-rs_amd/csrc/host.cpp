@@ -686,6 +686,27 @@ struct kivi_cache {
   CacheCore core;
   AttnSync attn;
   std::mutex mu;  // one mutating call at a time (the reference's &mut self)
+  // The stream of the latest device-pointer call on this cache, whose work may still run there
+  // (calls enqueued under stream capture are not counted). The host-pointer calls work on
+  // core.stream and return complete, as the reference's calls do: they first wait for that
+  // stream when it is another one (settle), so they never overlap its work; freeing the cache
+  // waits for it too.
+  std::mutex dev_mu;
+  hipStream_t dev_stream = nullptr;
+  bool dev_pending = false;
+  void note_device(hipStream_t s) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return;
+    std::lock_guard<std::mutex> lock(dev_mu);
+    dev_stream = s;
+    dev_pending = true;
+  }
+  Status settle() {
+    std::lock_guard<std::mutex> lock(dev_mu);
+    if (dev_pending && dev_stream != core.stream) HIP_TRY(hipStreamSynchronize(dev_stream), "device-call ordering");
+    dev_pending = false;
+    return Status{};
+  }
 };
 
 struct kivi_prefix_state {
@@ -1430,6 +1451,7 @@ kivi_status kivi_cache_new(const kivi_config* config, size_t batch, size_t num_k
 void kivi_cache_free(kivi_cache* cache) {
   if (cache == nullptr) return;
   DeviceScope scope(cache->core.device);
+  (void)cache->settle();
   (void)hipStreamSynchronize(cache->core.stream);
   (void)cache->attn.drain();
   delete cache;
@@ -1465,6 +1487,7 @@ kivi_status kivi_cache_append(kivi_cache* cache, const float* keys, size_t keys_
                               const float* values, size_t values_len, size_t seq_len,
                               kivi_error* err) {
   return guarded(err, [&] {
+    if (cache != nullptr) KIVI_TRY(cache->settle());
     return cache_append(cache, keys, keys_len, values, values_len, seq_len, false, nullptr);
   });
 }
@@ -1473,8 +1496,10 @@ kivi_status kivi_cache_append_device(kivi_cache* cache, const float* keys, size_
                                      const float* values, size_t values_len, size_t seq_len,
                                      void* stream, kivi_error* err) {
   return guarded(err, [&] {
-    return cache_append(cache, keys, keys_len, values, values_len, seq_len, true,
-                        static_cast<hipStream_t>(stream));
+    KIVI_TRY(cache_append(cache, keys, keys_len, values, values_len, seq_len, true,
+                          static_cast<hipStream_t>(stream)));
+    cache->note_device(static_cast<hipStream_t>(stream));
+    return Status{};
   });
 }
 
@@ -1482,6 +1507,7 @@ kivi_status kivi_cache_attention(const kivi_cache* cache, const float* query, si
                                  size_t num_q_heads, float scale, float* out, size_t out_len,
                                  kivi_error* err) {
   return guarded(err, [&] {
+    if (cache != nullptr) KIVI_TRY(const_cast<kivi_cache*>(cache)->settle());
     return cache_attention(cache, query, query_len, num_q_heads, scale, out, out_len, false, nullptr);
   });
 }
@@ -1491,8 +1517,10 @@ kivi_status kivi_cache_attention_device(const kivi_cache* cache, const float* qu
                                         float* out, size_t out_len, void* stream,
                                         kivi_error* err) {
   return guarded(err, [&] {
-    return cache_attention(cache, query, query_len, num_q_heads, scale, out, out_len, true,
-                           static_cast<hipStream_t>(stream));
+    KIVI_TRY(cache_attention(cache, query, query_len, num_q_heads, scale, out, out_len, true,
+                             static_cast<hipStream_t>(stream)));
+    const_cast<kivi_cache*>(cache)->note_device(static_cast<hipStream_t>(stream));
+    return Status{};
   });
 }
 
@@ -1501,20 +1529,27 @@ kivi_status kivi_cache_attention_device_noalloc(const kivi_cache* cache, const f
                                                 float* out, size_t out_len, void* stream,
                                                 kivi_error* err) {
   return guarded(err, [&] {
-    return cache_attention_noalloc(cache, query, query_len, num_q_heads, scale, out, out_len,
-                                   static_cast<hipStream_t>(stream));
+    KIVI_TRY(cache_attention_noalloc(cache, query, query_len, num_q_heads, scale, out, out_len,
+                                     static_cast<hipStream_t>(stream)));
+    const_cast<kivi_cache*>(cache)->note_device(static_cast<hipStream_t>(stream));
+    return Status{};
   });
 }
 
 kivi_status kivi_cache_dequantize(const kivi_cache* cache, float* keys, size_t keys_len,
                                   float* values, size_t values_len, kivi_error* err) {
-  return guarded(err, [&] { return cache_dequantize(cache, keys, keys_len, values, values_len, false, nullptr); });
+  return guarded(err, [&] {
+    if (cache != nullptr) KIVI_TRY(const_cast<kivi_cache*>(cache)->settle());
+    return cache_dequantize(cache, keys, keys_len, values, values_len, false, nullptr);
+  });
 }
 kivi_status kivi_cache_dequantize_device(const kivi_cache* cache, float* keys, size_t keys_len,
                                          float* values, size_t values_len, void* stream,
                                          kivi_error* err) {
   return guarded(err, [&] {
-    return cache_dequantize(cache, keys, keys_len, values, values_len, true, static_cast<hipStream_t>(stream));
+    KIVI_TRY(cache_dequantize(cache, keys, keys_len, values, values_len, true, static_cast<hipStream_t>(stream)));
+    const_cast<kivi_cache*>(cache)->note_device(static_cast<hipStream_t>(stream));
+    return Status{};
   });
 }
 
@@ -1526,6 +1561,7 @@ kivi_status kivi_cache_export_streams(const kivi_cache* cache, uint32_t* key_cod
                                       size_t value_codes_len, float* value_params,
                                       size_t value_params_len, kivi_error* err) {
   return guarded(err, [&] {
+    if (cache != nullptr) KIVI_TRY(const_cast<kivi_cache*>(cache)->settle());
     return cache_export(cache, key_codes, key_codes_len, key_params, key_params_len, value_codes,
                         value_codes_len, value_params, value_params_len, false, nullptr);
   });
@@ -1537,15 +1573,18 @@ kivi_status kivi_cache_export_streams_device(const kivi_cache* cache, uint32_t* 
                                              size_t value_params_len, void* stream,
                                              kivi_error* err) {
   return guarded(err, [&] {
-    return cache_export(cache, key_codes, key_codes_len, key_params, key_params_len, value_codes,
-                        value_codes_len, value_params, value_params_len, true,
-                        static_cast<hipStream_t>(stream));
+    KIVI_TRY(cache_export(cache, key_codes, key_codes_len, key_params, key_params_len, value_codes,
+                          value_codes_len, value_params, value_params_len, true,
+                          static_cast<hipStream_t>(stream)));
+    const_cast<kivi_cache*>(cache)->note_device(static_cast<hipStream_t>(stream));
+    return Status{};
   });
 }
 
 kivi_status kivi_cache_reserve(kivi_cache* cache, size_t tokens, kivi_error* err) {
   return guarded(err, [&] {
     KIVI_TRY(need(cache, "cache"));
+    KIVI_TRY(cache->settle());
     std::lock_guard<std::mutex> lock(cache->mu);
     DeviceScope scope(cache->core.device);
     KIVI_TRY(cache->core.ensure_capacity(tokens, cache->core.stream));
@@ -1584,6 +1623,7 @@ kivi_status kivi_cache_share_prefix(const kivi_cache* cache, kivi_prefix** out, 
   return guarded(err, [&] {
     KIVI_TRY(need(cache, "cache"));
     KIVI_TRY(need(out, "out"));
+    KIVI_TRY(const_cast<kivi_cache*>(cache)->settle());
     DeviceScope scope(cache->core.device);
     auto st = std::make_shared<kivi_prefix_state>();
     KIVI_TRY(cache->core.copy_into(st->core, cache->core.stream));
@@ -1735,6 +1775,7 @@ kivi_status kivi_runtime_new(const kivi_config* config, size_t batch, size_t num
 void kivi_runtime_free(kivi_runtime* rt) {
   if (rt == nullptr) return;
   DeviceScope scope(rt->cache.core.device);
+  (void)rt->cache.settle();
   (void)hipStreamSynchronize(rt->cache.core.stream);
   (void)rt->cache.attn.drain();
   delete rt;
@@ -1768,6 +1809,7 @@ kivi_status kivi_runtime_decode_device(kivi_runtime* rt, const float* key, size_
     return decode_fused(rt ? &rt->cache : nullptr, key, key_len, value, value_len, query, query_len,
                         num_q_heads, scale, out, out_len, static_cast<hipStream_t>(stream), &fused);
   });
+  if (fs == KIVI_OK && fused) rt->cache.note_device(static_cast<hipStream_t>(stream));
   if (fs != KIVI_OK || fused) return fs;
   kivi_status st = kivi_cache_append_device(rt ? &rt->cache : nullptr, key, key_len, value,
                                             value_len, 1, stream, err);
@@ -1820,6 +1862,7 @@ kivi_status kivi_guard_append(kivi_guard* guard, const float* keys, size_t keys_
                               size_t* num_checks, kivi_error* err) {
   return guarded(err, [&]() -> Status {
     KIVI_TRY(need(guard, "guard"));
+    KIVI_TRY(guard->cache->settle());
     const CacheCore& core0 = guard->cache->core;
     const size_t batch = core0.batch, heads = core0.heads, D = core0.head_dim;
     size_t expected, query_elems;

@@ -1,0 +1,82 @@
+"""Host-pointer calls on a cache right after a device-pointer append on another stream.
+
+The reference's calls are synchronous (src/cache.rs:186-279, src/prefix.rs:74-92): an append
+has finished before the next call reads the cache. Here `append_device` only enqueues its work
+on the caller's stream; a host-pointer call that follows on the cache's own stream must wait for
+that work (kivi.h), even when the caller's stream does not synchronize with the default stream
+(a non-blocking stream). Each case makes the host call at once, with no synchronization by the
+caller, and checks the result against the oracle's synchronous cache.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from kivi import KiviCache, KiviConfig
+from helpers import DeviceArrays
+from test_parity import assert_close, assert_same_state, assert_streams_equal
+
+pytestmark = pytest.mark.gpu
+
+HIP_STREAM_NON_BLOCKING = 1
+
+
+def non_blocking_stream(hip):
+    s = C.c_void_p()
+    assert hip.hipStreamCreateWithFlags(C.byref(s), HIP_STREAM_NON_BLOCKING) == 0
+    return s
+
+
+def prefill(rng, heads, seq, dim):
+    k = rng.standard_normal(heads * seq * dim).astype(np.float32)
+    v = rng.standard_normal(heads * seq * dim).astype(np.float32)
+    k.reshape(heads, seq, dim)[:, :, 3] *= 10
+    return k, v
+
+
+@pytest.mark.parametrize("bits", [2, 8])
+@pytest.mark.parametrize("then", ["export", "attention", "share_prefix", "reserve_then_append", "free"])
+def test_host_call_after_device_append_on_another_stream(amd, oracle, bits, then):
+    heads, dim, seq, qh = 8, 128, 16384, 32
+    cfg = KiviConfig(bits, 32, 128)
+    rng = np.random.default_rng(610 + bits)
+    k, v = prefill(rng, heads, seq, dim)
+    mem = DeviceArrays()
+    hip = mem._hip
+    s = non_blocking_stream(hip)
+    try:
+        dk, dv = mem.upload(k), mem.upload(v)
+        o = KiviCache(oracle, cfg, 1, heads, dim)
+        o.append(k, v, seq)
+        a = KiviCache(amd, cfg, 1, heads, dim)
+        a.append_device(dk, k.size, dv, v.size, seq, s.value)  # enqueued on s, not waited for
+        q = rng.standard_normal(qh * dim).astype(np.float32)
+        scale = np.float32(1 / np.sqrt(dim))
+        if then == "export":
+            assert_streams_equal(a, o)
+        elif then == "attention":
+            assert_close(a.attention(q, qh, scale), o.attention(q, qh, scale))
+        elif then == "share_prefix":
+            pa, po = a.share_prefix(), o.share_prefix()
+            del a
+            sa, so = pa.session(), po.session()
+            ks, vs = prefill(rng, heads, 40, dim)
+            sa.append(ks, vs, 40)
+            so.append(ks, vs, 40)
+            assert_close(sa.attention(q, qh, scale), so.attention(q, qh, scale))
+        elif then == "reserve_then_append":
+            # the reserve regrows the arenas (copying them) after the device append's work
+            a.reserve(seq + 5000)
+            k2, v2 = prefill(rng, heads, 300, dim)
+            a.append(k2, v2, 300)
+            o.append(k2, v2, 300)
+            assert_same_state(a, o)
+            assert_streams_equal(a, o)
+        else:
+            del a  # freeing waits for the append's work before the arenas go
+            assert hip.hipStreamSynchronize(s) == 0
+        assert hip.hipStreamSynchronize(s) == 0
+    finally:
+        hip.hipStreamSynchronize(s)
+        hip.hipStreamDestroy(s)
+        mem.free()
