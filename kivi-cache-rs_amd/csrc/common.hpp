@@ -97,7 +97,7 @@ struct CacheView {
   float* vparams;
   float* kres;   // [units][R][D]
   float* vring;  // [units][R][D]
-  // [units][kMaxSlots][kMaxStride]: running maxima of the key scales, the value scales, the
+  // [kMaxSlots][units][4]: running maxima of the key scales, the value scales, the
   // key |x| and the value |x| ever quantized into each unit (words kMaxKeyScale ..
   // kMaxValueAbs of a slot record; f32 bit patterns of values >= 0, so unsigned order is float
   // order). A writer raises the record its workgroup index selects (max_slot), a reader takes
@@ -106,25 +106,44 @@ struct CacheView {
   uint32_t* smax;
 };
 
-// The maxima records of a unit sit on their own 128-byte lines, so the atomics of one launch
-// spread over kMaxSlots lines per unit. With one record per unit, the records of eight units
-// shared one line and every quantize workgroup's atomics queued on it (batch 1 x 8 heads).
+// The maxima records: record s of every unit in region s ([kMaxSlots][units][4] words), so the
+// atomics of one launch spread over kMaxSlots regions: with one record per unit, the records of
+// eight units shared one 128-byte line and every quantize workgroup's atomics queued on it
+// (batch 1 x 8 heads). A reader takes the maximum over a unit's kMaxSlots records.
 constexpr uint32_t kMaxSlots = 8;
-constexpr uint32_t kMaxStride = 32;  // words per record
-constexpr uint32_t kMaxUnitWords = kMaxSlots * kMaxStride;
+constexpr uint32_t kMaxRecordWords = 4;  // key scale, value scale, key |x|, value |x|
+constexpr uint32_t kMaxUnitWords = kMaxSlots * kMaxRecordWords;
 constexpr uint32_t kMaxKeyScale = 0, kMaxValueScale = 1, kMaxKeyAbs = 2, kMaxValueAbs = 3;
 
 // Record `slot` (mod kMaxSlots) of a unit's maxima.
-__device__ __forceinline__ uint32_t* max_slot(uint32_t* smax, uint32_t unit, uint32_t slot) {
-  return smax + (uint64_t)unit * kMaxUnitWords + (slot % kMaxSlots) * kMaxStride;
+__device__ __forceinline__ uint32_t* max_slot(const CacheView& c, uint32_t unit, uint32_t slot) {
+  return c.smax + ((uint64_t)(slot % kMaxSlots) * c.geo.units + unit) * kMaxRecordWords;
+}
+
+// The largest key and value scale of a unit over its records (one pair of words per record,
+// both taken at once: the attention kernels need the value scale only after the logits, and a
+// second round of loads there would stand on a decode launch's critical path).
+__device__ __forceinline__ void unit_scale_max(const CacheView& c, uint32_t unit, float& kmax, float& vmax) {
+  const uint32_t* p = c.smax + (uint64_t)unit * kMaxRecordWords;
+  const uint64_t stride = (uint64_t)c.geo.units * kMaxRecordWords;
+  uint32_t km = 0, vm = 0;
+#pragma unroll
+  for (uint32_t s = 0; s < kMaxSlots; ++s) {
+    const uint2 w = *reinterpret_cast<const uint2*>(p + s * stride);
+    km = km > w.x ? km : w.x;
+    vm = vm > w.y ? vm : w.y;
+  }
+  kmax = __uint_as_float(km);
+  vmax = __uint_as_float(vm);
 }
 
 // Maximum `which` (kMaxKeyScale .. kMaxValueAbs) of a unit over its records.
-__device__ __forceinline__ float unit_max(const uint32_t* smax, uint32_t unit, uint32_t which) {
-  const uint32_t* p = smax + (uint64_t)unit * kMaxUnitWords + which;
+__device__ __forceinline__ float unit_max(const CacheView& c, uint32_t unit, uint32_t which) {
+  const uint32_t* p = c.smax + (uint64_t)unit * kMaxRecordWords + which;
+  const uint64_t stride = (uint64_t)c.geo.units * kMaxRecordWords;
   uint32_t m = p[0];
 #pragma unroll
-  for (uint32_t s = 1; s < kMaxSlots; ++s) m = m > p[s * kMaxStride] ? m : p[s * kMaxStride];
+  for (uint32_t s = 1; s < kMaxSlots; ++s) m = m > p[s * stride] ? m : p[s * stride];
   return __uint_as_float(m);
 }
 

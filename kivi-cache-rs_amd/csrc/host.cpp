@@ -695,15 +695,18 @@ struct kivi_cache {
   hipStream_t dev_stream = nullptr;
   bool dev_pending = false;
   void note_device(hipStream_t s) {
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(s, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return;
     std::lock_guard<std::mutex> lock(dev_mu);
     dev_stream = s;
     dev_pending = true;
   }
   Status settle() {
     std::lock_guard<std::mutex> lock(dev_mu);
-    if (dev_pending && dev_stream != core.stream) HIP_TRY(hipStreamSynchronize(dev_stream), "device-call ordering");
+    if (dev_pending && dev_stream != core.stream) {
+      // a stream still capturing holds no work yet (its graph runs where it is launched)
+      hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+      HIP_TRY(hipStreamIsCapturing(dev_stream, &cs), "device-call ordering");
+      if (cs == hipStreamCaptureStatusNone) HIP_TRY(hipStreamSynchronize(dev_stream), "device-call ordering");
+    }
     dev_pending = false;
     return Status{};
   }

@@ -948,7 +948,8 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
   // Power-of-two operand ranges: every key A operand |q * scale| * 2^ek and every value A
   // operand |w * scale| * 2^ev (w <= 1) stays below 2^15, from the unit's largest scales.
   qmax = warp_max(qmax);
-  const float kmax = unit_max(a.c.smax, unit, kMaxKeyScale);
+  float kmax, vmax_all;  // the unit's largest key and value scales
+  unit_scale_max(a.c, unit, kmax, vmax_all);
   constexpr float kLevels = static_cast<float>((1 << BITS) - 1);
   const int ek = std::min(60, std::max(-100, 15 - __builtin_amdgcn_frexp_expf(qmax * kmax)));
   constexpr int kExp = CodeUnit<BITS>::kExp;
@@ -1025,7 +1026,7 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
   // the value operands' range: the unit's largest value scale, raised by the evicted row's
   // quantization when a decode token is appended by this launch (as the append would have);
   // taken after the logits, so the evicted row's load is not waited for before them
-  float vmax = unit_max(a.c.smax, unit, kMaxValueScale);
+  float vmax = vmax_all;
   float ev_scale = 0.f, ev_amax = 0.f;  // the evicted row's largest scale and |x|
   if (D == 128 && a.pend_evict) {
     evict_groups(er, kLevels, ev_scale, ev_amax);
@@ -1097,8 +1098,8 @@ __device__ __forceinline__ void mfma_split(const AttnArgs& a, uint32_t unit, uin
           }
         }
         if (lane == 0) {
-          atomicMax(max_slot(a.c.smax, unit, 0) + kMaxValueScale, __float_as_uint(ev_scale));
-          atomicMax(max_slot(a.c.smax, unit, 0) + kMaxValueAbs, __float_as_uint(ev_amax));
+          atomicMax(max_slot(a.c, unit, 0) + kMaxValueScale, __float_as_uint(ev_scale));
+          atomicMax(max_slot(a.c, unit, 0) + kMaxValueAbs, __float_as_uint(ev_amax));
         }
       }
       }  // D == 128 (the decode is fused into the launch at head_dim 128 only)
@@ -1467,8 +1468,8 @@ __device__ __forceinline__ void wide_evict(const AttnArgs& a, uint32_t unit, con
         make_float2(sc, mn);
   }
   if (lane == 0) {
-    atomicMax(max_slot(a.c.smax, unit, 0) + kMaxValueScale, __float_as_uint(ev_scale));
-    atomicMax(max_slot(a.c.smax, unit, 0) + kMaxValueAbs, __float_as_uint(ev_amax));
+    atomicMax(max_slot(a.c, unit, 0) + kMaxValueScale, __float_as_uint(ev_scale));
+    atomicMax(max_slot(a.c, unit, 0) + kMaxValueAbs, __float_as_uint(ev_amax));
   }
 }
 
@@ -1533,7 +1534,8 @@ __device__ __forceinline__ void wide_split(const AttnArgs& a, uint32_t unit, uin
   }
   // power-of-two operand ranges from the unit's largest scales, as in the 4x4x4 path
   qmax = warp_max(qmax);
-  const float kmax = unit_max(a.c.smax, unit, kMaxKeyScale);
+  float kmax, vmax_all;  // the unit's largest key and value scales
+  unit_scale_max(a.c, unit, kmax, vmax_all);
   const int ek = std::min(60, std::max(-100, 15 - __builtin_amdgcn_frexp_expf(qmax * kmax)));
   const float kfac = ldexpf(1.f, ek);
   const float kout = ldexpf(1.f, -ek - kExp);
@@ -1605,7 +1607,7 @@ __device__ __forceinline__ void wide_split(const AttnArgs& a, uint32_t unit, uin
 
   // the value operands' range: the unit's largest value scale, raised by the evicted row's (as
   // the append would have raised it)
-  float vmax = unit_max(a.c.smax, unit, kMaxValueScale);
+  float vmax = vmax_all;
   float ev_scale = 0.f, ev_amax = 0.f;
   if constexpr (EVICT) {
     evict_groups(er, static_cast<float>((1 << BITS) - 1), ev_scale, ev_amax);
@@ -1820,7 +1822,8 @@ __device__ __forceinline__ void wide16_split(const AttnArgs& a, uint32_t unit, u
     for (int r = 0; r < 32; ++r) qmax = fmaxf(qmax, fabsf(qv[r]));
   }
   qmax = warp_max(qmax);
-  const float kmax = unit_max(a.c.smax, unit, kMaxKeyScale);
+  float kmax, vmax_all;  // the unit's largest key and value scales
+  unit_scale_max(a.c, unit, kmax, vmax_all);
   const int ek = std::min(60, std::max(-100, 15 - __builtin_amdgcn_frexp_expf(qmax * kmax)));
   const float kfac = ldexpf(1.f, ek);
   const float kout = ldexpf(1.f, -ek - kExp);
@@ -1892,7 +1895,7 @@ __device__ __forceinline__ void wide16_split(const AttnArgs& a, uint32_t unit, u
   mx = fmaxf(mx, __shfl_xor(mx, 32));
   const float mrow = mx * kout;
 
-  const float vmax = unit_max(a.c.smax, unit, kMaxValueScale);
+  const float vmax = vmax_all;
   const int ev = std::min(60, std::max(-100, 15 - __builtin_amdgcn_frexp_expf(vmax)));
   const float vout = ldexpf(1.f, -ev - kExp);
   const float moff = mrow == -INFINITY ? 0.f : mrow;
@@ -2906,8 +2909,8 @@ __device__ __forceinline__ void shared_split(const AttnArgs& a, uint32_t unit, u
     qhi[s] = __builtin_bit_cast(hx8, hi);
     qlo[s] = __builtin_bit_cast(hx8, lo);
   }
-  const int ek = range_exp(unit_max(a.c.smax, unit, kMaxKeyAbs));
-  const int ev = range_exp(unit_max(a.c.smax, unit, kMaxValueAbs));
+  const int ek = range_exp(unit_max(a.c, unit, kMaxKeyAbs));
+  const int ev = range_exp(unit_max(a.c, unit, kMaxValueAbs));
   const float kf = ldexpf(1.f, ek), vf = ldexpf(1.f, ev);
   const float s_unscale = ldexpf(1.f, -ek - eq);
   const float o_unscale = ldexpf(1.f, -ev) / kShPScale;  // O and l carry the P operand scale

@@ -244,8 +244,8 @@ __global__ void __launch_bounds__(256)
       am = fmaxf(am, __shfl_xor(am, o));
     }
     if (d % 64 == 0) {
-      atomicMax(max_slot(c.smax, unit, 0) + kMaxValueScale, __float_as_uint(sm));
-      atomicMax(max_slot(c.smax, unit, 0) + kMaxValueAbs, __float_as_uint(am));
+      atomicMax(max_slot(c, unit, 0) + kMaxValueScale, __float_as_uint(sm));
+      atomicMax(max_slot(c, unit, 0) + kMaxValueAbs, __float_as_uint(am));
     }
   }
   *slot = v;
@@ -265,7 +265,7 @@ __global__ void __launch_bounds__(kThreads)
     m = fmaxf(m, fabsf(base[(uint64_t)slot * D + d]));
   }
   for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-  if (threadIdx.x % 64 == 0) atomicMax(max_slot(c.smax, unit, 0) + kMaxKeyAbs + kind, __float_as_uint(m));
+  if (threadIdx.x % 64 == 0) atomicMax(max_slot(c, unit, 0) + kMaxKeyAbs + kind, __float_as_uint(m));
 }
 
 // Rows are staged through LDS as floats [rows][D+1] (the odd stride spreads a column over the
@@ -331,7 +331,7 @@ __global__ void __launch_bounds__(kThreads)
       codes_lds[t * D + d] = static_cast<uint8_t>(quant_code(x, zero, scale, levels));
     }
   }
-  raise_max(max_slot(c.smax, unit, blockIdx.x) + kMaxKeyScale, smax, amax);  // includes the barrier before the packing below
+  raise_max(max_slot(c, unit, blockIdx.x) + kMaxKeyScale, smax, amax);  // includes the barrier before the packing below
   const uint32_t ppw = geo.ppw();
   const uint32_t kw = geo.kwords_per_token();
   uint32_t* words = c.kcodes + unit * geo.kcodes_unit() + (g0 + g) * G * kw;
@@ -396,7 +396,7 @@ __global__ void __launch_bounds__(kThreads)
     }
     __syncthreads();  // the staging buffer is refilled by the next batch
   }
-  raise_max(max_slot(c.smax, unit, blockIdx.x) + kMaxValueScale, smax, amax);  // includes the barrier before the packing below
+  raise_max(max_slot(c, unit, blockIdx.x) + kMaxValueScale, smax, amax);  // includes the barrier before the packing below
   const uint32_t ppw = geo.ppw();
   const uint32_t vw = geo.vwords_per_channel();
   const uint32_t w_lo = static_cast<uint32_t>(t_lo % kValueBlock) / ppw;
@@ -529,7 +529,7 @@ __global__ void __launch_bounds__(kThreads)
 #pragma unroll
     for (int s2 = 0; s2 < (int)NS; ++s2) words[(s2 * LPW + m) * KW + lane / LPW] = keep[s2];
   }
-  raise_max(max_slot(c.smax, unit, blockIdx.x) + kMaxKeyScale, smax, amax);
+  raise_max(max_slot(c, unit, blockIdx.x) + kMaxKeyScale, smax, amax);
 }
 
 // Values: workgroup (unit, span) takes the unit's 64-token blocks span*kValueSpan .. +kValueSpan-1
@@ -680,7 +680,7 @@ __global__ void __launch_bounds__(kThreads)
       base[idx] = w0 < b_lo ? (v | base[idx]) : v;
     }
   }
-  raise_max(max_slot(c.smax, unit, blockIdx.x) + kMaxValueScale, smax, amax);
+  raise_max(max_slot(c, unit, blockIdx.x) + kMaxValueScale, smax, amax);
 }
 
 // ------------------------------------------------------------------ export to reference order

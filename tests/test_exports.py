@@ -129,12 +129,12 @@ def planned_bytes(bits, group, residual, batch, heads, dim, tokens):
     """Closed form of the arena layout: packed capacity C = max(tokens, 256) rounded up to
     lcm(64, G) tokens (0 with no tokens); per unit and token of capacity, key and value codes
     D*bits/8 bytes each, key params D/G*8, value params D/G*8; plus the fp32 key residual and
-    value window (R*D*4 each) and the scale maxima, eight 128-byte records per unit."""
+    value window (R*D*4 each) and the scale maxima, eight 16-byte records per unit."""
     units = batch * heads
     gran = 64 * group // math.gcd(64, group)
     cap = 0 if tokens == 0 else -(-max(tokens, 256) // gran) * gran
     per_token = 2 * dim * bits // 8 + 2 * (dim // group) * 8
-    return units * (cap * per_token + 2 * residual * dim * 4 + 8 * 128)
+    return units * (cap * per_token + 2 * residual * dim * 4 + 8 * 16)
 
 
 PLAN_CASES = [
