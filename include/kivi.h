@@ -27,9 +27,11 @@
  *    so that stream must still exist then (or the cache / session must be freed first).
  *    A host-pointer call on a cache (and kivi_cache_reserve, kivi_cache_share_prefix and
  *    freeing the cache) first waits for the stream of the latest `*_device` call on it when
- *    that is not the cache's own stream (kivi_cache_set_stream), so it never overlaps that
- *    work; that stream must still exist then too. Calls enqueued under stream capture are
- *    not counted. Between `*_device` calls on different streams the caller orders the work.
+ *    that is not the cache's own stream (kivi_cache_set_stream), and a host-pointer call on
+ *    a session for that of the latest `*_device` call on the session when it is not the
+ *    default stream, so it never overlaps that work; that stream must still exist then too.
+ *    Calls enqueued under stream capture are not counted. Between `*_device` calls on
+ *    different streams the caller orders the work.
  *  - Threading follows the reference's borrow rules: at most one mutating call
  *    (append, reserve, prefill, decode) in flight per cache; read-only calls
  *    (attention, dequantize, export, getters) may share a cache but must not overlap

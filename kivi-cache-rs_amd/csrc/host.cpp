@@ -682,34 +682,39 @@ using namespace kivi;
 
 // ---------------------------------------------------------------- opaque handles
 
+// The stream of the latest device-pointer call on a cache or session, whose work may still run
+// there. The host-pointer calls return complete, as the reference's calls do: before they
+// enqueue on their own stream they wait for that stream when it is another one (settle), so
+// they never overlap its work.
+struct DeviceCallOrder {
+  std::mutex mu;
+  hipStream_t stream = nullptr;
+  bool pending = false;
+  void note(hipStream_t s) {
+    std::lock_guard<std::mutex> lock(mu);
+    stream = s;
+    pending = true;
+  }
+  Status settle(hipStream_t own) {
+    std::lock_guard<std::mutex> lock(mu);
+    if (pending && stream != own) {
+      // a stream still capturing holds no work yet (its graph runs where it is launched)
+      hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+      HIP_TRY(hipStreamIsCapturing(stream, &cs), "device-call ordering");
+      if (cs == hipStreamCaptureStatusNone) HIP_TRY(hipStreamSynchronize(stream), "device-call ordering");
+    }
+    pending = false;
+    return Status{};
+  }
+};
+
 struct kivi_cache {
   CacheCore core;
   AttnSync attn;
   std::mutex mu;  // one mutating call at a time (the reference's &mut self)
-  // The stream of the latest device-pointer call on this cache, whose work may still run there
-  // (calls enqueued under stream capture are not counted). The host-pointer calls work on
-  // core.stream and return complete, as the reference's calls do: they first wait for that
-  // stream when it is another one (settle), so they never overlap its work; freeing the cache
-  // waits for it too.
-  std::mutex dev_mu;
-  hipStream_t dev_stream = nullptr;
-  bool dev_pending = false;
-  void note_device(hipStream_t s) {
-    std::lock_guard<std::mutex> lock(dev_mu);
-    dev_stream = s;
-    dev_pending = true;
-  }
-  Status settle() {
-    std::lock_guard<std::mutex> lock(dev_mu);
-    if (dev_pending && dev_stream != core.stream) {
-      // a stream still capturing holds no work yet (its graph runs where it is launched)
-      hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-      HIP_TRY(hipStreamIsCapturing(dev_stream, &cs), "device-call ordering");
-      if (cs == hipStreamCaptureStatusNone) HIP_TRY(hipStreamSynchronize(dev_stream), "device-call ordering");
-    }
-    dev_pending = false;
-    return Status{};
-  }
+  DeviceCallOrder dev;  // host-pointer calls work on core.stream; freeing waits too
+  void note_device(hipStream_t s) { dev.note(s); }
+  Status settle() { return dev.settle(core.stream); }
 };
 
 struct kivi_prefix_state {
@@ -728,6 +733,7 @@ struct kivi_session {
   AttnSync attn;
   DevBuf keys, values;            // [units][cap][D] fp32 suffix (the reference re-splices, src/prefix.rs:196-221)
   uint64_t len = 0, cap = 0;
+  DeviceCallOrder dev;            // host-pointer calls work on the default stream
 };
 
 struct kivi_runtime {
@@ -1723,6 +1729,7 @@ kivi_status kivi_session_append(kivi_session* session, const float* keys, size_t
                                 const float* values, size_t values_len, size_t seq_len,
                                 kivi_error* err) {
   return guarded(err, [&] {
+    if (session != nullptr) KIVI_TRY(session->dev.settle(nullptr));
     return session_append(session, keys, keys_len, values, values_len, seq_len, false, nullptr);
   });
 }
@@ -1731,8 +1738,10 @@ kivi_status kivi_session_append_device(kivi_session* session, const float* keys,
                                        size_t keys_len, const float* values, size_t values_len,
                                        size_t seq_len, void* stream, kivi_error* err) {
   return guarded(err, [&] {
-    return session_append(session, keys, keys_len, values, values_len, seq_len, true,
-                          static_cast<hipStream_t>(stream));
+    KIVI_TRY(session_append(session, keys, keys_len, values, values_len, seq_len, true,
+                            static_cast<hipStream_t>(stream)));
+    session->dev.note(static_cast<hipStream_t>(stream));
+    return Status{};
   });
 }
 
@@ -1740,6 +1749,7 @@ kivi_status kivi_session_attention(const kivi_session* session, const float* que
                                    size_t query_len, size_t num_q_heads, float scale, float* out,
                                    size_t out_len, kivi_error* err) {
   return guarded(err, [&] {
+    if (session != nullptr) KIVI_TRY(const_cast<kivi_session*>(session)->dev.settle(nullptr));
     return session_attend(session, query, query_len, num_q_heads, scale, out, out_len, false, nullptr);
   });
 }
@@ -1749,8 +1759,10 @@ kivi_status kivi_sessions_attention_device(const kivi_session* const* sessions, 
                                            size_t num_q_heads, float scale, float* out,
                                            size_t out_len, void* stream, kivi_error* err) {
   return guarded(err, [&] {
-    return batched_sessions(sessions, n, queries, queries_len, num_q_heads, scale, out, out_len,
-                            true, static_cast<hipStream_t>(stream));
+    KIVI_TRY(batched_sessions(sessions, n, queries, queries_len, num_q_heads, scale, out, out_len,
+                              true, static_cast<hipStream_t>(stream)));
+    for (size_t i = 0; i < n; ++i) const_cast<kivi_session*>(sessions[i])->dev.note(static_cast<hipStream_t>(stream));
+    return Status{};
   });
 }
 
@@ -1759,6 +1771,9 @@ kivi_status kivi_sessions_attention(const kivi_session* const* sessions, size_t 
                                     size_t num_q_heads, float scale, float* out, size_t out_len,
                                     kivi_error* err) {
   return guarded(err, [&] {
+    if (sessions != nullptr)
+      for (size_t i = 0; i < n; ++i)
+        if (sessions[i] != nullptr) KIVI_TRY(const_cast<kivi_session*>(sessions[i])->dev.settle(nullptr));
     return batched_sessions(sessions, n, queries, queries_len, num_q_heads, scale, out, out_len,
                             false, nullptr);
   });

@@ -1,4 +1,5 @@
-"""Host-pointer calls on a cache right after a device-pointer append on another stream.
+"""Host-pointer calls on a cache or session right after a device-pointer append on another
+stream.
 
 The reference's calls are synchronous (src/cache.rs:186-279, src/prefix.rs:74-92): an append
 has finished before the next call reads the cache. Here `append_device` only enqueues its work
@@ -12,6 +13,7 @@ import ctypes as C
 import numpy as np
 import pytest
 
+import kivi
 from kivi import KiviCache, KiviConfig
 from helpers import DeviceArrays
 from test_parity import assert_close, assert_same_state, assert_streams_equal
@@ -32,6 +34,41 @@ def prefill(rng, heads, seq, dim):
     v = rng.standard_normal(heads * seq * dim).astype(np.float32)
     k.reshape(heads, seq, dim)[:, :, 3] *= 10
     return k, v
+
+
+def test_session_host_attention_after_device_append_on_another_stream(amd, oracle):
+    """RagSession::append on device pointers (enqueued on a non-blocking stream) then the
+    session's host-pointer attention and the batched host call, with no synchronization by the
+    caller (src/prefix.rs:173-289)."""
+    heads, dim, seq, qh, suffix = 8, 128, 4096, 32, 3000
+    cfg = KiviConfig(2, 32, 128)
+    rng = np.random.default_rng(620)
+    k, v = prefill(rng, heads, seq, dim)
+    a, o = KiviCache(amd, cfg, 1, heads, dim), KiviCache(oracle, cfg, 1, heads, dim)
+    a.append(k, v, seq)
+    o.append(k, v, seq)
+    pa, po = a.share_prefix(), o.share_prefix()
+    mem = DeviceArrays()
+    hip = mem._hip
+    s = non_blocking_stream(hip)
+    try:
+        ks, vs = prefill(rng, heads, suffix, dim)
+        dk, dv = mem.upload(ks), mem.upload(vs)
+        q = rng.standard_normal(qh * dim).astype(np.float32)
+        scale = np.float32(1 / np.sqrt(dim))
+        sa, so = pa.session(), po.session()
+        so.append(ks, vs, suffix)
+        sa.append_device(dk, ks.size, dv, vs.size, suffix, s.value)  # enqueued on s, not waited for
+        assert_close(sa.attention(q, qh, scale), so.attention(q, qh, scale))
+        sb = pa.session()
+        sb.append_device(dk, ks.size, dv, vs.size, suffix, s.value)
+        got = kivi.sessions_attention(amd, [sb], q, qh, scale)
+        assert_close(got, so.attention(q, qh, scale))
+        assert hip.hipStreamSynchronize(s) == 0
+    finally:
+        hip.hipStreamSynchronize(s)
+        hip.hipStreamDestroy(s)
+        mem.free()
 
 
 @pytest.mark.parametrize("bits", [2, 8])
