@@ -145,7 +145,9 @@ kivi_status kivi_cache_new(const kivi_config* config, size_t batch, size_t num_k
 void kivi_cache_free(kivi_cache* cache);
 
 /* Stream used by the host-pointer entry points and by internal copies
- * (hipStream_t as void*; NULL = the default stream). */
+ * (hipStream_t as void*; NULL = the default stream). Switching waits for the work enqueued
+ * on the previous stream (and for the latest `*_device` call's stream) first, so the
+ * previous stream must still exist then. */
 kivi_status kivi_cache_set_stream(kivi_cache* cache, void* stream, kivi_error* err);
 
 /* Getters (src/cache.rs:122-156, 328-337). */

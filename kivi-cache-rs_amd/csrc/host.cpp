@@ -1469,7 +1469,18 @@ void kivi_cache_free(kivi_cache* cache) {
 kivi_status kivi_cache_set_stream(kivi_cache* cache, void* stream, kivi_error* err) {
   return guarded(err, [&] {
     KIVI_TRY(need(cache, "cache"));
-    cache->core.stream = static_cast<hipStream_t>(stream);
+    KIVI_TRY(cache->settle());
+    std::lock_guard<std::mutex> lock(cache->mu);
+    const hipStream_t next = static_cast<hipStream_t>(stream);
+    if (next != cache->core.stream) {
+      // `*_device` calls made on the previous stream are not recorded as pending (host-pointer
+      // calls on it follow them in stream order): they end before the new stream is used
+      DeviceScope scope(cache->core.device);
+      hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+      HIP_TRY(hipStreamIsCapturing(cache->core.stream, &cs), "set stream");
+      if (cs == hipStreamCaptureStatusNone) HIP_TRY(hipStreamSynchronize(cache->core.stream), "set stream");
+    }
+    cache->core.stream = next;
     return Status{};
   });
 }

@@ -71,6 +71,38 @@ def test_session_host_attention_after_device_append_on_another_stream(amd, oracl
         mem.free()
 
 
+def test_set_stream_waits_for_device_work_on_the_previous_stream(amd, oracle):
+    """A device-pointer append on the cache's own stream (kivi_cache_set_stream) is ordered
+    before later host-pointer calls by that stream alone. Switching the cache to another stream
+    right after it must wait for it, so a host-pointer call on the new stream sees the tokens."""
+    heads, dim, seq, qh = 8, 128, 16384, 32
+    cfg = KiviConfig(2, 32, 128)
+    rng = np.random.default_rng(640)
+    k, v = prefill(rng, heads, seq, dim)
+    mem = DeviceArrays()
+    hip = mem._hip
+    s1, s2 = non_blocking_stream(hip), non_blocking_stream(hip)
+    try:
+        o = KiviCache(oracle, cfg, 1, heads, dim)
+        o.append(k, v, seq)
+        a = KiviCache(amd, cfg, 1, heads, dim)
+        a.set_stream(s1.value)
+        dk, dv = mem.upload(k), mem.upload(v)
+        a.append_device(dk, k.size, dv, v.size, seq, s1.value)  # on the cache's own stream
+        a.set_stream(s2.value)
+        q = rng.standard_normal(qh * dim).astype(np.float32)
+        scale = np.float32(1 / np.sqrt(dim))
+        assert_close(a.attention(q, qh, scale), o.attention(q, qh, scale))
+        assert_streams_equal(a, o)
+        a.set_stream(0)
+        del a
+    finally:
+        for s in (s1, s2):
+            hip.hipStreamSynchronize(s)
+            hip.hipStreamDestroy(s)
+        mem.free()
+
+
 @pytest.mark.parametrize("bits", [2, 8])
 @pytest.mark.parametrize("then", ["export", "attention", "share_prefix", "reserve_then_append", "free"])
 def test_host_call_after_device_append_on_another_stream(amd, oracle, bits, then):
