@@ -2362,10 +2362,23 @@ __global__ void __launch_bounds__(kMergeThreads)
 #pragma unroll
   for (int i = 0; i < CPL; ++i) acc[i] = 0.f;
   uint32_t sess = 0, unit = 0, h = 0;
+  // a decode token's rows (one wave per unit writes them at the end): requested first, so
+  // their round trip overlaps the partials' loads
+  float pk[CPL], pv[CPL];
+  bool pend_rows = false;
   if (live) {
     sess = row / (units * gq);
     unit = (row / gq) % units;
     h = row % gq;
+    pend_rows = pend.k != nullptr && sess == 0 && h == 0 && part == 0;
+    if (pend_rows) {
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) {
+        const uint32_t d = lane + 64 * i;
+        pk[i] = d < D ? pend.k[(uint64_t)unit * D + d] : 0.f;
+        pv[i] = d < D ? pend.v[(uint64_t)unit * D + d] : 0.f;
+      }
+    }
     const uint64_t stride = (uint64_t)gq * (D + 2);
     const float* base = ws + sess * ws_sess_stride + (uint64_t)unit * nsplit * stride + h * (D + 2);
     for (uint32_t s0 = part; s0 < nsplit; s0 += parts * SB) {
@@ -2432,10 +2445,14 @@ __global__ void __launch_bounds__(kMergeThreads)
     const uint32_t c = lane + 64 * i;
     if (c < D) o[c] = acc[i] / lp;
   }
-  if (pend.k != nullptr && sess == 0 && h == 0) {
-    for (uint32_t d = lane; d < D; d += 64) {
-      pend.kres[((uint64_t)unit * pend.R + pend.kslot) * D + d] = pend.k[(uint64_t)unit * D + d];
-      pend.vring[((uint64_t)unit * pend.R + pend.vslot) * D + d] = pend.v[(uint64_t)unit * D + d];
+  if (pend_rows) {
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const uint32_t d = lane + 64 * i;
+      if (d < D) {
+        pend.kres[((uint64_t)unit * pend.R + pend.kslot) * D + d] = pk[i];
+        pend.vring[((uint64_t)unit * pend.R + pend.vslot) * D + d] = pv[i];
+      }
     }
   }
 }
