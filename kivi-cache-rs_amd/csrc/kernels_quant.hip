@@ -685,19 +685,52 @@ __global__ void __launch_bounds__(kThreads)
 
 // ------------------------------------------------------------------ export to reference order
 
+// Swap mask of a block-transpose round: the low s-element half of every 2s-element run of a
+// word of 32/bits elements.
+constexpr uint32_t swap_mask(uint32_t bits, uint32_t s) {
+  uint32_t m = 0;
+  for (uint32_t e = 0; e < 32 / bits; ++e)
+    if ((e / s) % 2 == 0) m |= ((1u << bits) - 1u) << (bits * e);
+  return m;
+}
+
+// Transpose of a PPW x PPW block of codes held in PPW native words: word t holds row t, its
+// element i at bit code_shift(BITS, i). Afterwards word code_shift(BITS, i) / BITS holds
+// column i with row t at bit BITS*t, the reference's order (first element in the low bits).
+// log2(PPW) rounds: in the round of half-size s, the upper s-element half of each 2s-element
+// run of row t (t & s == 0) trades places with the lower half of row t + s. A native word's
+// elements sit at a permutation of the element slots, so the rounds move whole columns and
+// only the output word that receives each column changes.
+template <int BITS>
+__device__ __forceinline__ void transpose_codes(uint32_t (&w)[32 / BITS]) {
+  constexpr int N = 32 / BITS;
+#pragma unroll
+  for (int s = N / 2; s >= 1; s /= 2) {
+    const uint32_t m = swap_mask(BITS, s);
+#pragma unroll
+    for (int t = 0; t < N; ++t) {
+      if (t & s) continue;
+      const uint32_t x = ((w[t] >> (BITS * s)) ^ w[t + s]) & m;
+      w[t + s] ^= x;
+      w[t] ^= x << (BITS * s);
+    }
+  }
+}
+
 // Key words (g*D + d)*ipc + w hold tokens g*G + w*ppw + i of channel d (src/quant.rs:312-323).
-// Grid (group slices, units): a workgroup stages its `per` groups' words in LDS at once
-// (coalesced reads, one barrier), then writes their channel-major words (coalesced writes);
-// the ppw codes of an output word are gathered with the shifts unrolled.
+// Grid (group slices, units): a workgroup stages its `per` groups' native words in LDS
+// (coalesced reads, one barrier); each thread then transposes one ppw x ppw block (ppw tokens
+// of one native word of channels) in registers and puts its ppw output words in a second LDS
+// buffer (`stage_out`; else straight to memory), which is written out with coalesced stores.
 constexpr uint32_t kExportGroups = 8;        // groups per workgroup, at most
 constexpr uint32_t kExportLdsWords = 16384;  // staging words per workgroup, at most (64 KB)
 template <int BITS>
 __global__ void __launch_bounds__(kThreads)
-    k_export_keys(CacheView c, uint64_t kq, uint32_t per, uint32_t* out) {
-  constexpr uint32_t PPW = 32 / BITS, MASK = (1u << BITS) - 1u;
+    k_export_keys(CacheView c, uint64_t kq, uint32_t per, uint32_t stage_out, uint32_t* out) {
+  constexpr uint32_t PPW = 32 / BITS;
   // [per][kw][G + 4]: native word (token t, channel word k) at k * (G + 4) + t, so that the
-  // PPW tokens of an output word are 16-byte reads (rows 16-byte aligned, 4 words apart in
-  // banks between rows)
+  // PPW tokens of a block are 16-byte reads (rows 16-byte aligned, 4 banks apart); then
+  // [per][n] output words when staged
   extern __shared__ uint32_t words[];
   const Geometry& geo = c.geo;
   const uint32_t G = geo.G, kw = geo.kwords_per_token(), row = G + 4;
@@ -705,6 +738,7 @@ __global__ void __launch_bounds__(kThreads)
   const uint64_t ngroups = kq / G;
   const uint64_t g0 = (uint64_t)blockIdx.x * per;
   const uint32_t ng = static_cast<uint32_t>(std::min<uint64_t>(per, ngroups - g0));
+  uint32_t* staged = words + per * np;
   for (uint32_t unit = blockIdx.y; unit < geo.units; unit += gridDim.y) {
     const uint32_t* src = c.kcodes + unit * geo.kcodes_unit() + g0 * n;
     uint32_t* dst = out + (uint64_t)unit * ngroups * n + g0 * n;
@@ -713,60 +747,93 @@ __global__ void __launch_bounds__(kThreads)
       words[gg * np + (r % kw) * row + r / kw] = src[i];
     }
     __syncthreads();
-    for (uint32_t o = threadIdx.x; o < ng * n; o += blockDim.x) {
-      const uint32_t gg = o / n, r = o % n, w = r % ipc, d = r / ipc;
-      const uint32_t sh = code_shift(BITS, d % PPW);
-      const uint4* tw = reinterpret_cast<const uint4*>(words + gg * np + (d / PPW) * row + w * PPW);
-      uint32_t word = 0;
+    // block (group gg, channel word k, token run tb): channels k*PPW + i, tokens tb*PPW + t
+    for (uint32_t task = threadIdx.x; task < ng * kw * ipc; task += blockDim.x) {
+      const uint32_t gg = task / (kw * ipc), r = task % (kw * ipc), k = r / ipc, tb = r % ipc;
+      const uint4* tw = reinterpret_cast<const uint4*>(words + gg * np + k * row + tb * PPW);
+      uint32_t w[PPW];
 #pragma unroll
       for (uint32_t q = 0; q < PPW / 4; ++q) {
         const uint4 x = tw[q];
-        const uint32_t xs[4] = {x.x, x.y, x.z, x.w};
-#pragma unroll
-        for (uint32_t e = 0; e < 4; ++e) word |= ((xs[e] >> sh) & MASK) << (BITS * (4 * q + e));
+        w[4 * q] = x.x;
+        w[4 * q + 1] = x.y;
+        w[4 * q + 2] = x.z;
+        w[4 * q + 3] = x.w;
       }
-      dst[o] = word;
+      transpose_codes<BITS>(w);
+#pragma unroll
+      for (uint32_t i = 0; i < PPW; ++i) {
+        const uint32_t o = gg * n + (k * PPW + i) * ipc + tb;
+        const uint32_t v = w[code_shift(BITS, i) / BITS];
+        if (stage_out) staged[o] = v;
+        else dst[o] = v;
+      }
     }
-    __syncthreads();  // the staging buffer is refilled for the next unit
+    if (stage_out) {
+      __syncthreads();
+      for (uint32_t i = threadIdx.x; i < ng * n; i += blockDim.x) dst[i] = staged[i];
+    }
+    __syncthreads();  // the staging buffers are refilled for the next unit
   }
 }
 
 // Value words (t*(D/G) + cg)*ipg + w = t*(D/ppw) + j hold channels j*ppw + i of token t
 // (src/quant.rs:362-372); params (t*(D/G) + cg)*2 (src/quant.rs:360-361). Grid (block slices,
-// units): a workgroup stages its `per` 64-token blocks' channel-major words in LDS at once and
-// writes their token-major words and (scale, zero) pairs.
+// units): a workgroup stages its `per` 64-token blocks' native words in LDS; each thread
+// transposes one ppw x ppw block (ppw channels of one native word of tokens) in registers into
+// ppw output words, staged for coalesced stores as the key export does, and the (scale, zero)
+// pairs are copied in token order.
 constexpr uint32_t kExportBlocks = 4;  // 64-token blocks per workgroup, at most
 template <int BITS>
 __global__ void __launch_bounds__(kThreads)
-    k_export_values(CacheView c, uint64_t vq, uint32_t per, uint32_t* out_codes, float* out_params) {
-  constexpr uint32_t PPW = 32 / BITS, MASK = (1u << BITS) - 1u, VW = kValueBlock / PPW;
-  // [per][D * VW + D / PPW]: native word (channel c, w) at c * VW + w + c / PPW, so that the
-  // lanes gathering one output word each (channel runs PPW apart) hit distinct banks
+    k_export_values(CacheView c, uint64_t vq, uint32_t per, uint32_t stage_out, uint32_t* out_codes,
+                    float* out_params) {
+  constexpr uint32_t PPW = 32 / BITS, VW = kValueBlock / PPW;
+  // [per][VW][D + 4]: native word (channel c, word w) at w * (D + 4) + c, so that the PPW
+  // channels of a block are 16-byte reads; then [per][64][D / PPW] output words when staged
   extern __shared__ uint32_t words[];
   const Geometry& geo = c.geo;
-  const uint32_t D = geo.D, ncg = geo.ncg(), wpt = D / PPW, n = D * VW, np = n + D / PPW;
+  const uint32_t D = geo.D, ncg = geo.ncg(), wpt = D / PPW, n = D * VW, row = D + 4, np = VW * row;
   const uint64_t nblk = (vq + kValueBlock - 1) / kValueBlock;
   const uint64_t b0 = (uint64_t)blockIdx.x * per;
   const uint32_t nb = static_cast<uint32_t>(std::min<uint64_t>(per, nblk - b0));
   // tokens of this workgroup's blocks (the last block of the stream may be partial)
   const uint32_t ntok = static_cast<uint32_t>(std::min<uint64_t>((uint64_t)nb * kValueBlock, vq - b0 * kValueBlock));
+  uint32_t* staged = words + per * np;
   for (uint32_t unit = blockIdx.y; unit < geo.units; unit += gridDim.y) {
     const uint32_t* src = c.vcodes + unit * geo.vcodes_unit() + b0 * n;
     const float2* prm = reinterpret_cast<const float2*>(c.vparams + unit * geo.vparams_unit()) + b0 * ncg * kValueBlock;
     uint32_t* dst = out_codes + (uint64_t)unit * vq * wpt + b0 * kValueBlock * wpt;
     for (uint32_t i = threadIdx.x; i < nb * n; i += blockDim.x) {
-      const uint32_t bb = i / n, r = i % n;
-      words[bb * np + r + r / (PPW * VW)] = src[i];
+      const uint32_t bb = i / n, r = i % n;  // r = channel * VW + word
+      words[bb * np + (r % VW) * row + r / VW] = src[i];
     }
     __syncthreads();
-    for (uint32_t o = threadIdx.x; o < ntok * wpt; o += blockDim.x) {
-      const uint32_t tk = o / wpt, j = o % wpt, bb = tk / kValueBlock, tt = tk % kValueBlock;
-      const uint32_t sh = code_shift(BITS, tt % PPW);
-      const uint32_t* cw = words + bb * np + (j * PPW) * VW + j + tt / PPW;
-      uint32_t word = 0;
+    // block (block bb, channel run j, word w): channels j*PPW + t, tokens w*PPW + i
+    for (uint32_t task = threadIdx.x; task < nb * wpt * VW; task += blockDim.x) {
+      const uint32_t bb = task / (wpt * VW), r = task % (wpt * VW), j = r / VW, wd = r % VW;
+      const uint4* tw = reinterpret_cast<const uint4*>(words + bb * np + wd * row + j * PPW);
+      uint32_t w[PPW];
 #pragma unroll
-      for (uint32_t i = 0; i < PPW; ++i) word |= ((cw[i * VW] >> sh) & MASK) << (BITS * i);
-      dst[o] = word;
+      for (uint32_t q = 0; q < PPW / 4; ++q) {
+        const uint4 x = tw[q];
+        w[4 * q] = x.x;
+        w[4 * q + 1] = x.y;
+        w[4 * q + 2] = x.z;
+        w[4 * q + 3] = x.w;
+      }
+      transpose_codes<BITS>(w);
+#pragma unroll
+      for (uint32_t i = 0; i < PPW; ++i) {
+        const uint32_t tk = bb * kValueBlock + wd * PPW + i;  // token within the workgroup's blocks
+        const uint32_t v = w[code_shift(BITS, i) / BITS];
+        if (stage_out) staged[tk * wpt + j] = v;
+        else if (tk < ntok) dst[tk * wpt + j] = v;
+      }
+    }
+    if (stage_out) {
+      __syncthreads();
+      for (uint32_t o = threadIdx.x; o < ntok * wpt; o += blockDim.x) dst[o] = staged[o];
     }
     if (out_params != nullptr) {
       float2* dpar = reinterpret_cast<float2*>(out_params) + ((uint64_t)unit * vq + b0 * kValueBlock) * ncg;
@@ -775,7 +842,7 @@ __global__ void __launch_bounds__(kThreads)
         dpar[o] = prm[((uint64_t)bb * ncg + cg) * kValueBlock + tt];
       }
     }
-    __syncthreads();  // the staging buffer is refilled for the next unit
+    __syncthreads();  // the staging buffers are refilled for the next unit
   }
 }
 
@@ -1330,11 +1397,14 @@ hipError_t launch_export_keys(const CacheView& c, uint64_t kq, uint32_t* codes, 
   const Geometry& g = c.geo;
   if (kq == 0) return hipSuccess;
   if (codes != nullptr) {
-    // staged words per group: kw rows of G + 4 tokens
-    const uint32_t np = g.kwords_per_token() * (g.G + 4);
-    const uint32_t per = std::max(1u, std::min(kExportGroups, kExportLdsWords / np));
+    // staged words per group: kw rows of G + 4 tokens, then the n output words when both
+    // fit the budget (else the output words go straight to memory)
+    const uint32_t np = g.kwords_per_token() * (g.G + 4), n = g.G * g.kwords_per_token();
+    const uint32_t stage_out = np + n <= kExportLdsWords ? 1u : 0u;
+    const uint32_t per_group = np + (stage_out ? n : 0u);
+    const uint32_t per = std::max(1u, std::min(kExportGroups, kExportLdsWords / per_group));
     const uint64_t slices = (kq / g.G + per - 1) / per;
-    const size_t lds = (size_t)per * np * sizeof(uint32_t);
+    const size_t lds = (size_t)per * per_group * sizeof(uint32_t);
     const dim3 grid(static_cast<unsigned>(std::min<uint64_t>(slices, 1u << 30)), std::min(g.units, 65535u));
     hipError_t e = hipSuccess;
     if (lds > 65536) {
@@ -1344,9 +1414,9 @@ hipError_t launch_export_keys(const CacheView& c, uint64_t kq, uint32_t* codes, 
       e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
       if (e != hipSuccess) return e;
     }
-    if (g.bits == 2) k_export_keys<2><<<grid, kThreads, lds, stream>>>(c, kq, per, codes);
-    else if (g.bits == 4) k_export_keys<4><<<grid, kThreads, lds, stream>>>(c, kq, per, codes);
-    else k_export_keys<8><<<grid, kThreads, lds, stream>>>(c, kq, per, codes);
+    if (g.bits == 2) k_export_keys<2><<<grid, kThreads, lds, stream>>>(c, kq, per, stage_out, codes);
+    else if (g.bits == 4) k_export_keys<4><<<grid, kThreads, lds, stream>>>(c, kq, per, stage_out, codes);
+    else k_export_keys<8><<<grid, kThreads, lds, stream>>>(c, kq, per, stage_out, codes);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
@@ -1370,23 +1440,26 @@ hipError_t launch_export_values(const CacheView& c, uint64_t vq, uint32_t* codes
     codes = tmp;
   }
   const uint64_t nblk = (vq + kValueBlock - 1) / kValueBlock;
-  // staged words per block, padded by one word per run of ppw channels; a block of the widest
-  // heads (D = 1024, 8-bit) stages 16640 words (65 KB)
-  const uint32_t np = g.D * g.vwords_per_channel() + g.D / g.ppw();
-  const uint32_t per = std::max(1u, std::min(kExportBlocks, kExportLdsWords / np));
+  // staged words per block: VW rows of D + 4 channels (a block of the widest heads, D = 1024
+  // at 8 bits, stages 16448 words: 64.3 KB), then the output words when both fit the budget
+  const uint32_t vw = g.vwords_per_channel();
+  const uint32_t np = vw * (g.D + 4), n = g.D * vw;
+  const uint32_t stage_out = np + n <= kExportLdsWords ? 1u : 0u;
+  const uint32_t per_block = np + (stage_out ? n : 0u);
+  const uint32_t per = std::max(1u, std::min(kExportBlocks, kExportLdsWords / per_block));
   const uint64_t slices = (nblk + per - 1) / per;
-  const size_t lds = (size_t)per * np * sizeof(uint32_t);
+  const size_t lds = (size_t)per * per_block * sizeof(uint32_t);
   const dim3 grid(static_cast<unsigned>(std::min<uint64_t>(slices, 1u << 30)), std::min(g.units, 65535u));
   hipError_t e = hipSuccess;
-  if (g.bits == 2) {
-    k_export_values<2><<<grid, kThreads, lds, stream>>>(c, vq, per, codes, params);
-  } else if (g.bits == 4) {
-    k_export_values<4><<<grid, kThreads, lds, stream>>>(c, vq, per, codes, params);
-  } else {
-    if (lds > 65536)
-      e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_export_values<8>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-    if (e == hipSuccess) k_export_values<8><<<grid, kThreads, lds, stream>>>(c, vq, per, codes, params);
+  const void* f = g.bits == 2 ? reinterpret_cast<const void*>(&k_export_values<2>)
+                  : g.bits == 4 ? reinterpret_cast<const void*>(&k_export_values<4>)
+                                : reinterpret_cast<const void*>(&k_export_values<8>);
+  if (lds > 65536)
+    e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+  if (e == hipSuccess) {
+    if (g.bits == 2) k_export_values<2><<<grid, kThreads, lds, stream>>>(c, vq, per, stage_out, codes, params);
+    else if (g.bits == 4) k_export_values<4><<<grid, kThreads, lds, stream>>>(c, vq, per, stage_out, codes, params);
+    else k_export_values<8><<<grid, kThreads, lds, stream>>>(c, vq, per, stage_out, codes, params);
   }
   if (e == hipSuccess) e = hipGetLastError();
   if (tmp != nullptr) {
