@@ -850,18 +850,39 @@ __global__ void __launch_bounds__(kThreads)
 
 // KiviCache::dequantize (src/cache.rs:282-325): packed tokens as fma(code, scale, zero)
 // (src/quant.rs:406, 443), residual tokens copied. A workgroup takes one 64-token block of a
-// unit at a time: the block's value words are staged in LDS as [word][channel] (so the four
-// channels of a float4 are one 16-byte read) with their (scale, zero) pairs, and a thread
-// writes float4 runs of consecutive channels (D % 4 == 0) of keys and values.
+// unit at a time and stages everything the block's packed tokens read in LDS with coalesced
+// loads: the value words as [word][channel] rows padded by 4 words (the four channels of a
+// float4 are one 16-byte read, and the transposing writes spread over the banks), the value
+// (scale, zero) pairs, the key words as stored and the (scale, zero) pairs of the key groups
+// the block touches. A thread then writes float4 runs of consecutive channels (D % 4 == 0) of
+// keys and values from LDS only.
+struct DequantLds {
+  uint32_t vrow, vwords, vparams, kwords, kgroups, kparams, total;  // offsets and sizes in words
+};
+__host__ __device__ inline DequantLds dequant_lds(const Geometry& g) {
+  DequantLds l;
+  l.vrow = g.D + 4;
+  l.vwords = 0;
+  l.vparams = g.vwords_per_channel() * l.vrow;
+  l.kwords = l.vparams + 2 * g.ncg() * kValueBlock;
+  l.kgroups = (kValueBlock + g.G - 1) / g.G + 1;  // groups a run of 64 tokens can touch
+  l.kparams = l.kwords + kValueBlock * g.kwords_per_token();
+  l.total = l.kparams + 2 * l.kgroups * g.D;
+  return l;
+}
 __global__ void __launch_bounds__(kThreads)
     k_dequant_cache(CacheView c, SeqState s, uint64_t seq, float* keys, float* values) {
-  extern __shared__ uint32_t stage[];  // [vw][D] words, then [ncg][64] (scale, zero)
+  extern __shared__ uint32_t stage[];
   const Geometry& geo = c.geo;
+  const DequantLds L = dequant_lds(geo);
   const uint32_t D = geo.D, G = geo.G, R = geo.R, bits = geo.bits, ppw = geo.ppw();
   const uint32_t kw = geo.kwords_per_token(), vw = geo.vwords_per_channel(), ncg = geo.ncg();
   const uint32_t mask = geo.levels();
   const uint32_t q4 = D / 4;
-  float2* sprm = reinterpret_cast<float2*>(stage + vw * D);
+  uint32_t* svw = stage + L.vwords;
+  float2* svp = reinterpret_cast<float2*>(stage + L.vparams);
+  uint32_t* skw = stage + L.kwords;
+  float2* skp = reinterpret_cast<float2*>(stage + L.kparams);
   const uint64_t nblk = (seq + kValueBlock - 1) / kValueBlock;
   const uint64_t total = nblk * geo.units;
   for (uint64_t job = blockIdx.x; job < total; job += gridDim.x) {
@@ -869,25 +890,32 @@ __global__ void __launch_bounds__(kThreads)
     const uint64_t tb = job % nblk;
     const uint64_t t0 = tb * kValueBlock;
     const uint32_t ntok = static_cast<uint32_t>(std::min<uint64_t>(kValueBlock, seq - t0));
-    const uint32_t* kc = c.kcodes + unit * geo.kcodes_unit();
-    const float2* kp = reinterpret_cast<const float2*>(c.kparams + unit * geo.kparams_unit());
-    const bool packed_v = t0 < s.vq;
-    if (packed_v) {
+    // packed key tokens of the block and the key groups they lie in
+    const uint32_t nk = t0 < s.kq ? static_cast<uint32_t>(std::min<uint64_t>(kValueBlock, s.kq - t0)) : 0u;
+    const uint64_t g_lo = t0 / G;
+    if (nk > 0) {
+      const uint32_t* kc = c.kcodes + unit * geo.kcodes_unit() + t0 * kw;
+      for (uint32_t i = threadIdx.x; i < nk * kw; i += blockDim.x) skw[i] = kc[i];
+      const uint32_t ng = static_cast<uint32_t>((t0 + nk - 1) / G - g_lo + 1);
+      const float2* kp = reinterpret_cast<const float2*>(c.kparams + unit * geo.kparams_unit()) + g_lo * D;
+      for (uint32_t i = threadIdx.x; i < ng * D; i += blockDim.x) skp[i] = kp[i];
+    }
+    if (t0 < s.vq) {
       const uint32_t* vc = c.vcodes + unit * geo.vcodes_unit() + tb * D * vw;
-      for (uint32_t i = threadIdx.x; i < D * vw; i += blockDim.x) stage[(i % vw) * D + i / vw] = vc[i];
+      for (uint32_t i = threadIdx.x; i < D * vw; i += blockDim.x) svw[(i % vw) * L.vrow + i / vw] = vc[i];
       const float2* vp = reinterpret_cast<const float2*>(c.vparams + unit * geo.vparams_unit()) + tb * ncg * kValueBlock;
-      for (uint32_t i = threadIdx.x; i < ncg * kValueBlock; i += blockDim.x) sprm[i] = vp[i];
+      for (uint32_t i = threadIdx.x; i < ncg * kValueBlock; i += blockDim.x) svp[i] = vp[i];
     }
     __syncthreads();
     for (uint32_t r = threadIdx.x; r < ntok * q4; r += blockDim.x) {
       const uint32_t tt = r / q4, d0 = (r % q4) * 4;
       const uint64_t t = t0 + tt;
       float k[4], v[4];
-      if (t < s.kq) {
+      if (tt < nk) {
         // one code word holds the four channels (ppw >= 4); their (scale, zero) pairs are 32
         // contiguous bytes
-        const uint32_t word = kc[t * kw + d0 / ppw];
-        const float4* pp = reinterpret_cast<const float4*>(kp + (t / G) * D + d0);
+        const uint32_t word = skw[tt * kw + d0 / ppw];
+        const float4* pp = reinterpret_cast<const float4*>(skp + (t / G - g_lo) * D + d0);
         const float4 p01 = pp[0], p23 = pp[1];
         const float sc[4] = {p01.x, p01.z, p23.x, p23.z}, zr[4] = {p01.y, p01.w, p23.y, p23.w};
 #pragma unroll
@@ -899,8 +927,8 @@ __global__ void __launch_bounds__(kThreads)
       }
       if (t < s.vq) {
         const uint32_t sh = code_shift(bits, tt % ppw);
-        const float2 sz = sprm[(d0 / G) * kValueBlock + tt];  // one group holds the four (G % 4 == 0)
-        const uint4 w = *reinterpret_cast<const uint4*>(stage + (tt / ppw) * D + d0);
+        const float2 sz = svp[(d0 / G) * kValueBlock + tt];  // one group holds the four (G % 4 == 0)
+        const uint4 w = *reinterpret_cast<const uint4*>(svw + (tt / ppw) * L.vrow + d0);
         const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] = fmaf(static_cast<float>((ws[e] >> sh) & mask), sz.x, sz.y);
@@ -1474,7 +1502,7 @@ hipError_t launch_dequant_cache(const CacheView& c, const SeqState& s, float* ke
   const uint64_t seq = s.kq + s.kres;
   const uint64_t work = seq * (c.geo.D / 4);
   if (work == 0) return hipSuccess;
-  const size_t lds = ((size_t)c.geo.vwords_per_channel() * c.geo.D + 2 * c.geo.ncg() * kValueBlock) * sizeof(uint32_t);
+  const size_t lds = (size_t)dequant_lds(c.geo).total * sizeof(uint32_t);
   // unaligned outputs, and blocks whose staging would not fit the default 64 KB of LDS (wide
   // heads with small groups): one element per thread
   if (reinterpret_cast<uintptr_t>(keys) % 16 != 0 || reinterpret_cast<uintptr_t>(values) % 16 != 0 ||
