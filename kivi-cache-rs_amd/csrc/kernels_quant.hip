@@ -1511,7 +1511,7 @@ hipError_t launch_dequant_cache(const CacheView& c, const SeqState& s, float* ke
     return hipGetLastError();
   }
   const uint64_t blocks = (seq + kValueBlock - 1) / kValueBlock * c.geo.units;
-  k_dequant_cache<<<static_cast<unsigned>(std::min<uint64_t>(blocks, 8192)), kThreads, lds, stream>>>(
+  k_dequant_cache<<<static_cast<unsigned>(std::min<uint64_t>(blocks, 32768)), kThreads, lds, stream>>>(
       c, s, seq, keys, values);
   return hipGetLastError();
 }
