@@ -30,6 +30,8 @@
  *    that is not the cache's own stream (kivi_cache_set_stream), and a host-pointer call on
  *    a session for that of the latest `*_device` call on the session when it is not the
  *    default stream, so it never overlaps that work; that stream must still exist then too.
+ *    Likewise the host reads of a QuantizedTensor made by kivi_quantize_*_device wait for
+ *    the stream of that call first.
  *    Calls enqueued under stream capture are not counted. Between `*_device` calls on
  *    different streams the caller orders the work.
  *  - Threading follows the reference's borrow rules: at most one mutating call

@@ -747,6 +747,10 @@ struct kivi_quantized {
   size_t group_size = 0, batch = 0, heads = 0, tokens = 0, head_dim = 0;
   DevBuf codes, params;  // reference PackedStream order, concatenated over units
   size_t n_codes = 0, n_params = 0;
+  mutable DeviceCallOrder dev;  // the stream of a `*_device` quantize; host reads wait for it
+  kivi_quantized() = default;
+  kivi_quantized(const kivi_quantized&) = delete;
+  kivi_quantized& operator=(const kivi_quantized&) = delete;
 };
 
 namespace {
@@ -1996,8 +2000,10 @@ kivi_status kivi_quantize_per_channel_device(const float* data, size_t data_len,
                                              uint8_t bits, size_t group_size, void* stream,
                                              kivi_quantized** out, kivi_error* err) {
   return guarded(err, [&] {
-    return quantize(data, data_len, batch, heads, tokens, head_dim, bits, group_size, true, true,
-                    static_cast<hipStream_t>(stream), out);
+    KIVI_TRY(quantize(data, data_len, batch, heads, tokens, head_dim, bits, group_size, true, true,
+                      static_cast<hipStream_t>(stream), out));
+    (*out)->dev.note(static_cast<hipStream_t>(stream));
+    return Status{};
   });
 }
 
@@ -2006,8 +2012,10 @@ kivi_status kivi_quantize_per_token_device(const float* data, size_t data_len, s
                                            uint8_t bits, size_t group_size, void* stream,
                                            kivi_quantized** out, kivi_error* err) {
   return guarded(err, [&] {
-    return quantize(data, data_len, batch, heads, tokens, head_dim, bits, group_size, false, true,
-                    static_cast<hipStream_t>(stream), out);
+    KIVI_TRY(quantize(data, data_len, batch, heads, tokens, head_dim, bits, group_size, false, true,
+                      static_cast<hipStream_t>(stream), out));
+    (*out)->dev.note(static_cast<hipStream_t>(stream));
+    return Status{};
   });
 }
 
@@ -2027,19 +2035,29 @@ size_t kivi_quantized_metadata_bytes(const kivi_quantized* q) { return q->n_para
 
 kivi_status kivi_quantized_codes(const kivi_quantized* q, uint32_t* out, size_t out_len,
                                  kivi_error* err) {
-  return guarded(err, [&] { return quantized_read(q, out, out_len, q ? q->n_codes : 0, 0); });
+  return guarded(err, [&] {
+    if (q != nullptr) KIVI_TRY(q->dev.settle(nullptr));  // host reads use the default stream
+    return quantized_read(q, out, out_len, q ? q->n_codes : 0, 0);
+  });
 }
 kivi_status kivi_quantized_pytorch_codes(const kivi_quantized* q, uint32_t* out, size_t out_len,
                                          kivi_error* err) {
-  return guarded(err, [&] { return quantized_read(q, out, out_len, q ? q->n_codes : 0, 1); });
+  return guarded(err, [&] {
+    if (q != nullptr) KIVI_TRY(q->dev.settle(nullptr));  // host reads use the default stream
+    return quantized_read(q, out, out_len, q ? q->n_codes : 0, 1);
+  });
 }
 kivi_status kivi_quantized_scale_zero(const kivi_quantized* q, float* out, size_t out_len,
                                       kivi_error* err) {
-  return guarded(err, [&] { return quantized_read(q, out, out_len, q ? q->n_params : 0, 2); });
+  return guarded(err, [&] {
+    if (q != nullptr) KIVI_TRY(q->dev.settle(nullptr));  // host reads use the default stream
+    return quantized_read(q, out, out_len, q ? q->n_params : 0, 2);
+  });
 }
 kivi_status kivi_quantized_dequantize(const kivi_quantized* q, float* out, size_t out_len,
                                       kivi_error* err) {
   return guarded(err, [&] {
+    if (q != nullptr) KIVI_TRY(q->dev.settle(nullptr));  // host reads use the default stream
     const size_t n = q ? q->batch * q->heads * q->tokens * q->head_dim : 0;
     return quantized_read(q, out, out_len, n, 3);
   });

@@ -955,6 +955,17 @@ def quantize_per_token(backend, data, batch, heads, tokens, head_dim, bits, grou
                      group_size)
 
 
+def quantize_device(backend, per_channel, data_ptr, data_len, batch, heads, tokens, head_dim, bits,
+                    group_size, stream=0):
+    """``quantize_per_channel`` / ``quantize_per_token`` on device input, enqueued on ``stream``
+    (HIP library only)."""
+    h = C.c_void_p()
+    name = "quantize_per_channel_device" if per_channel else "quantize_per_token_device"
+    backend.call(name, C.c_void_p(data_ptr), data_len, batch, heads, tokens, head_dim, bits,
+                 group_size, C.c_void_p(stream), C.byref(h))
+    return QuantizedTensor(backend, h, (batch, heads, tokens, head_dim))
+
+
 # ------------------------------------------------------------------ seeded inputs
 
 

@@ -149,3 +149,29 @@ def test_host_call_after_device_append_on_another_stream(amd, oracle, bits, then
         hip.hipStreamSynchronize(s)
         hip.hipStreamDestroy(s)
         mem.free()
+
+
+@pytest.mark.parametrize("per_channel", [True, False])
+def test_quantized_host_reads_after_device_quantize_on_another_stream(amd, oracle, per_channel):
+    """quantize_per_channel / per_token on device input, enqueued on a non-blocking stream, then
+    the QuantizedTensor's host reads at once (src/quant.rs:24-151): they wait for the quantize."""
+    batch, heads, tokens, dim, bits, group = 4, 8, 8192, 128, 2, 32
+    rng = np.random.default_rng(650 + per_channel)
+    x = rng.standard_normal(batch * heads * tokens * dim).astype(np.float32)
+    q = kivi.quantize_per_channel if per_channel else kivi.quantize_per_token
+    want = q(oracle, x, batch, heads, tokens, dim, bits, group)
+    mem = DeviceArrays()
+    hip = mem._hip
+    s = non_blocking_stream(hip)
+    try:
+        dx = mem.upload(x)
+        got = kivi.quantize_device(amd, per_channel, dx, x.size, batch, heads, tokens, dim, bits, group, s.value)
+        assert np.array_equal(got.codes(), want.codes())
+        assert np.array_equal(got.scale_zero().view(np.uint32), want.scale_zero().view(np.uint32))
+        assert np.array_equal(got.pytorch_codes(), want.pytorch_codes())
+        assert np.array_equal(got.dequantize().view(np.uint32), want.dequantize().view(np.uint32))
+        del got
+    finally:
+        hip.hipStreamSynchronize(s)
+        hip.hipStreamDestroy(s)
+        mem.free()
