@@ -11,6 +11,7 @@
 #include "kivi.h"
 
 #include <algorithm>
+#include <mutex>
 
 namespace kivi {
 namespace {
@@ -1503,10 +1504,19 @@ hipError_t launch_dequant_cache(const CacheView& c, const SeqState& s, float* ke
   const uint64_t work = seq * (c.geo.D / 4);
   if (work == 0) return hipSuccess;
   const size_t lds = (size_t)dequant_lds(c.geo).total * sizeof(uint32_t);
-  // unaligned outputs, and blocks whose staging would not fit the default 64 KB of LDS (wide
-  // heads with small groups): one element per thread
-  if (reinterpret_cast<uintptr_t>(keys) % 16 != 0 || reinterpret_cast<uintptr_t>(values) % 16 != 0 ||
-      lds > 65536) {
+  // staging beyond the default 64 KB of LDS (wide heads) is asked for, up to 128 KB
+  bool fits = lds <= 65536;
+  if (!fits && lds <= 131072) {
+    static std::once_flag once;
+    static hipError_t configured = hipSuccess;
+    std::call_once(once, [] {
+      configured = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_dequant_cache),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, 131072);
+    });
+    fits = configured == hipSuccess;
+  }
+  // unaligned outputs, and blocks whose staging would not fit: one element per thread
+  if (reinterpret_cast<uintptr_t>(keys) % 16 != 0 || reinterpret_cast<uintptr_t>(values) % 16 != 0 || !fits) {
     k_dequant_cache_elem<<<grid_for(work * 4 * c.geo.units), kThreads, 0, stream>>>(c, s, seq, keys, values);
     return hipGetLastError();
   }
