@@ -226,6 +226,11 @@ hipError_t launch_export_values(const CacheView& c, uint64_t vq, uint32_t* codes
 hipError_t launch_dequant_cache(const CacheView& c, const SeqState& s, float* keys, float* values,
                                 hipStream_t stream);
 
+// Let `kernel` launch with `bytes` of dynamic LDS on the current device. The limit is an
+// attribute of the kernel on each device (64 KB unless raised); each (kernel, device) pair is
+// raised once to the largest size asked for so far, from any thread.
+hipError_t raise_lds_limit(const void* kernel, size_t bytes);
+
 // Copy `units` blocks of `bytes` from src (pitch src_pitch) to dst (pitch dst_pitch).
 hipError_t copy_units(void* dst, size_t dst_pitch, const void* src, size_t src_pitch, size_t bytes,
                       uint32_t units, hipStream_t stream);

@@ -3408,14 +3408,10 @@ hipError_t launch_shared(const AttnArgs& a, const SessionTable& t, const GroupBy
     if (e != hipSuccess) return e;
   }
   if (a.nsplit_fast == 0) return hipSuccess;
-  // the attribute is per kernel and per process: set once, under any number of threads
-  static std::once_flag once;
-  static hipError_t configured = hipSuccess;
-  std::call_once(once, [] {
-    configured = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_shared<BITS>),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kShLdsBytes));
-  });
-  if (configured != hipSuccess) return configured;
+  {
+    const hipError_t e = raise_lds_limit(reinterpret_cast<const void*>(&k_attn_shared<BITS>), kShLdsBytes);
+    if (e != hipSuccess) return e;
+  }
   const uint32_t rblocks = (a.nsess * a.gq + kShRows - 1) / kShRows;
   {
     TimedLaunch timed(KIVI_KERNEL_ATTN_SHARED, stream, by.prefix + by.queries);

@@ -11,7 +11,9 @@
 #include "kivi.h"
 
 #include <algorithm>
+#include <map>
 #include <mutex>
+#include <utility>
 
 namespace kivi {
 namespace {
@@ -1389,9 +1391,8 @@ hipError_t launch_quant_values(const CacheView& c, RowSource ring, uint32_t n_ri
   const uint32_t TB = std::max<uint32_t>(1, std::min<uint32_t>(kValueBlock, kStageFloats / (D + 1)));
   const size_t lds = ((size_t)kValueBlock * D + 15) / 16 * 16 + (size_t)TB * (D + 1) * sizeof(float);
   const bool vec4 = rows_vec4(ring, D) && (n_in == 0 || rows_vec4(in, D));
-  if (lds > 65536) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_quant_values),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+  {
+    const hipError_t e = raise_lds_limit(reinterpret_cast<const void*>(&k_quant_values), lds);
     if (e != hipSuccess) return e;
   }
   const double rows = (double)c.geo.units * n;
@@ -1435,14 +1436,11 @@ hipError_t launch_export_keys(const CacheView& c, uint64_t kq, uint32_t* codes, 
     const uint64_t slices = (kq / g.G + per - 1) / per;
     const size_t lds = (size_t)per * per_group * sizeof(uint32_t);
     const dim3 grid(static_cast<unsigned>(std::min<uint64_t>(slices, 1u << 30)), std::min(g.units, 65535u));
-    hipError_t e = hipSuccess;
-    if (lds > 65536) {
-      const void* f = g.bits == 2 ? reinterpret_cast<const void*>(&k_export_keys<2>)
-                      : g.bits == 4 ? reinterpret_cast<const void*>(&k_export_keys<4>)
-                                    : reinterpret_cast<const void*>(&k_export_keys<8>);
-      e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-      if (e != hipSuccess) return e;
-    }
+    const void* f = g.bits == 2 ? reinterpret_cast<const void*>(&k_export_keys<2>)
+                    : g.bits == 4 ? reinterpret_cast<const void*>(&k_export_keys<4>)
+                                  : reinterpret_cast<const void*>(&k_export_keys<8>);
+    hipError_t e = raise_lds_limit(f, lds);
+    if (e != hipSuccess) return e;
     if (g.bits == 2) k_export_keys<2><<<grid, kThreads, lds, stream>>>(c, kq, per, stage_out, codes);
     else if (g.bits == 4) k_export_keys<4><<<grid, kThreads, lds, stream>>>(c, kq, per, stage_out, codes);
     else k_export_keys<8><<<grid, kThreads, lds, stream>>>(c, kq, per, stage_out, codes);
@@ -1479,12 +1477,10 @@ hipError_t launch_export_values(const CacheView& c, uint64_t vq, uint32_t* codes
   const uint64_t slices = (nblk + per - 1) / per;
   const size_t lds = (size_t)per * per_block * sizeof(uint32_t);
   const dim3 grid(static_cast<unsigned>(std::min<uint64_t>(slices, 1u << 30)), std::min(g.units, 65535u));
-  hipError_t e = hipSuccess;
   const void* f = g.bits == 2 ? reinterpret_cast<const void*>(&k_export_values<2>)
                   : g.bits == 4 ? reinterpret_cast<const void*>(&k_export_values<4>)
                                 : reinterpret_cast<const void*>(&k_export_values<8>);
-  if (lds > 65536)
-    e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+  hipError_t e = raise_lds_limit(f, lds);
   if (e == hipSuccess) {
     if (g.bits == 2) k_export_values<2><<<grid, kThreads, lds, stream>>>(c, vq, per, stage_out, codes, params);
     else if (g.bits == 4) k_export_values<4><<<grid, kThreads, lds, stream>>>(c, vq, per, stage_out, codes, params);
@@ -1505,16 +1501,7 @@ hipError_t launch_dequant_cache(const CacheView& c, const SeqState& s, float* ke
   if (work == 0) return hipSuccess;
   const size_t lds = (size_t)dequant_lds(c.geo).total * sizeof(uint32_t);
   // staging beyond the default 64 KB of LDS (wide heads) is asked for, up to 128 KB
-  bool fits = lds <= 65536;
-  if (!fits && lds <= 131072) {
-    static std::once_flag once;
-    static hipError_t configured = hipSuccess;
-    std::call_once(once, [] {
-      configured = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_dequant_cache),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, 131072);
-    });
-    fits = configured == hipSuccess;
-  }
+  const bool fits = lds <= 131072 && raise_lds_limit(reinterpret_cast<const void*>(&k_dequant_cache), lds) == hipSuccess;
   // unaligned outputs, and blocks whose staging would not fit: one element per thread
   if (reinterpret_cast<uintptr_t>(keys) % 16 != 0 || reinterpret_cast<uintptr_t>(values) % 16 != 0 || !fits) {
     k_dequant_cache_elem<<<grid_for(work * 4 * c.geo.units), kThreads, 0, stream>>>(c, s, seq, keys, values);
@@ -1524,6 +1511,21 @@ hipError_t launch_dequant_cache(const CacheView& c, const SeqState& s, float* ke
   k_dequant_cache<<<static_cast<unsigned>(std::min<uint64_t>(blocks, 32768)), kThreads, lds, stream>>>(
       c, s, seq, keys, values);
   return hipGetLastError();
+}
+
+hipError_t raise_lds_limit(const void* kernel, size_t bytes) {
+  if (bytes <= 65536) return hipSuccess;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  static std::mutex mu;
+  static std::map<std::pair<const void*, int>, size_t> raised;
+  std::lock_guard<std::mutex> lock(mu);
+  size_t& have = raised[{kernel, dev}];
+  if (have >= bytes) return hipSuccess;
+  e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
+  if (e == hipSuccess) have = bytes;
+  return e;
 }
 
 hipError_t copy_units(void* dst, size_t dst_pitch, const void* src, size_t src_pitch, size_t bytes,
