@@ -1480,6 +1480,11 @@ __device__ __forceinline__ void wide_split(const AttnArgs& a, uint32_t unit, uin
                                            float* lds) {
   constexpr int CPW = wide_cpw(BITS), NH = kWideHeads, D = 128;
   constexpr int ROW = CPW * 64 + kRowPad;
+  // At 8 bits (two workgroups per CU) a wave raises its issue priority from the start of a
+  // chunk step until that step's next-chunk requests are out, so the requests of the SIMD's
+  // waves are not held behind the other waves' matrix and vector work (C3 at 8 bits: 68.6 ->
+  // 65.0 us). At three workgroups per CU (2 and 4 bits) the same raise cost 40%.
+  constexpr bool kRaise = BITS == 8;
   constexpr int kExp = CodeUnit<BITS>::kExp;
   constexpr float kUnit = kExp == 0 ? 1.0f : kExp == -1 ? 0.5f : 0.001953125f;
   const uint32_t b = unit / a.heads, kvh = unit % a.heads;
@@ -1546,12 +1551,14 @@ __device__ __forceinline__ void wide_split(const AttnArgs& a, uint32_t unit, uin
   float mx = -INFINITY;
   {
     auto step = [&](int k, const WideKeyWords<BITS>& cur, WideKeyWords<BITS>& next) {
+      if constexpr (kRaise) __builtin_amdgcn_s_setprio(1);
       // this chunk's (scale, zero) pairs to LDS (after the previous chunk's reads of them),
       // then the next chunk's requested (the last step re-reads an L2-resident chunk)
       wide_stage(wl, ROW, k, lane, kp0, kp1);
       const int32_t kn = chunk_of(std::min(k + 1, nch - 1));
       wide_load_key_params(a, unit, kn, lane, kp0, kp1);
       wide_load_keys<BITS>(a, unit, kn, g, n, next);
+      if constexpr (kRaise) __builtin_amdgcn_s_setprio(0);
       v4f acc[4];
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) acc[mt] = v4f{0.f, 0.f, 0.f, 0.f};
@@ -1633,6 +1640,7 @@ __device__ __forceinline__ void wide_split(const AttnArgs& a, uint32_t unit, uin
       wide_load_values<BITS>(a, unit, chunk_of(0), g, n, vw0);
     }
     auto step = [&](int k, WideValueWords<BITS>& cur, WideValueWords<BITS>& next) {
+      if constexpr (kRaise) __builtin_amdgcn_s_setprio(1);
       // weights (times 2^ev) of head hq, tokens 16g .. 16g+15, read from the slot before the
       // chunk's (scale, zero) pairs are staged over it
       float4 lg[4];
@@ -1649,6 +1657,7 @@ __device__ __forceinline__ void wide_split(const AttnArgs& a, uint32_t unit, uin
       const int32_t kn = chunk_of(std::min(k + 1, nch - 1));
       wide_load_value_params(a, unit, kn, lane, vp0, vp1);
       wide_load_values<BITS>(a, unit, kn, g, n, next);
+      if constexpr (kRaise) __builtin_amdgcn_s_setprio(0);
       float w[16];
       {
 #pragma unroll
@@ -1783,6 +1792,11 @@ __device__ __forceinline__ void wide16_split(const AttnArgs& a, uint32_t unit, u
                                              float* lds) {
   constexpr int CPW = kWide16Cpw, NH = kWide16Heads, D = 128;
   constexpr int ROW = CPW * 64 + kRowPad;
+  // At 2 bits a wave raises its issue priority from the start of a chunk step until that
+  // step's next-chunk requests are out, as the eight-head kernel does at 8 bits (GQA 16 at
+  // batch 4: 35.3 -> 33.7 us; 128 q / 8 KV heads at batch 16: 198.5 -> 194.0 us). At 4 bits
+  // it made no difference and at 8 bits it cost 25%.
+  constexpr bool kRaise = BITS == 2;
   constexpr int kExp = CodeUnit<BITS>::kExp;
   constexpr float kUnit = kExp == 0 ? 1.0f : kExp == -1 ? 0.5f : 0.001953125f;
   const uint32_t b = unit / a.heads, kvh = unit % a.heads;
@@ -1834,10 +1848,12 @@ __device__ __forceinline__ void wide16_split(const AttnArgs& a, uint32_t unit, u
   float mx = -INFINITY;
   {
     auto step = [&](int k, const WideKeyWords<BITS>& cur, WideKeyWords<BITS>& next) {
+      if constexpr (kRaise) __builtin_amdgcn_s_setprio(1);
       wide_stage(wl, ROW, k, lane, kp0, kp1);
       const int32_t kn = chunk_of(std::min(k + 1, nch - 1));
       wide_load_key_params(a, unit, kn, lane, kp0, kp1);
       wide_load_keys<BITS>(a, unit, kn, g, n, next);
+      if constexpr (kRaise) __builtin_amdgcn_s_setprio(0);
       v4f acc[4];
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) acc[mt] = v4f{0.f, 0.f, 0.f, 0.f};
@@ -1916,6 +1932,7 @@ __device__ __forceinline__ void wide16_split(const AttnArgs& a, uint32_t unit, u
       wide_load_values<BITS>(a, unit, chunk_of(0), g, n, vw0);
     }
     auto step = [&](int k, const WideValueWords<BITS>& cur, WideValueWords<BITS>& next) {
+      if constexpr (kRaise) __builtin_amdgcn_s_setprio(1);
       // weights (times 2^ev) of head n, tokens 16g .. 16g+15, read from the slot before the
       // chunk's (scale, zero) pairs are staged over it
       float4 lg[4];
@@ -1928,6 +1945,7 @@ __device__ __forceinline__ void wide16_split(const AttnArgs& a, uint32_t unit, u
       const int32_t kn = chunk_of(std::min(k + 1, nch - 1));
       wide_load_value_params(a, unit, kn, lane, vp0, vp1);
       wide_load_values<BITS>(a, unit, kn, g, n, next);
+      if constexpr (kRaise) __builtin_amdgcn_s_setprio(0);
       float w[16];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
